@@ -1,0 +1,142 @@
+/* tritonkv_amd -- C ABI of the MI355X (gfx950) quantized-KV decode-attention kernels.
+ *
+ * Every entry point is extern "C", takes plain device pointers and sizes,
+ * enqueues work on the given hipStream_t, never allocates and never
+ * synchronises (so a caller may capture it in a HIP graph), and returns
+ *     0            success
+ *     < 0          TKV_E* argument error (nothing was launched)
+ *     > 0          the hipError_t of a failed launch
+ *
+ * Data layout is the reference's contract (quantize.py:40-54, :73-146):
+ *   packed  uint8  (B, HKV, S, D/P)    P = 8/nbits codes per byte, split-P:
+ *                                      bits [p*nbits,(p+1)*nbits) of byte j hold dim j + p*D/P
+ *   scale   fp16   (B, HKV, S, D/gs)
+ *   zero    fp16   (B, HKV, S, D/gs)
+ *   q       fp16 or fp32 (B, HQ, D);  out fp32 (B, HQ, D)
+ *   partials acc fp32 (B, HQ, num_splits, D), maxs/sums fp32 (B, HQ, num_splits)
+ * All tensors are contiguous row-major.  fp16 values are passed as uint16_t
+ * bit patterns.
+ */
+#ifndef TKV_H_
+#define TKV_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t *tkv_stream_t; /* == hipStream_t */
+
+enum {
+  TKV_OK = 0,
+  TKV_EINVAL = -1,       /* inconsistent or out-of-range argument */
+  TKV_EUNSUPPORTED = -2, /* valid but not compiled: D, nbits, group size combination */
+  TKV_ENODEVICE = -3     /* no HIP device visible */
+};
+
+/* Arguments of one decode step.  For the quantized path k/v are the packed
+ * codes and k_scale/k_zero/v_scale/v_zero the fp16 metadata; for the fp16
+ * control path k/v are fp16 (B, HKV, S, D) and the metadata pointers are unused.
+ *
+ * S is the token capacity of each (b, kv-head) block.  If seq_lens is NULL every
+ * row attends to all S tokens; otherwise row b attends to its first seq_lens[b]
+ * tokens (1 <= seq_lens[b] <= S) -- an extension the reference does not have
+ * (it uses one S for the whole batch, kernels/fused_decode_attn.py:469).
+ *
+ * The history [0, S) is cut into num_splits ranges of split_size tokens
+ * (the last one ragged).  If num_splits == 1 the kernel writes out directly and
+ * acc/maxs/sums may be NULL; otherwise it writes the partials and a combine
+ * pass writes out. */
+typedef struct tkv_decode_args {
+  const void *q;
+  int32_t q_is_fp32;
+  const void *k, *k_scale, *k_zero;
+  const void *v, *v_scale, *v_zero;
+  const int32_t *seq_lens;
+  float *acc, *maxs, *sums;
+  float *out;
+  int32_t B, HQ, HKV, S, D;
+  int32_t k_nbits, v_nbits; /* 2 or 4 (K and V may differ); ignored by the fp16 path */
+  int32_t group_size;       /* 16, 32, 64 or 128, <= D; ignored by the fp16 path */
+  float sm_scale;
+  int32_t split_size, num_splits;
+} tkv_decode_args;
+
+/* Fused 2/4-bit split-P decode attention: the split kernel, then (if
+ * num_splits > 1) the log-sum-exp combine.
+ * Replaces the two Triton launches of kernels/fused_decode_attn.py:525-568
+ * (_fused_decode_attn_split :155-353 and _combine_splits :355-395). */
+int tkv_fused_decode_attention(const tkv_decode_args *args, tkv_stream_t stream);
+
+/* fp16 control: identical split, softmax and combine; K/V read as fp16.
+ * Replaces kernels/fp16_decode_attn.py:207-239 (_fp16_decode_attn_split :47-135). */
+int tkv_fp16_decode_attention(const tkv_decode_args *args, tkv_stream_t stream);
+
+/* The split kernels alone (no combine): with num_splits == 1 they write out,
+ * otherwise only the partials acc/maxs/sums.  Replace the single launches
+ * kernels/fused_decode_attn.py:525-556 and kernels/fp16_decode_attn.py:207-227;
+ * used to time the split kernel by itself. */
+int tkv_fused_decode_split(const tkv_decode_args *args, tkv_stream_t stream);
+int tkv_fp16_decode_split(const tkv_decode_args *args, tkv_stream_t stream);
+
+/* Log-sum-exp merge of split partials into out, as _combine_splits
+ * (kernels/fused_decode_attn.py:355-395, launched at :558-568). */
+int tkv_combine_splits(const float *acc, const float *maxs, const float *sums, float *out,
+                       int32_t B, int32_t HQ, int32_t num_splits, int32_t D,
+                       tkv_stream_t stream);
+
+/* Group-wise asymmetric quantize + split-P pack of N new tokens per
+ * (b, kv-head), written into a cache at token positions.
+ *   x: (B, HKV, N, D) fp16 (x_is_fp32 == 0) or fp32
+ *   positions: NULL (write tokens [0, N)) or B int32 start positions; the
+ *              tokens of batch row b land at [positions[b], positions[b] + N)
+ *   packed/scale/zero: caches of capacity S_cap tokens per (b, kv-head)
+ * Bit-exact with quantize_groupwise + pack_codes (quantize.py:186-236,
+ * :149-169); used for one-token decode appends and for whole-cache setup. */
+int tkv_quantize_pack(const void *x, int32_t x_is_fp32, int32_t B, int32_t HKV, int32_t N,
+                      int32_t D, int32_t nbits, int32_t group_size, const int32_t *positions,
+                      int32_t S_cap, uint8_t *packed, uint16_t *scale, uint16_t *zero,
+                      tkv_stream_t stream);
+
+/* Split-P pack of uint8 codes (rows, D) -> (rows, D/P), as pack_codes
+ * (quantize.py:149-169). */
+int tkv_pack_codes(const uint8_t *codes, int64_t rows, int32_t D, int32_t nbits,
+                   uint8_t *packed, tkv_stream_t stream);
+
+/* Unpack + fp32 dequantize rows of a quantized cache, through the same
+ * register unpack the decode kernel uses (path 0: the K-operand extraction,
+ * path 1: the transposed V-operand extraction).  codes_out (rows, D) uint8
+ * and/or values_out (rows, D) fp32 = code * scale + zero; either may be NULL.
+ * As unpack_codes / dequantize_groupwise (quantize.py:172-183, :239-246). */
+int tkv_unpack_dequant(const uint8_t *packed, const uint16_t *scale, const uint16_t *zero,
+                       int64_t rows, int32_t D, int32_t nbits, int32_t group_size,
+                       int32_t path, uint8_t *codes_out, float *values_out,
+                       tkv_stream_t stream);
+
+typedef struct tkv_device_info_t {
+  int32_t device;
+  int32_t compute_units;
+  int32_t warp_size;
+  int32_t l2_bytes;
+  int64_t global_mem_bytes;
+  int32_t clock_khz;
+  int32_t mem_clock_khz;
+  int32_t mem_bus_bits;
+  char gcn_arch[64];
+} tkv_device_info_t;
+
+/* Properties of the current device (the one the calling thread has selected). */
+int tkv_device_info(tkv_device_info_t *info);
+
+/* Human-readable text for a status code returned by any tkv_ function. */
+const char *tkv_status_string(int status);
+
+/* ABI version of this library (bumped on any incompatible change). */
+int tkv_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TKV_H_ */

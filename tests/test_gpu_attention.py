@@ -1,0 +1,309 @@
+"""GPU parity of the fused decode-attention and fp16 control kernels.
+
+Ports every kernel assertion of the reference's ``test_correctness.py:163-343``
+to the HIP kernels, with the oracle's fp32 dequantise-then-attend as the
+reference, and adds the north-star tolerance (2e-3 max-abs, 1e-3 mean-abs)
+to every comparison.  Beyond the reference: the fp16 control kernel, mixed
+K/V bit widths, per-row context lengths, q in fp32, head_dim 64, GQA groups
+larger than 16, HIP-graph replay, and the large benchmark shapes checked on a
+sample of (batch row, kv head) units.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oatt
+from oracle import inputs as oinp
+from oracle import quant as oq
+from tests.helpers import (
+    KERNEL_COSINE_MIN,
+    KERNEL_REL_L2_MAX,
+    KERNEL_VS_BASELINE_ERR_RATIO_MAX,
+    assert_close_to_reference,
+    fp16_baseline_rows,
+    make_case,
+    metrics,
+    oracle_attention_on_quant,
+    qt_to_np,
+)
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+SHAPES = [
+    # (B, HQ, HKV, D) -- Qwen2.5-1.5B attention shape, plus GQA edge cases
+    (1, 12, 2, 128),
+    (1, 8, 8, 64),  # no GQA sharing (MHA)
+    (2, 32, 8, 64),  # Llama-3.2-1B shape, batch 2
+]
+SEQ_LENS = [1, 17, 128, 512, 2048, 8192, 16384]
+
+
+def _fused(q, kq, vq, **kw):
+    from tritonkv_amd.kernels import fused_decode_attention
+
+    return fused_decode_attention(q, kq, vq, **kw)
+
+
+def _case_and_check(B, HQ, HKV, D, S, nbits, gs, seed, **kw):
+    print(f"case B={B} HQ={HQ} HKV={HKV} D={D} S={S} nbits={nbits} gs={gs} seed={seed} {kw}",
+          flush=True)
+    q, k, v, kq, vq = make_case(B, HQ, HKV, D, S, nbits, gs, seed)
+    got = _fused(q, kq, vq, **kw)
+    torch.cuda.synchronize()
+    ref = oracle_attention_on_quant(q, kq, vq)
+    return assert_close_to_reference(got, ref, f"S={S} nbits={nbits} gs={gs} seed={seed} {kw}")
+
+
+@pytest.mark.parametrize("S", SEQ_LENS)
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_kernel_matches_dequant_reference_4bit(S, seed):
+    _case_and_check(1, 12, 2, 128, S, 4, 32, seed)
+
+
+@pytest.mark.parametrize("S", [512, 2048, 8192, 16384])
+@pytest.mark.parametrize("seed", [0, 1])
+def test_kernel_matches_dequant_reference_2bit(S, seed):
+    _case_and_check(1, 12, 2, 128, S, 2, 32, seed)
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("nbits", [2, 4])
+def test_kernel_shapes_and_gqa(shape, nbits):
+    B, HQ, HKV, D = shape
+    _case_and_check(B, HQ, HKV, D, 1024, nbits, 32, 3)
+
+
+@pytest.mark.parametrize("group_size", [16, 32, 64, 128])
+@pytest.mark.parametrize("nbits", [2, 4])
+def test_kernel_group_sizes(group_size, nbits):
+    _case_and_check(1, 12, 2, 128, 2048, nbits, group_size, 4)
+
+
+@pytest.mark.parametrize("D", [64])
+@pytest.mark.parametrize("group_size", [16, 32, 64])
+@pytest.mark.parametrize("nbits", [2, 4])
+def test_kernel_head_dim_64_group_sizes(D, group_size, nbits):
+    _case_and_check(2, 8, 2, D, 777, nbits, group_size, 12)
+
+
+def test_kernel_is_not_the_source_of_error():
+    """Kernel error vs the fp16 truth must stay within 1.5x the fp16 dequant baseline's."""
+    for S in (512, 2048, 8192, 16384):
+        q, k, v, kq, vq = make_case(1, 12, 2, 128, S, 4, 32, 5)
+        got = _fused(q, kq, vq)
+        qn, kn, vn = q.float().cpu().numpy(), k.float().cpu().numpy(), v.float().cpu().numpy()
+        truth = oatt.reference_decode_attention(qn, kn, vn)
+        # reference.py:288-304: fp16 dequant (c*s, +z each rounded to fp16), then attention.
+        kb = fp16_baseline_rows(qt_to_np(kq)).astype(np.float32)
+        vb = fp16_baseline_rows(qt_to_np(vq)).astype(np.float32)
+        base = oatt.reference_decode_attention(qn.astype(np.float16).astype(np.float32), kb, vb)
+        e_kernel = metrics(got, truth)["rel_l2"]
+        e_base = metrics(base, truth)["rel_l2"]
+        assert e_kernel <= KERNEL_VS_BASELINE_ERR_RATIO_MAX * e_base, (S, e_kernel, e_base)
+
+
+@pytest.mark.parametrize("num_splits", [1, 2, 5, 17, 64])
+def test_split_count_does_not_change_the_answer(num_splits):
+    _case_and_check(1, 12, 2, 128, 4096, 4, 32, 6, num_splits=num_splits)
+
+
+@pytest.mark.parametrize("block_n", [16, 32, 64, 128])
+def test_block_sizes(block_n):
+    _case_and_check(1, 12, 2, 128, 3000, 4, 32, 7, block_n=block_n)
+
+
+def test_output_is_finite_with_extreme_scores():
+    q, k, v, kq, vq = make_case(1, 12, 2, 128, 2048, 4, 32, 8)
+    q = q * 50.0
+    got = _fused(q, kq, vq)
+    assert torch.isfinite(got).all()
+    ref = oracle_attention_on_quant(q, kq, vq)
+    assert metrics(got, ref)["cosine"] >= KERNEL_COSINE_MIN
+
+
+def test_single_token_cache():
+    """S=1: attention output must be exactly the single dequantized V row."""
+    q, k, v, kq, vq = make_case(1, 12, 2, 128, 1, 4, 32, 9)
+    got = _fused(q, kq, vq).cpu().numpy()
+    v_deq = oq.dequantize_groupwise(qt_to_np(vq))  # (1, HKV, 1, D)
+    expect = np.repeat(v_deq[:, :, 0, :], 6, axis=1)
+    assert metrics(got, expect)["rel_l2"] < 1e-3
+    assert np.abs(got - expect).max() <= 2e-3
+
+
+def test_per_element_worst_case_not_hidden_by_aggregate():
+    q, k, v, kq, vq = make_case(1, 12, 2, 128, 8192, 4, 32, 10)
+    got = _fused(q, kq, vq).cpu().numpy()
+    ref = oracle_attention_on_quant(q, kq, vq)
+    worst = np.abs(got - ref).max() / max(np.abs(ref).mean(), 1e-6)
+    assert worst < 0.05
+
+
+@pytest.mark.parametrize("S", [1, 17, 512, 2048, 8192])
+@pytest.mark.parametrize("nbits", [2, 4])
+@pytest.mark.parametrize("group_size", [16, 32, 64, 128])
+def test_metadata_broadcast_and_fp16_dequant_flags_are_bitwise_identical(S, nbits, group_size):
+    """meta_bcast / dequant_fp16 / fold_zp select Triton variants; here they must not change a bit."""
+    q, k, v, kq, vq = make_case(1, 12, 2, 128, S, nbits, group_size, 11)
+    base = _fused(q, kq, vq)
+    for kw in (dict(meta_bcast=False), dict(dequant_fp16=True), dict(fold_zp=True),
+               dict(num_warps=8, num_stages=3)):
+        assert torch.equal(base, _fused(q, kq, vq, **kw)), kw
+
+
+def test_deterministic_across_calls_and_workspace_reuse():
+    q, k, v, kq, vq = make_case(1, 12, 2, 128, 5000, 4, 32, 13)
+    ws = {}
+    out = torch.empty(1, 12, 128, device=DEV)
+    a = _fused(q, kq, vq, out=out, _workspace=ws).clone()
+    acc_ptr = ws["acc"].data_ptr()
+    b = _fused(q, kq, vq, out=out, _workspace=ws)
+    assert torch.equal(a, b) and ws["acc"].data_ptr() == acc_ptr and b.data_ptr() == out.data_ptr()
+
+
+def test_q_in_fp32_is_rounded_like_fp16():
+    q, k, v, kq, vq = make_case(1, 12, 2, 128, 2048, 4, 32, 14)
+    assert torch.equal(_fused(q.float(), kq, vq), _fused(q, kq, vq))
+
+
+def test_gqa_group_larger_than_16():
+    # 32 query heads per kv head: two 16-head blocks per workgroup column.
+    _case_and_check(1, 64, 2, 128, 1500, 4, 32, 15)
+
+
+@pytest.mark.parametrize("kbits,vbits", [(4, 2), (2, 4)])
+def test_mixed_bit_widths(kbits, vbits):
+    from tritonkv_amd.quantize import quantize_groupwise
+
+    q, k, v = oinp.make_random_kv(2, 16, 2, 3000, 128, seed=16)
+    q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
+    kq, vq = quantize_groupwise(k, kbits, 32), quantize_groupwise(v, vbits, 32)
+    with pytest.raises(ValueError):
+        _fused(q, kq, vq)
+    got = _fused(q, kq, vq, allow_mixed_bits=True)
+    assert_close_to_reference(got, oracle_attention_on_quant(q, kq, vq), f"K{kbits}/V{vbits}")
+
+
+def test_ragged_sequence_lengths():
+    from tritonkv_amd.quantize import quantize_groupwise
+
+    B, HQ, HKV, S, D = 4, 16, 2, 5000, 128
+    q, k, v = oinp.make_random_kv(B, HQ, HKV, S, D, seed=17)
+    q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
+    kq, vq = quantize_groupwise(k, 4, 32), quantize_groupwise(v, 2, 32)
+    lens = torch.tensor([5000, 1, 777, 4097], dtype=torch.int32)
+    for ns in (None, 1, 13):
+        got = _fused(q, kq, vq, seq_lens=lens.to(DEV), allow_mixed_bits=True, num_splits=ns)
+        ref = oracle_attention_on_quant(q, kq, vq, seq_lens=lens.numpy())
+        assert_close_to_reference(got, ref, f"ragged ns={ns}")
+
+
+@pytest.mark.parametrize("S", [1, 17, 1000, 8192, 16384])
+@pytest.mark.parametrize("shape", [(1, 12, 2, 128), (2, 32, 8, 64)])
+def test_fp16_control_matches_fp32_reference(S, shape):
+    from tritonkv_amd.kernels import fp16_decode_attention
+
+    B, HQ, HKV, D = shape
+    q, k, v = oinp.make_random_kv(B, HQ, HKV, S, D, seed=18)
+    got = fp16_decode_attention(q.to(DEV), k.to(DEV), v.to(DEV))
+    ref = oatt.reference_decode_attention(q.float().numpy(), k.float().numpy(), v.float().numpy())
+    assert_close_to_reference(got, ref, f"fp16 control S={S} {shape}")
+
+
+@pytest.mark.parametrize("num_splits", [1, 3, 64])
+def test_fp16_control_split_invariance(num_splits):
+    from tritonkv_amd.kernels import fp16_decode_attention
+
+    q, k, v = oinp.make_random_kv(1, 12, 2, 4096, 128, seed=19)
+    got = fp16_decode_attention(q.to(DEV), k.to(DEV), v.to(DEV), num_splits=num_splits)
+    ref = oatt.reference_decode_attention(q.float().numpy(), k.float().numpy(), v.float().numpy())
+    assert_close_to_reference(got, ref, f"fp16 control ns={num_splits}")
+
+
+def test_graph_replay_matches_eager():
+    """Captured decode steps (fused + control) replayed with eager work in between."""
+    from tritonkv_amd.kernels import fp16_decode_attention
+
+    q, k, v, kq, vq = make_case(1, 12, 2, 128, 8192, 4, 32, 20)
+    out_f = torch.empty(1, 12, 128, device=DEV)
+    out_c = torch.empty(1, 12, 128, device=DEV)
+    ws_f, ws_c = {}, {}
+    want_f = _fused(q, kq, vq, out=out_f, _workspace=ws_f).clone()
+    want_c = fp16_decode_attention(q, k, v, out=out_c, _workspace=ws_c).clone()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        _fused(q, kq, vq, out=out_f, _workspace=ws_f)
+        fp16_decode_attention(q, k, v, out=out_c, _workspace=ws_c)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        _fused(q, kq, vq, out=out_f, _workspace=ws_f)
+        fp16_decode_attention(q, k, v, out=out_c, _workspace=ws_c)
+    for i in range(4):
+        out_f.zero_(), out_c.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_f, want_f), i
+        assert torch.equal(out_c, want_c), i
+        _ = (q.float() * 2).sum().item()  # eager work between replays
+
+
+def test_llama3_8b_shape_on_sampled_units():
+    """Config L (B=32, HQ=32, HKV=8, S=32768), checked on 3 of the 256 (b, kv) units."""
+    B, HQ, HKV, S, D = 32, 32, 8, 32768, 128
+    gen = torch.Generator(device=DEV).manual_seed(21)
+    k = torch.randn(B, HKV, S, D, device=DEV, generator=gen).half()
+    v = torch.randn(B, HKV, S, D, device=DEV, generator=gen).half()
+    q = torch.randn(B, HQ, D, device=DEV, generator=gen).half()
+    from tritonkv_amd.quantize import quantize_kv
+
+    for nbits, gs in ((4, 32), (2, 128)):
+        kq, vq = quantize_kv(k, v, nbits, gs)
+        got = _fused(q, kq, vq).cpu().numpy()
+        for b, h in ((0, 0), (17, 5), (31, 7)):
+            def unit(qt):
+                return oq.QuantNP(*(t[b:b + 1, h:h + 1].cpu().numpy()
+                                    for t in (qt.packed, qt.scale, qt.zero)), nbits, gs, D)
+            qn = q[b:b + 1, 4 * h:4 * h + 4].float().cpu().numpy()
+            ref = oatt.reference_decode_attention(qn, oq.dequantize_groupwise(unit(kq)),
+                                                  oq.dequantize_groupwise(unit(vq)))
+            assert_close_to_reference(got[b:b + 1, 4 * h:4 * h + 4], ref,
+                                      f"llama nbits={nbits} gs={gs} b={b} h={h}")
+
+
+def test_split_partials_combine_through_the_c_abi():
+    """tkv_fused_decode_split + tkv_combine_splits == tkv_fused_decode_attention."""
+    from tritonkv_amd import _lib
+    from tritonkv_amd.kernels import plan_splits
+
+    q, k, v, kq, vq = make_case(2, 12, 2, 128, 3333, 4, 32, 22)
+    _, ns, size = plan_splits(3333, 64, 9, 2, 2, 6)
+    acc = torch.empty(2, 12, ns, 128, device=DEV)
+    mx = torch.empty(2, 12, ns, device=DEV)
+    sm = torch.empty(2, 12, ns, device=DEV)
+    out = torch.empty(2, 12, 128, device=DEV)
+    a = _lib.DecodeArgs(q=q.data_ptr(), k=kq.packed.data_ptr(), k_scale=kq.scale.data_ptr(),
+                        k_zero=kq.zero.data_ptr(), v=vq.packed.data_ptr(),
+                        v_scale=vq.scale.data_ptr(), v_zero=vq.zero.data_ptr(),
+                        acc=acc.data_ptr(), maxs=mx.data_ptr(), sums=sm.data_ptr(),
+                        out=out.data_ptr(), B=2, HQ=12, HKV=2, S=3333, D=128, k_nbits=4,
+                        v_nbits=4, group_size=32, sm_scale=128 ** -0.5, split_size=size,
+                        num_splits=ns)
+    L = _lib.load()
+    st = _lib.stream_handle(q.device)
+    _lib.check(L.tkv_fused_decode_split(a, st), "split")
+    _lib.check(L.tkv_combine_splits(acc.data_ptr(), mx.data_ptr(), sm.data_ptr(), out.data_ptr(),
+                                    2, 12, ns, 128, st), "combine")
+    want = _fused(q, kq, vq, num_splits=9)
+    assert torch.equal(out, want)
+    # The partials themselves: each split's acc/sum is the split-local softmax numerator/denominator.
+    m = mx.cpu().numpy()
+    assert np.isfinite(m).all() and (sm.cpu().numpy() > 0).all()

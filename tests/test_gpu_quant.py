@@ -1,0 +1,149 @@
+"""GPU parity of the quantize / pack / unpack / dequant kernels -- bit-exact.
+
+Compared with the oracle (itself pinned by ``tests/test_oracle.py``) and with
+the golden vectors written from the reference's ``quantize_groupwise``.  The
+unpack/dequant export runs through both register unpack paths of the decode
+kernel (K operand, transposed V operand), so these tests also prove that the
+decode kernel sees exactly the reference's codes and ``code*scale + zero``.
+"""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import inputs as oinp
+from oracle import quant as oq
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "quantize_golden.npz")
+DEV = "cuda"
+
+
+def _bits16(t):
+    return t.detach().cpu().numpy().view(np.uint16)
+
+
+def _golden_names():
+    return [str(n) for n in np.load(GOLDEN)["names"]]
+
+
+@pytest.mark.parametrize("name", _golden_names())
+def test_gpu_quantize_matches_reference_golden(name):
+    from tritonkv_amd.quantize import dequantize_groupwise, quantize_groupwise
+
+    z = np.load(GOLDEN)
+    x = torch.from_numpy(z[f"{name}__x"]).to(DEV)
+    nbits, gs = (int(v) for v in z[f"{name}__meta"])
+    print(f"golden case {name} nbits={nbits} gs={gs} dtype={x.dtype}", flush=True)
+    qt = quantize_groupwise(x, nbits, gs)
+    assert np.array_equal(qt.packed.cpu().numpy(), z[f"{name}__packed"])
+    assert np.array_equal(_bits16(qt.scale), z[f"{name}__scale"].view(np.uint16))
+    assert np.array_equal(_bits16(qt.zero), z[f"{name}__zero"].view(np.uint16))
+    deq = dequantize_groupwise(qt).cpu().numpy()
+    assert np.array_equal(deq.view(np.uint32), z[f"{name}__deq"].view(np.uint32))
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("nbits", [2, 4])
+@pytest.mark.parametrize("gs", [16, 32, 64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_gpu_quantize_matches_oracle_bitwise(D, nbits, gs, dtype):
+    if gs > D:
+        pytest.skip("group larger than head_dim")
+    from tritonkv_amd.quantize import quantize_groupwise
+
+    print(f"quantize D={D} nbits={nbits} gs={gs} {dtype}", flush=True)
+    _, k, _ = oinp.make_random_kv(2, 4, 2, 257, D, seed=D + nbits + gs, dtype=dtype)
+    qt = quantize_groupwise(k.to(DEV), nbits, gs)
+    ref = oq.quantize_groupwise(k.numpy(), nbits, gs)
+    assert np.array_equal(qt.packed.cpu().numpy(), ref.packed)
+    assert np.array_equal(_bits16(qt.scale), ref.scale.view(np.uint16))
+    assert np.array_equal(_bits16(qt.zero), ref.zero.view(np.uint16))
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("nbits", [2, 4])
+@pytest.mark.parametrize("gs", [16, 32, 64, 128])
+@pytest.mark.parametrize("path", [0, 1])
+def test_decode_unpack_paths_are_bit_exact(D, nbits, gs, path):
+    """Codes and fp32 dequant through the decode kernel's own register unpack."""
+    if gs > D:
+        pytest.skip("group larger than head_dim")
+    from tritonkv_amd.quantize import quantize_groupwise, unpack_dequant_path
+
+    print(f"unpack path={path} D={D} nbits={nbits} gs={gs}", flush=True)
+    # 77 rows: not a multiple of the 16/32-row unpack tiles, so the tail is exercised.
+    _, k, _ = oinp.make_random_kv(1, 1, 1, 77, D, seed=31 * D + nbits + gs)
+    qt = quantize_groupwise(k.to(DEV), nbits, gs)
+    codes, vals = unpack_dequant_path(qt, path)
+    ref = oq.QuantNP(qt.packed.cpu().numpy(), qt.scale.cpu().numpy(), qt.zero.cpu().numpy(),
+                     nbits, gs, D)
+    assert np.array_equal(codes.cpu().numpy(), oq.unpack_codes(ref.packed, nbits, D))
+    assert np.array_equal(vals.cpu().numpy().view(np.uint32),
+                          oq.dequantize_groupwise(ref).view(np.uint32))
+
+
+@pytest.mark.parametrize("nbits", [2, 4])
+@pytest.mark.parametrize("D", [64, 128])
+def test_gpu_pack_unpack_roundtrip(nbits, D):
+    from tritonkv_amd.quantize import pack_codes, unpack_codes
+
+    g = torch.Generator().manual_seed(0)
+    codes = torch.randint(0, 2 ** nbits, (3, 5, D), generator=g, dtype=torch.uint8)
+    packed = pack_codes(codes.to(DEV), nbits)
+    assert np.array_equal(packed.cpu().numpy(), oq.pack_codes(codes.numpy(), nbits))
+    assert torch.equal(unpack_codes(packed, nbits, D).cpu(), codes)
+
+
+@pytest.mark.parametrize("nbits", [2, 4])
+def test_append_matches_whole_cache_quantization(nbits):
+    """Token-by-token append at ragged per-row positions == quantizing the whole cache."""
+    from tritonkv_amd.quantize import append_kv, empty_cache, quantize_groupwise
+
+    B, HKV, S, D, gs = 3, 2, 40, 128, 32
+    _, k, _ = oinp.make_random_kv(B, 4, HKV, S, D, seed=nbits)
+    k = k.to(DEV)
+    whole = quantize_groupwise(k, nbits, gs)
+    cache = empty_cache(B, HKV, S, D, nbits, gs, DEV)
+    cache.packed.zero_(), cache.scale.zero_(), cache.zero.zero_()
+    for t in range(S):
+        pos = torch.tensor([t] * B, dtype=torch.int32, device=DEV)
+        append_kv(cache, k[:, :, t:t + 1].contiguous(), pos)
+    assert torch.equal(cache.packed, whole.packed)
+    assert torch.equal(cache.scale, whole.scale)
+    assert torch.equal(cache.zero, whole.zero)
+
+
+def test_append_ragged_positions_and_out_of_range_rows_are_not_written():
+    from tritonkv_amd.quantize import append_kv, empty_cache, quantize_groupwise
+
+    B, HKV, S, D, nbits, gs = 4, 2, 16, 128, 4, 32
+    _, k, _ = oinp.make_random_kv(B, 4, HKV, 2, D, seed=9)
+    k = k.to(DEV)
+    cache = empty_cache(B, HKV, S, D, nbits, gs, DEV)
+    cache.packed.fill_(0xAB), cache.scale.zero_(), cache.zero.zero_()
+    pos = torch.tensor([0, 5, 15, 40], dtype=torch.int32, device=DEV)  # row 2: 1 of 2 fits; row 3: none
+    append_kv(cache, k, pos)
+    ref = quantize_groupwise(k, nbits, gs)
+    assert torch.equal(cache.packed[0, :, 0:2], ref.packed[0])
+    assert torch.equal(cache.packed[1, :, 5:7], ref.packed[1])
+    assert torch.equal(cache.packed[2, :, 15:16], ref.packed[2, :, :1])
+    assert bool((cache.packed[3] == 0xAB).all())
+    untouched = torch.ones(S, dtype=torch.bool, device=DEV)
+    untouched[5:7] = False
+    assert bool((cache.packed[1][:, untouched] == 0xAB).all())
+
+
+def test_roundtrip_error_report():
+    from tritonkv_amd.quantize import roundtrip_error
+
+    x = torch.randn(4, 7, 128, generator=torch.Generator().manual_seed(1)).to(DEV)
+    r4 = roundtrip_error(x, 4, 32)
+    r2 = roundtrip_error(x, 2, 32)
+    assert r4["effective_bits"] == 5.0 and r2["effective_bits"] == 3.0
+    assert r4["rel_l2"] < r2["rel_l2"] and r4["cosine"] > 0.99

@@ -1,0 +1,227 @@
+"""CPU tests of the host side and the C ABI (no kernel is launched).
+
+* the library loads and exports every symbol ``include/tkv.h`` declares;
+* the ctypes mirror of ``tkv_decode_args`` has the C struct's layout;
+* the C entry points reject bad arguments before touching the GPU;
+* the Python wrappers validate in the reference's order and raise its errors
+  (``kernels/fused_decode_attn.py:465-483``) before the backend check;
+* split arithmetic matches the oracle's restatement of the reference;
+* nothing on the product path runs on the CPU (no fallback).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+import torch
+
+from oracle import splits as osp
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tkv.h")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(tkv_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_abi():
+    syms = _declared_symbols()
+    for name in ("tkv_fused_decode_attention", "tkv_fp16_decode_attention", "tkv_combine_splits",
+                 "tkv_quantize_pack", "tkv_unpack_dequant", "tkv_pack_codes"):
+        assert name in syms
+
+
+def test_library_exports_every_declared_symbol():
+    from tritonkv_amd import _lib
+
+    lib = _lib.load()
+    for name in _declared_symbols():
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert lib.tkv_abi_version() == 1
+
+
+def test_library_is_gfx950_only():
+    from tritonkv_amd import _lib
+
+    with tempfile.TemporaryDirectory() as d:
+        fb = os.path.join(d, "fatbin.bin")
+        subprocess.run(["objcopy", "-O", "binary", "--only-section=.hip_fatbin", _lib.LIB_PATH, fb],
+                       check=True)
+        out = subprocess.run(["/opt/rocm/llvm/bin/clang-offload-bundler", "--list", "--type=o",
+                              f"--input={fb}"], capture_output=True, text=True, check=True)
+    targets = [t for t in out.stdout.split() if "amdgcn" in t]
+    assert targets == ["hipv4-amdgcn-amd-amdhsa--gfx950"], targets
+
+
+def test_decode_args_layout_matches_c():
+    from tritonkv_amd import _lib
+
+    src = r"""
+    #include <stdio.h>
+    #include <stddef.h>
+    #include "tkv.h"
+    int main(void) {
+      printf("%zu %zu %zu %zu %zu %zu %zu\n", sizeof(tkv_decode_args),
+             offsetof(tkv_decode_args, q_is_fp32), offsetof(tkv_decode_args, seq_lens),
+             offsetof(tkv_decode_args, B), offsetof(tkv_decode_args, sm_scale),
+             offsetof(tkv_decode_args, num_splits), sizeof(tkv_device_info_t));
+      return 0;
+    }"""
+    with tempfile.TemporaryDirectory() as d:
+        c = os.path.join(d, "l.c")
+        open(c, "w").write(src)
+        exe = os.path.join(d, "l")
+        subprocess.run(["gcc", "-I", os.path.dirname(HEADER), c, "-o", exe], check=True)
+        vals = [int(x) for x in subprocess.run([exe], capture_output=True, text=True,
+                                               check=True).stdout.split()]
+    A = _lib.DecodeArgs
+    assert vals == [ctypes.sizeof(A), A.q_is_fp32.offset, A.seq_lens.offset, A.B.offset,
+                    A.sm_scale.offset, A.num_splits.offset, ctypes.sizeof(_lib.DeviceInfo)]
+
+
+def test_c_entry_points_reject_bad_arguments_without_a_gpu():
+    from tritonkv_amd import _lib
+
+    lib = _lib.load()
+    a = _lib.DecodeArgs()  # all NULL / zero
+    assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    assert lib.tkv_fp16_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    assert lib.tkv_fused_decode_split(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    assert lib.tkv_combine_splits(None, None, None, None, 1, 1, 1, 128, None) == _lib.TKV_EINVAL
+    assert lib.tkv_quantize_pack(None, 0, 1, 1, 1, 128, 4, 32, None, 1, None, None, None,
+                                 None) == _lib.TKV_EINVAL
+    assert lib.tkv_pack_codes(None, 1, 128, 4, None, None) == _lib.TKV_EINVAL
+    assert lib.tkv_unpack_dequant(None, None, None, 1, 128, 4, 32, 0, None, None,
+                                  None) == _lib.TKV_EINVAL
+    # Non-null but inconsistent arguments: HQ not a multiple of HKV, uncovered history.
+    dummy = 0x1000
+    a = _lib.DecodeArgs(q=dummy, k=dummy, v=dummy, k_scale=dummy, k_zero=dummy, v_scale=dummy,
+                        v_zero=dummy, out=dummy, B=1, HQ=12, HKV=5, S=64, D=128, k_nbits=4,
+                        v_nbits=4, group_size=32, sm_scale=0.1, split_size=64, num_splits=1)
+    assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    a.HKV, a.split_size = 2, 32
+    assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    a.split_size, a.group_size = 64, 48
+    assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    a.group_size, a.D = 32, 96
+    assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EUNSUPPORTED
+    assert _lib.status_string(_lib.TKV_EINVAL) == "invalid argument"
+
+
+def _fake_qt(B=1, HKV=2, S=64, D=128, nbits=4, gs=32, device="cpu"):
+    from tritonkv_amd.quantize import QuantizedTensor
+
+    P = 8 // nbits
+    return QuantizedTensor(torch.zeros(B, HKV, S, D // P, dtype=torch.uint8, device=device),
+                           torch.ones(B, HKV, S, D // gs, dtype=torch.float16, device=device),
+                           torch.zeros(B, HKV, S, D // gs, dtype=torch.float16, device=device),
+                           nbits, gs, D)
+
+
+def test_python_validation_precedes_backend_check():
+    from tritonkv_amd.kernels import fused_decode_attention
+
+    q = torch.zeros(1, 12, 128, dtype=torch.float16)
+    with pytest.raises(ValueError, match="same nbits"):
+        fused_decode_attention(q, _fake_qt(nbits=4), _fake_qt(nbits=2))
+    with pytest.raises(ValueError, match="same nbits"):
+        fused_decode_attention(q, _fake_qt(gs=32), _fake_qt(gs=64))
+    with pytest.raises(ValueError, match="incompatible"):
+        fused_decode_attention(torch.zeros(2, 12, 128), _fake_qt(), _fake_qt())
+    with pytest.raises(ValueError, match="multiple of HKV"):
+        fused_decode_attention(torch.zeros(1, 12, 128), _fake_qt(HKV=5), _fake_qt(HKV=5))
+    with pytest.raises(ValueError, match="power of two"):
+        fused_decode_attention(torch.zeros(1, 12, 96), _fake_qt(D=96), _fake_qt(D=96))
+    with pytest.raises(ValueError, match="multiple of group_size"):
+        fused_decode_attention(torch.zeros(1, 12, 64), _fake_qt(D=64, gs=128),
+                               _fake_qt(D=64, gs=128))
+    with pytest.raises(ValueError, match="fold_zp"):
+        fused_decode_attention(q, _fake_qt(gs=8), _fake_qt(gs=8), fold_zp=True)
+    with pytest.raises(ValueError, match="same shape"):
+        fused_decode_attention(q, _fake_qt(S=64), _fake_qt(S=32))
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU error path")
+def test_backend_unavailable_raises_runtime_error():
+    from tritonkv_amd.kernels import fp16_decode_attention, fused_decode_attention, triton_available
+
+    ok, why = triton_available()
+    assert not ok and why
+    with pytest.raises(RuntimeError):
+        fused_decode_attention(torch.zeros(1, 12, 128), _fake_qt(), _fake_qt())
+    with pytest.raises(RuntimeError):
+        fp16_decode_attention(torch.zeros(1, 12, 128), torch.zeros(1, 2, 8, 128),
+                              torch.zeros(1, 2, 8, 128))
+
+
+def test_quantizer_has_no_cpu_fallback():
+    from tritonkv_amd import quantize as tq
+
+    with pytest.raises(RuntimeError, match="GPU"):
+        tq.quantize_groupwise(torch.randn(2, 128), 4, 32)
+    with pytest.raises(RuntimeError, match="GPU"):
+        tq.unpack_codes(torch.zeros(2, 64, dtype=torch.uint8), 4, 128)
+    with pytest.raises(RuntimeError, match="GPU"):
+        tq.pack_codes(torch.zeros(2, 128, dtype=torch.uint8), 4)
+    # argument errors still come first, as in quantize.py:68-70, :156-161, :177-178, :200-204
+    with pytest.raises(ValueError):
+        tq.quantize_groupwise(torch.randn(2, 128), 3, 32)
+    with pytest.raises(ValueError):
+        tq.quantize_groupwise(torch.randn(2, 128), 4, 48)
+    with pytest.raises(TypeError):
+        tq.pack_codes(torch.zeros(2, 128, dtype=torch.int32), 4)
+    with pytest.raises(ValueError):
+        tq.unpack_codes(torch.zeros(2, 60, dtype=torch.uint8), 4, 128)
+
+
+def test_quantized_tensor_accounting():
+    qt = _fake_qt(B=1, HKV=2, S=16, D=128, nbits=4, gs=32)
+    assert qt.effective_bits_per_element() == 5.0
+    assert qt.nbytes() * 8 / (2 * 16 * 128) == pytest.approx(5.0)
+    assert qt.shape == (1, 2, 16, 128) and qt.n_groups == 4 and qt.codes_per_byte == 2
+    assert _fake_qt(nbits=2).effective_bits_per_element() == 3.0
+
+
+@pytest.mark.parametrize("S,block_n,ns", [(4096, 64, 5), (4096, 64, 17), (4096, 64, 64),
+                                          (3000, 128, 7), (1, 64, 8), (17, 64, 3),
+                                          (16384, 16, 1000), (2048, 32, 2)])
+def test_plan_splits_honours_explicit_num_splits_like_the_reference(S, block_n, ns):
+    from tritonkv_amd.kernels import plan_splits
+
+    assert plan_splits(S, block_n, ns, 1, 2, 6) == osp.split_plan(S, block_n, ns)
+
+
+def test_pick_num_splits_formula():
+    from tritonkv_amd.kernels import pick_num_splits
+
+    for B, HKV, nb, tgt in [(1, 2, 256, 1024), (32, 8, 512, 1024), (64, 8, 100, 1024),
+                            (1, 1, 3, 7), (4, 8, 1, 1024)]:
+        assert pick_num_splits(B, HKV, nb, tgt) == osp.pick_num_splits(B, HKV, nb, tgt)
+
+
+@pytest.mark.parametrize("B,HKV,G,S", [(1, 2, 6, 512), (1, 2, 6, 16384), (32, 8, 4, 32768),
+                                       (64, 8, 8, 131072), (1, 8, 1, 1), (2, 8, 4, 17)])
+def test_default_split_plan_covers_history_without_empty_splits(B, HKV, G, S):
+    from tritonkv_amd.kernels import plan_splits
+
+    _, ns, size = plan_splits(S, 64, None, B, HKV, G)
+    assert ns >= 1 and size * ns >= S and size * (ns - 1) < S
+
+
+def test_timing_stats_match_reference_definition():
+    from tritonkv_amd.timing import replicas_for, stats
+
+    s = stats([4.0, 1.0, 3.0, 2.0])
+    assert s["median_ms"] == 2.5 and s["p25_ms"] == 1.75 and s["p75_ms"] == 3.25
+    assert s["iqr_frac_of_median"] == pytest.approx(0.6)
+    assert replicas_for(163_840, 768_000_000) == 4688
+    assert replicas_for(16_777_216, 768_000_000) == 46
+    assert replicas_for(0, 768_000_000) == 1

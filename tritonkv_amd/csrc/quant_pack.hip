@@ -1,0 +1,324 @@
+// GPU quantize/pack (decode-step append and whole-cache setup), split-P pack
+// of given codes, and the unpack/dequant export used to prove bit-exactness.
+//
+// Reference behaviour being reproduced bit for bit:
+//   quantize_groupwise  quantize.py:186-236   (fp32 min/max per group,
+//       scale = range/qmax or 1 for a degenerate group, scale and zero rounded
+//       to fp16 first, code = rint((x - zero)/scale) clamped to [0, qmax])
+//   pack_codes          quantize.py:149-169
+//   unpack_codes        quantize.py:172-183
+//   dequantize_groupwise quantize.py:239-246 (fp32 code*scale + zero; the
+//       product is exact since code <= 15 and scale has 11 significant bits,
+//       so fmaf gives the same bits as the reference's mul-then-add)
+//
+// The arithmetic relies on IEEE binary32 division (hipcc's default correctly
+// rounded fp32 divide -- this file must not be built with fast-math) and on
+// rintf rounding half to even like torch.round.
+#include <type_traits>
+
+#include "tkv_codec.h"
+#include "../../include/tkv.h"
+
+namespace tkv {
+
+// One wave per cache row (token x kv head); lane l holds dims [l*EPL, l*EPL+EPL).
+template <int D, int NB, int GS, bool F32>
+__global__ void __launch_bounds__(256)
+quantize_pack_kernel(const void* __restrict__ x, int64_t rows, int HKV, int N,
+                     const int32_t* __restrict__ positions, int S_cap,
+                     uint8_t* __restrict__ packed, uint16_t* __restrict__ scale,
+                     uint16_t* __restrict__ zero) {
+  constexpr int EPL = D / 64;
+  constexpr int LPG = GS / EPL;  // lanes per group
+  constexpr int P = 8 / NB, DP = D / P, NG = D / GS, QMAX = (1 << NB) - 1;
+  __shared__ uint8_t codes_lds[4][D];
+
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t rr = (int64_t)blockIdx.x * 4 + w;
+  if (rr >= rows) return;  // whole wave; no workgroup barrier below
+  const int64_t bh = rr / N;
+  const int t = (int)(rr % N);
+  const int b = (int)(bh / HKV);
+  const int64_t dst_t = (int64_t)(positions ? positions[b] : 0) + t;
+  const bool in_range = dst_t >= 0 && dst_t < S_cap;
+  const int64_t dst_row = bh * S_cap + dst_t;
+
+  float xv[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const int64_t idx = rr * D + lane * EPL + e;
+    xv[e] = F32 ? static_cast<const float*>(x)[idx] : (float)static_cast<const _Float16*>(x)[idx];
+  }
+  float mn = xv[0], mx = xv[0];
+#pragma unroll
+  for (int e = 1; e < EPL; ++e) {
+    mn = fminf(mn, xv[e]);
+    mx = fmaxf(mx, xv[e]);
+  }
+#pragma unroll
+  for (int k = 1; k < LPG; k <<= 1) {
+    mn = fminf(mn, __shfl_xor(mn, k, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, k, 64));
+  }
+  float sc = (mx - mn) / (float)QMAX;
+  if (!(sc > 0.0f)) sc = 1.0f;
+  const _Float16 s16 = (_Float16)sc;
+  const _Float16 z16 = (_Float16)mn;
+  const float sf = (float)s16, zf = (float)z16;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    float c = rintf((xv[e] - zf) / sf);
+    if (c != c) c = 0.0f;  // 0/0 when the fp16 scale underflows: torch yields code 0
+    c = fminf(fmaxf(c, 0.0f), (float)QMAX);
+    codes_lds[w][lane * EPL + e] = (uint8_t)c;
+  }
+  if (in_range && (lane % LPG) == 0) {
+    const int g = lane / LPG;
+    scale[dst_row * NG + g] = __builtin_bit_cast(uint16_t, s16);
+    zero[dst_row * NG + g] = __builtin_bit_cast(uint16_t, z16);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (in_range && lane < DP / 4) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int jb = 4 * lane + k;
+      uint32_t byte = 0;
+#pragma unroll
+      for (int p = 0; p < P; ++p) byte |= (uint32_t)codes_lds[w][jb + p * DP] << (p * NB);
+      word |= byte << (8 * k);
+    }
+    reinterpret_cast<uint32_t*>(packed + dst_row * DP)[lane] = word;
+  }
+}
+
+// One thread per packed dword.
+__global__ void __launch_bounds__(256)
+pack_codes_kernel(const uint8_t* __restrict__ codes, int64_t rows, int D, int NB,
+                  uint8_t* __restrict__ packed) {
+  const int P = 8 / NB, DP = D / P, DW = DP / 4;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * DW) return;
+  const int64_t row = i / DW;
+  const int q = (int)(i % DW);
+  const uint8_t* c = codes + row * D;
+  uint32_t word = 0;
+  for (int k = 0; k < 4; ++k) {
+    const int jb = 4 * q + k;
+    uint32_t byte = 0;
+    for (int p = 0; p < P; ++p) byte |= (uint32_t)(c[jb + p * DP] & ((1 << NB) - 1)) << (p * NB);
+    word |= byte << (8 * k);
+  }
+  reinterpret_cast<uint32_t*>(packed + row * DP)[q] = word;
+}
+
+__device__ __forceinline__ void emit(uint8_t* codes_out, float* values_out,
+                                     const uint16_t* scale, const uint16_t* zero, int64_t row,
+                                     int D, int GS, int d, uint32_t code) {
+  if (codes_out) codes_out[row * D + d] = (uint8_t)code;
+  if (values_out) {
+    const int NG = D / GS;
+    const float s = (float)__builtin_bit_cast(_Float16, scale[row * NG + d / GS]);
+    const float z = (float)__builtin_bit_cast(_Float16, zero[row * NG + d / GS]);
+    values_out[row * D + d] = fmaf((float)code, s, z);
+  }
+}
+
+// Path 0: the K-operand extraction of the decode kernel.  One wave per 16 rows;
+// lane (r = l%16, j = l/16) plays the MFMA A-operand role for row r.
+template <int D, int NB, int GS>
+__global__ void __launch_bounds__(64)
+unpack_k_kernel(const uint8_t* __restrict__ packed, const uint16_t* __restrict__ scale,
+                const uint16_t* __restrict__ zero, int64_t rows, uint8_t* codes_out,
+                float* values_out) {
+  using KL = KLayout<D, NB, GS>;
+  const int lane = threadIdx.x, r = lane & 15, j = lane >> 4;
+  const int64_t row = (int64_t)blockIdx.x * 16 + r;
+  const int64_t lr = row < rows ? row : rows - 1;
+  typename std::conditional<KL::CB == 8, u2, uint32_t>::type kx[KL::NLOAD];
+#pragma unroll
+  for (int Lh = 0; Lh < KL::NLOAD; ++Lh) {
+    const uint8_t* src = packed + lr * KL::DP + KL::load_offset(Lh, j);
+    if constexpr (KL::CB == 8) kx[Lh] = ld_u2(src);
+    else kx[Lh] = ld_u32(src);
+  }
+  if (row >= rows) return;
+#pragma unroll
+  for (int m = 0; m < KL::NKM; ++m) {
+    const int p = KL::slice_of(m, j);
+    const uint32_t mask = slice_mask<NB>(p);
+    uint32_t wv[4] = {0, 0, 0, 0};
+    if constexpr (KL::CB == 8) {
+      const u4 a = k_extract8(kx[KL::load_of_step(m)], mask);
+      wv[0] = a[0]; wv[1] = a[1]; wv[2] = a[2]; wv[3] = a[3];
+    } else {
+      const u2 a = k_extract4(kx[KL::load_of_step(m)], mask);
+      wv[0] = a[0]; wv[1] = a[1];
+    }
+#pragma unroll
+    for (int s = 0; s < KL::CB; ++s) {
+      const uint32_t half = (s & 1) ? (wv[s / 2] >> 16) : wv[s / 2];
+      emit(codes_out, values_out, scale, zero, row, D, GS, KL::dim_of(m, j, s),
+           code_of_half(half, p * NB));
+    }
+  }
+}
+
+// Path 1: the transposed V-operand extraction.  One wave per 32 tokens; lane
+// (r, j) gathers tokens slot_token(j, 0..7) for A-operand row r.
+template <int D, int NB, int GS>
+__global__ void __launch_bounds__(64)
+unpack_v_kernel(const uint8_t* __restrict__ packed, const uint16_t* __restrict__ scale,
+                const uint16_t* __restrict__ zero, int64_t rows, uint8_t* codes_out,
+                float* values_out) {
+  using VL = VLayout<D, NB, GS>;
+  const int lane = threadIdx.x, r = lane & 15, j = lane >> 4;
+  const int64_t base = (int64_t)blockIdx.x * 32;
+  uint32_t vx[8][VL::NWIN];
+  int64_t tok[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    tok[i] = base + (i < 4 ? 0 : 12) + 4 * j + i;
+    const int64_t lr = tok[i] < rows ? tok[i] : rows - 1;
+#pragma unroll
+    for (int wi = 0; wi < VL::NWIN; ++wi)
+      vx[i][wi] = ld_u32(packed + lr * VL::DP + VL::dword_offset(wi, r));
+  }
+#pragma unroll
+  for (int wi = 0; wi < VL::NWIN; ++wi) {
+#pragma unroll
+    for (int e = 0; e < VL::NE; ++e) {
+      const uint32_t sel = VL::perm_sel(VL::byte_in_dword(e, r));
+#pragma unroll
+      for (int p = 0; p < VL::P; ++p) {
+        const int mv = VL::mfma_index(p, wi, e);
+        const int d = VL::dim_of(mv, r);
+        const uint32_t mask = slice_mask<NB>(p);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t pr = v_extract(vx[2 * i + 1][wi], vx[2 * i][wi], sel, mask);
+          if (tok[2 * i] < rows)
+            emit(codes_out, values_out, scale, zero, tok[2 * i], D, GS, d,
+                 code_of_half(pr, p * NB));
+          if (tok[2 * i + 1] < rows)
+            emit(codes_out, values_out, scale, zero, tok[2 * i + 1], D, GS, d,
+                 code_of_half(pr >> 16, p * NB));
+        }
+      }
+    }
+  }
+}
+
+template <int D, int NB, int GS>
+static void launch_quantize(const void* x, bool f32, int64_t rows, int HKV, int N,
+                            const int32_t* pos, int S_cap, uint8_t* pk, uint16_t* sc,
+                            uint16_t* zr, hipStream_t st) {
+  const dim3 grid((unsigned)((rows + 3) / 4));
+  if (f32)
+    quantize_pack_kernel<D, NB, GS, true><<<grid, 256, 0, st>>>(x, rows, HKV, N, pos, S_cap, pk, sc, zr);
+  else
+    quantize_pack_kernel<D, NB, GS, false><<<grid, 256, 0, st>>>(x, rows, HKV, N, pos, S_cap, pk, sc, zr);
+}
+
+template <int D, int NB, int GS>
+static void launch_unpack(const uint8_t* pk, const uint16_t* sc, const uint16_t* zr, int64_t rows,
+                          int path, uint8_t* co, float* vo, hipStream_t st) {
+  if (path == 0)
+    unpack_k_kernel<D, NB, GS><<<dim3((unsigned)((rows + 15) / 16)), 64, 0, st>>>(pk, sc, zr, rows, co, vo);
+  else
+    unpack_v_kernel<D, NB, GS><<<dim3((unsigned)((rows + 31) / 32)), 64, 0, st>>>(pk, sc, zr, rows, co, vo);
+}
+
+// Calls F<D, NB, GS>::run(args...) for the compiled (D, nbits, group size) set.
+#define TKV_DISPATCH_DNG(D_, NB_, GS_, CALL)                                          \
+  do {                                                                               \
+    if ((D_) == 128) {                                                               \
+      if ((NB_) == 4) {                                                              \
+        if ((GS_) == 16) { CALL(128, 4, 16); }                                       \
+        else if ((GS_) == 32) { CALL(128, 4, 32); }                                  \
+        else if ((GS_) == 64) { CALL(128, 4, 64); }                                  \
+        else if ((GS_) == 128) { CALL(128, 4, 128); }                                \
+        else return TKV_EUNSUPPORTED;                                                \
+      } else {                                                                       \
+        if ((GS_) == 16) { CALL(128, 2, 16); }                                       \
+        else if ((GS_) == 32) { CALL(128, 2, 32); }                                  \
+        else if ((GS_) == 64) { CALL(128, 2, 64); }                                  \
+        else if ((GS_) == 128) { CALL(128, 2, 128); }                                \
+        else return TKV_EUNSUPPORTED;                                                \
+      }                                                                              \
+    } else if ((D_) == 64) {                                                         \
+      if ((NB_) == 4) {                                                              \
+        if ((GS_) == 16) { CALL(64, 4, 16); }                                        \
+        else if ((GS_) == 32) { CALL(64, 4, 32); }                                   \
+        else if ((GS_) == 64) { CALL(64, 4, 64); }                                   \
+        else return TKV_EUNSUPPORTED;                                                \
+      } else {                                                                       \
+        if ((GS_) == 16) { CALL(64, 2, 16); }                                        \
+        else if ((GS_) == 32) { CALL(64, 2, 32); }                                   \
+        else if ((GS_) == 64) { CALL(64, 2, 64); }                                   \
+        else return TKV_EUNSUPPORTED;                                                \
+      }                                                                              \
+    } else {                                                                         \
+      return TKV_EUNSUPPORTED;                                                       \
+    }                                                                                \
+  } while (0)
+
+}  // namespace tkv
+
+extern "C" int tkv_quantize_pack(const void* x, int32_t x_is_fp32, int32_t B, int32_t HKV,
+                                 int32_t N, int32_t D, int32_t nbits, int32_t group_size,
+                                 const int32_t* positions, int32_t S_cap, uint8_t* packed,
+                                 uint16_t* scale, uint16_t* zero, tkv_stream_t stream) {
+  using namespace tkv;
+  if (!x || !packed || !scale || !zero) return TKV_EINVAL;
+  if (B <= 0 || HKV <= 0 || N <= 0 || D <= 0 || S_cap <= 0) return TKV_EINVAL;
+  if (nbits != 2 && nbits != 4) return TKV_EINVAL;
+  if (group_size <= 0 || D % group_size) return TKV_EINVAL;
+  if (!positions && N > S_cap) return TKV_EINVAL;
+  const int64_t rows = (int64_t)B * HKV * N;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  (void)hipGetLastError();
+#define TKV_Q(Dv, NBv, GSv) \
+  launch_quantize<Dv, NBv, GSv>(x, x_is_fp32 != 0, rows, HKV, N, positions, S_cap, packed, scale, zero, st)
+  TKV_DISPATCH_DNG(D, nbits, group_size, TKV_Q);
+#undef TKV_Q
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? TKV_OK : (int)e;
+}
+
+extern "C" int tkv_pack_codes(const uint8_t* codes, int64_t rows, int32_t D, int32_t nbits,
+                              uint8_t* packed, tkv_stream_t stream) {
+  using namespace tkv;
+  if (!codes || !packed || rows <= 0 || D <= 0) return TKV_EINVAL;
+  if (nbits != 2 && nbits != 4) return TKV_EINVAL;
+  const int P = 8 / nbits;
+  if (D % (4 * P)) return TKV_EUNSUPPORTED;  // whole packed dwords per row
+  const int64_t n = rows * (D / P / 4);
+  (void)hipGetLastError();
+  pack_codes_kernel<<<dim3((unsigned)((n + 255) / 256)), 256, 0,
+                      reinterpret_cast<hipStream_t>(stream)>>>(codes, rows, D, nbits, packed);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? TKV_OK : (int)e;
+}
+
+extern "C" int tkv_unpack_dequant(const uint8_t* packed, const uint16_t* scale,
+                                  const uint16_t* zero, int64_t rows, int32_t D, int32_t nbits,
+                                  int32_t group_size, int32_t path, uint8_t* codes_out,
+                                  float* values_out, tkv_stream_t stream) {
+  using namespace tkv;
+  if (!packed || rows <= 0 || D <= 0) return TKV_EINVAL;
+  if (nbits != 2 && nbits != 4) return TKV_EINVAL;
+  if (group_size <= 0 || D % group_size) return TKV_EINVAL;
+  if (path != 0 && path != 1) return TKV_EINVAL;
+  if (values_out && (!scale || !zero)) return TKV_EINVAL;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  (void)hipGetLastError();
+#define TKV_U(Dv, NBv, GSv) \
+  launch_unpack<Dv, NBv, GSv>(packed, scale, zero, rows, path, codes_out, values_out, st)
+  TKV_DISPATCH_DNG(D, nbits, group_size, TKV_U);
+#undef TKV_U
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? TKV_OK : (int)e;
+}

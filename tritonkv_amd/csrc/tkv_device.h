@@ -1,0 +1,117 @@
+// Device-side building blocks shared by the tritonkv_amd HIP kernels (gfx950).
+//
+// Everything here is written for CDNA4: 64-wide wavefronts, the
+// v_mfma_f32_16x16x{16,32}_f16 matrix instructions, and v_perm_b32 / bitwise
+// AND for unpacking split-P codes straight into MFMA operand registers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tkv {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+// MFMA operands carry codes as fp16 *subnormals*: the bit pattern c << s is the
+// value c * 2^(s-24), exact.  Products with fp16 q are exact in fp32, so every
+// quantized dot product comes out scaled by 2^-24 and is rescaled once in fp32.
+constexpr float kTwo24 = 16777216.0f;
+constexpr float kTwoM24 = 5.9604644775390625e-08f;
+
+// ---------------------------------------------------------------------------
+// MFMA wrappers.  Lane layout (verified on gfx950):
+//   A: lane l holds A[l%16][K/4*(l/16) + i]     (i < K/4)
+//   B: lane l holds B[K/4*(l/16) + i][l%16]
+//   D: lane l holds D[4*(l/16) + i][l%16]        (i < 4)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ f4 mfma_k32(u4 a, u4 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a),
+                                                __builtin_bit_cast(h8, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f4 mfma_k16(u2 a, u2 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, a),
+                                               __builtin_bit_cast(h4, b), c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// Split-P code extraction.
+//
+// Layout (reference quantize.py:40-54): byte j of a packed row holds the codes
+// of dims j, j+DP, j+2*DP, ... in bit slices of NBITS bits.  From one dword
+// holding bytes (b0,b1,b2,b3) of a row, slice p of bytes b0 and b2 is
+//     x & ((m << s) | (m << (16+s)))         s = p*NBITS, m = 2^NBITS-1
+// which *is* a pair of fp16 subnormals (b0's code << s, b2's code << s).
+// Bytes b1/b3 need one shift by 8 first.  So a dword yields its 4*P codes as
+// 2*P fp16 pairs in "slot order" b0,b2,b1,b3.
+// ---------------------------------------------------------------------------
+template <int NBITS>
+__device__ __forceinline__ constexpr uint32_t slice_mask(int p) {
+  return ((((1u << NBITS) - 1u) << (p * NBITS)) * 0x00010001u);
+}
+
+// Slot order of the four bytes of a dword after extraction: slots 0,1 come
+// from bytes 0,2 and slots 2,3 from bytes 1,3.
+__device__ __forceinline__ constexpr int slot_byte(int s) {
+  return (s & ~3) + ((s & 1) << 1) + ((s >> 1) & 1);
+}
+
+// Decode a subnormal-encoded fp16 half back to an integer code.
+__device__ __forceinline__ uint32_t code_of_half(uint32_t half_bits, int shift) {
+  return (half_bits & 0xffffu) >> shift;
+}
+
+// ---------------------------------------------------------------------------
+// Wave-level helpers.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float xor_max16_32(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  v = fmaxf(v, __shfl_xor(v, 32, 64));
+  return v;
+}
+__device__ __forceinline__ float xor_sum16_32(float v) {
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
+  h2 v = {(_Float16)lo, (_Float16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ float half_lo(uint32_t w) {
+  return (float)__builtin_bit_cast(h2, w)[0];
+}
+__device__ __forceinline__ float half_hi(uint32_t w) {
+  return (float)__builtin_bit_cast(h2, w)[1];
+}
+__device__ __forceinline__ uint32_t pk_mul(uint32_t a, uint32_t b) {
+  h2 r = __builtin_bit_cast(h2, a) * __builtin_bit_cast(h2, b);
+  return __builtin_bit_cast(uint32_t, r);
+}
+__device__ __forceinline__ uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi_src, lo_src, sel);
+}
+
+__device__ __forceinline__ float safe_exp2_diff(float a, float b) {
+  // exp2(a - b) with exp2(-inf - x) = 0 and never NaN for a == b == -inf.
+  return (a == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(a - b);
+}
+
+// Global loads of 4/8/16 bytes through the vector memory path.
+__device__ __forceinline__ uint32_t ld_u32(const uint8_t* p) {
+  return *reinterpret_cast<const uint32_t*>(p);
+}
+__device__ __forceinline__ u2 ld_u2(const uint8_t* p) {
+  return *reinterpret_cast<const u2*>(p);
+}
+__device__ __forceinline__ u4 ld_u4(const uint8_t* p) {
+  return *reinterpret_cast<const u4*>(p);
+}
+
+}  // namespace tkv

@@ -1,0 +1,79 @@
+"""fp16 flash-decoding attention on MI355X -- the *control* for the fused kernel.
+
+Drop-in for the reference's ``kernels/fp16_decode_attn.py``
+(``fp16_decode_attention`` :142-241).  It uses the same split arithmetic and
+workspace as the fused path and the same C-ABI skeleton
+(``tkv_fp16_decode_attention``): identical split, online softmax, GQA grouping,
+workgroup merge and combine kernel, with K/V read as fp16 instead of being
+unpacked -- so fused vs control isolates the quantization effect, and SDPA vs
+control the flash-decoding effect (reference :1-25).
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .. import _lib
+from .fused_decode_attn import (
+    _check_out,
+    _seq_lens_arg,
+    _workspace_for,
+    plan_splits,
+    triton_available,
+)
+
+
+def fp16_decode_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    sm_scale: float | None = None,
+    block_n: int = 64,
+    num_warps: int = 4,
+    num_stages: int = 2,
+    num_splits: int | None = None,
+    out: torch.Tensor | None = None,
+    _workspace: dict | None = None,
+    *,
+    seq_lens: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Decode attention on an unquantized fp16 cache, same shape as the fused kernel.
+
+    q: (B, HQ, D); k, v: (B, HKV, S, D) fp16. Returns (B, HQ, D) float32.
+    """
+    B, HQ, D = q.shape
+    _, HKV, S, _ = k.shape
+    if HQ % HKV != 0:
+        raise ValueError(f"HQ={HQ} must be a multiple of HKV={HKV}")
+    if k.shape != v.shape or k.shape[0] != B or k.shape[3] != D:
+        raise ValueError(f"k {tuple(k.shape)} / v {tuple(v.shape)} incompatible with q {tuple(q.shape)}")
+
+    ok, why = triton_available()
+    if not ok:
+        raise RuntimeError(f"tritonkv_amd HIP backend unavailable: {why}")
+
+    group = HQ // HKV
+    sm_scale = 1.0 / math.sqrt(D) if sm_scale is None else sm_scale
+    _, num_splits, split_size = plan_splits(S, block_n, num_splits, B, HKV, group)
+
+    q = q.contiguous()
+    if q.dtype not in (torch.float16, torch.float32):
+        q = q.float()
+    k = k.contiguous() if k.dtype == torch.float16 else k.half().contiguous()
+    v = v.contiguous() if v.dtype == torch.float16 else v.half().contiguous()
+    out = _check_out(out, B, HQ, D, q.device)
+    acc, maxs, sums = _workspace_for(_workspace, B, HQ, num_splits, D, q.device)
+    lens = _seq_lens_arg(seq_lens, B, S, q.device)
+
+    args = _lib.DecodeArgs(
+        q=q.data_ptr(), q_is_fp32=int(q.dtype == torch.float32),
+        k=k.data_ptr(), v=v.data_ptr(), seq_lens=_lib.ptr(lens),
+        acc=_lib.ptr(acc), maxs=_lib.ptr(maxs), sums=_lib.ptr(sums), out=out.data_ptr(),
+        B=B, HQ=HQ, HKV=HKV, S=S, D=D, k_nbits=16, v_nbits=16, group_size=D,
+        sm_scale=float(sm_scale), split_size=split_size, num_splits=num_splits)
+    with torch.cuda.device(q.device):
+        rc = _lib.load().tkv_fp16_decode_attention(args, _lib.stream_handle(q.device))
+    _lib.check(rc, "fp16_decode_attention")
+    return out

@@ -1,0 +1,231 @@
+"""Fused dequantize + decode attention on MI355X (gfx950 HIP kernels).
+
+Drop-in for the reference's ``kernels/fused_decode_attn.py``: same public names
+(``fused_decode_attention`` :419-570, ``pick_num_splits`` :402-416,
+``triton_available`` :81-86), same arguments, defaults, validation order of
+checks, split arithmetic, workspace keys and return value.  The two Triton
+launches (split :525-556, combine :558-568) are replaced by one call into the
+C ABI ``tkv_fused_decode_attention`` (``include/tkv.h``), which enqueues the
+gfx950 split kernel and, for more than one split, the combine kernel on
+torch's current stream.  Nothing is allocated inside the call once ``out`` and
+``_workspace`` are supplied, so it can be captured in a HIP graph.
+
+Differences a caller can observe, all deliberate:
+
+* Argument errors are raised *before* the backend check, so they are testable
+  on a host without a GPU (the reference checks the backend first, :461-463).
+* ``num_warps`` / ``num_stages`` are Triton tuning knobs: accepted and ignored.
+  ``meta_bcast`` and ``dequant_fp16`` selected between bitwise-identical
+  Triton variants (``test_correctness.py:292-343``); here both values run the
+  same kernel, so the outputs are trivially ``torch.equal``.
+* ``fold_zp``: the HIP kernel always computes scores in the folded form
+  ``sum_g s_g (q_g . c_g) + z_g sum(q_g)`` (the reference's FOLD_ZP algebra,
+  :229-272) -- it is the form that lets the matrix cores consume raw codes.
+  The ``gs >= 16`` check of ``fold_zp=True`` is kept.
+* When ``num_splits`` is None the split count is chosen for 256 compute units
+  (see :func:`default_num_splits`); an explicit ``num_splits`` is honoured
+  exactly as in the reference (clamp to ``n_blocks``, then tighten).
+* ``allow_mixed_bits=True`` (new, keyword-only) lets K and V use different bit
+  widths (e.g. 4-bit K, 2-bit V); without it the reference's ValueError is
+  raised.  ``seq_lens`` (new) gives one context length per batch row.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .. import _lib
+from ..quantize import QuantizedTensor
+
+LOG2E = 1.4426950408889634
+
+# Fewest tokens one workgroup should stream: 4 waves x 32-token chunks.
+_MIN_SPLIT_TOKENS = 128
+
+
+def triton_available() -> tuple[bool, str]:
+    """``(ok, why)`` for the HIP backend (the reference's name is kept for callers)."""
+    err = _lib.load_error()
+    if err is not None:
+        return False, err
+    if not torch.cuda.is_available():
+        return False, "torch.cuda.is_available() is False"
+    return True, f"tritonkv_amd HIP backend (abi {_lib.load().tkv_abi_version()})"
+
+
+hip_available = triton_available
+
+
+def _next_pow2(x: int) -> int:
+    return 1 << (x - 1).bit_length()
+
+
+def _cdiv(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+_CU_COUNT: dict = {}
+
+
+def compute_units(device=None) -> int | None:
+    try:
+        dev = torch.cuda.current_device() if device is None else torch.device(device).index or 0
+        if dev not in _CU_COUNT:
+            _CU_COUNT[dev] = torch.cuda.get_device_properties(dev).multi_processor_count
+        return _CU_COUNT[dev]
+    except Exception:
+        return None
+
+
+def pick_num_splits(B: int, HKV: int, n_blocks: int, target_programs: int | None = None) -> int:
+    """The reference's heuristic (:402-416): ``target // (B*HKV)`` clamped to ``[1, n_blocks]``.
+
+    ``target_programs`` defaults to 4 programs per compute unit (1024 on a
+    256-CU MI355X), or 128 without a device.
+    """
+    if target_programs is None:
+        cu = compute_units()
+        target_programs = cu * 4 if cu else 128
+    want = max(1, target_programs // max(1, B * HKV))
+    return max(1, min(n_blocks, want))
+
+
+def default_num_splits(B: int, HKV: int, G: int, S: int, block_n: int) -> int:
+    """Split count used when the caller passes ``num_splits=None``.
+
+    Aims at two workgroups per compute unit (each workgroup is 4 waves and
+    streams at least 128 tokens), counting every (batch row, kv head, block of
+    16 query heads) as one unit of parallelism.  Returned in units of
+    ``block_n`` blocks so the reference's tightening applies unchanged.
+    """
+    cu = compute_units() or 256
+    units = B * HKV * _cdiv(G, 16)
+    want = max(1, _cdiv(2 * cu, units))
+    n_blocks = _cdiv(S, block_n)
+    max_splits = max(1, _cdiv(S, max(_MIN_SPLIT_TOKENS, block_n)))
+    return max(1, min(want, max_splits, n_blocks))
+
+
+def plan_splits(S: int, block_n: int, num_splits: int | None, B: int, HKV: int, G: int):
+    """Reference split arithmetic (:486-499) -> (block_n, num_splits, split_size)."""
+    block_n = min(block_n, max(16, _next_pow2(S)))
+    n_blocks = _cdiv(S, block_n)
+    if num_splits is None:
+        num_splits = default_num_splits(B, HKV, G, S, block_n)
+    num_splits = max(1, min(num_splits, n_blocks))
+    blocks_per_split = _cdiv(n_blocks, num_splits)
+    num_splits = _cdiv(n_blocks, blocks_per_split)  # tighten: no empty splits
+    return block_n, num_splits, blocks_per_split * block_n
+
+
+def _workspace_for(ws: dict | None, B: int, HQ: int, num_splits: int, D: int, device):
+    """Partials buffers, reused under the reference's keys (:505-521)."""
+    ws = ws if ws is not None else {}
+    if num_splits == 1:
+        acc = ws.get("dummy_acc")
+        if acc is None:
+            acc = torch.empty((1, 1, 1, 1), device=device, dtype=torch.float32)
+            ws["dummy_acc"] = acc
+        return None, None, None
+    key = (B, HQ, num_splits, D)
+    if ws.get("key") == key:
+        return ws["acc"], ws["maxs"], ws["sums"]
+    acc = torch.empty((B, HQ, num_splits, D), device=device, dtype=torch.float32)
+    maxs = torch.empty((B, HQ, num_splits), device=device, dtype=torch.float32)
+    sums = torch.empty((B, HQ, num_splits), device=device, dtype=torch.float32)
+    ws.update(key=key, acc=acc, maxs=maxs, sums=sums)
+    return acc, maxs, sums
+
+
+def _check_out(out, B, HQ, D, device):
+    if out is None:
+        return torch.empty((B, HQ, D), device=device, dtype=torch.float32)
+    if out.shape != (B, HQ, D) or out.dtype != torch.float32 or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous float32 ({B}, {HQ}, {D}) tensor")
+    return out
+
+
+def _seq_lens_arg(seq_lens, B, S, device):
+    if seq_lens is None:
+        return None
+    if not isinstance(seq_lens, torch.Tensor) or seq_lens.dtype != torch.int32 \
+            or seq_lens.numel() != B or seq_lens.device != device:
+        raise ValueError("seq_lens must be an int32 tensor of B lengths on the cache's device")
+    return seq_lens.contiguous()
+
+
+def fused_decode_attention(
+    q: torch.Tensor,
+    kq: QuantizedTensor,
+    vq: QuantizedTensor,
+    sm_scale: float | None = None,
+    block_n: int = 64,
+    num_warps: int = 4,
+    num_stages: int = 2,
+    num_splits: int | None = None,
+    meta_bcast: bool = True,
+    fold_zp: bool = False,
+    dequant_fp16: bool = False,
+    out: torch.Tensor | None = None,
+    _workspace: dict | None = None,
+    *,
+    seq_lens: torch.Tensor | None = None,
+    allow_mixed_bits: bool = False,
+) -> torch.Tensor:
+    """Single decode step of attention, computed directly on packed low-bit K/V.
+
+    q: ``(B, HQ, D)`` fp16 or fp32 (rounded to fp16 in the kernel, as the
+    reference does); kq, vq: quantized caches with ``packed`` of shape
+    ``(B, HKV, S, D//P)``.  Returns ``(B, HQ, D)`` float32.
+    """
+    if kq.group_size != vq.group_size or (kq.nbits != vq.nbits and not allow_mixed_bits):
+        raise ValueError("K and V must use the same nbits/group_size")
+
+    B, HQ, D = q.shape
+    Bk, HKV, S, DPk = kq.packed.shape
+    if (B, D) != (Bk, kq.head_dim):
+        raise ValueError(f"q shape {tuple(q.shape)} incompatible with cache {tuple(kq.packed.shape)}")
+    if vq.packed.shape[:3] != kq.packed.shape[:3] or vq.head_dim != kq.head_dim \
+            or (vq.nbits == kq.nbits and vq.packed.shape != kq.packed.shape):
+        raise ValueError("K and V caches must have the same shape")
+    if HQ % HKV != 0:
+        raise ValueError(f"HQ={HQ} must be a multiple of HKV={HKV}")
+    if D & (D - 1):
+        raise ValueError(f"head_dim must be a power of two, got {D}")
+    if D % kq.group_size:
+        raise ValueError(f"head_dim {D} must be a multiple of group_size {kq.group_size}")
+    if fold_zp and kq.group_size < 16:
+        raise ValueError(f"fold_zp needs group_size >= 16, got {kq.group_size}")
+
+    ok, why = triton_available()
+    if not ok:
+        raise RuntimeError(f"fused_decode_attention requires the tritonkv_amd HIP backend: {why}")
+
+    group = HQ // HKV
+    sm_scale = 1.0 / math.sqrt(D) if sm_scale is None else sm_scale
+    _, num_splits, split_size = plan_splits(S, block_n, num_splits, B, HKV, group)
+
+    q = q.contiguous()
+    if q.dtype not in (torch.float16, torch.float32):
+        q = q.float()
+    kp, ks, kz = kq.packed.contiguous(), kq.scale.contiguous(), kq.zero.contiguous()
+    vp, vs, vz = vq.packed.contiguous(), vq.scale.contiguous(), vq.zero.contiguous()
+    out = _check_out(out, B, HQ, D, q.device)
+    acc, maxs, sums = _workspace_for(_workspace, B, HQ, num_splits, D, q.device)
+    lens = _seq_lens_arg(seq_lens, B, S, q.device)
+
+    args = _lib.DecodeArgs(
+        q=q.data_ptr(), q_is_fp32=int(q.dtype == torch.float32),
+        k=kp.data_ptr(), k_scale=ks.data_ptr(), k_zero=kz.data_ptr(),
+        v=vp.data_ptr(), v_scale=vs.data_ptr(), v_zero=vz.data_ptr(),
+        seq_lens=_lib.ptr(lens), acc=_lib.ptr(acc), maxs=_lib.ptr(maxs), sums=_lib.ptr(sums),
+        out=out.data_ptr(), B=B, HQ=HQ, HKV=HKV, S=S, D=D,
+        k_nbits=kq.nbits, v_nbits=vq.nbits, group_size=kq.group_size,
+        sm_scale=float(sm_scale), split_size=split_size, num_splits=num_splits)
+    with torch.cuda.device(q.device):
+        rc = _lib.load().tkv_fused_decode_attention(args, _lib.stream_handle(q.device))
+    _lib.check(rc, "fused_decode_attention")
+    return out
+
