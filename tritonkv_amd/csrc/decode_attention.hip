@@ -568,6 +568,12 @@ static int validate_common(const tkv_decode_args* a) {
   if ((int64_t)a->split_size * (a->num_splits - 1) >= a->S) return TKV_EINVAL;  // empty split
   if ((int64_t)a->split_size * a->num_splits < a->S) return TKV_EINVAL;        // uncovered
   if (a->num_splits > 1 && (!a->acc || !a->maxs || !a->sums)) return TKV_EINVAL;
+  // Vector loads: caches 16-byte aligned, metadata 4-byte, partials 8-byte.
+  if (((uintptr_t)a->k | (uintptr_t)a->v) & 15) return TKV_EINVAL;
+  if (((uintptr_t)a->k_scale | (uintptr_t)a->k_zero | (uintptr_t)a->v_scale |
+       (uintptr_t)a->v_zero | (uintptr_t)a->q) & 3)
+    return TKV_EINVAL;
+  if (((uintptr_t)a->acc | (uintptr_t)a->out) & 7) return TKV_EINVAL;
   if (a->D != 64 && a->D != 128) return TKV_EUNSUPPORTED;
   return TKV_OK;
 }
@@ -711,6 +717,7 @@ extern "C" int tkv_combine_splits(const float* acc, const float* maxs, const flo
                                   int32_t D, tkv_stream_t stream) {
   using namespace tkv;
   if (!acc || !maxs || !sums || !out || B <= 0 || HQ <= 0 || num_splits <= 0) return TKV_EINVAL;
+  if (((uintptr_t)acc | (uintptr_t)out) & 7) return TKV_EINVAL;
   if (D <= 0 || D > 128 || (D & 1)) return TKV_EUNSUPPORTED;
   (void)hipGetLastError();
   launch_combine(acc, maxs, sums, out, B, HQ, num_splits, D, reinterpret_cast<hipStream_t>(stream));

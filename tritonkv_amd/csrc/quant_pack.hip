@@ -277,6 +277,8 @@ extern "C" int tkv_quantize_pack(const void* x, int32_t x_is_fp32, int32_t B, in
   if (nbits != 2 && nbits != 4) return TKV_EINVAL;
   if (group_size <= 0 || D % group_size) return TKV_EINVAL;
   if (!positions && N > S_cap) return TKV_EINVAL;
+  if (((uintptr_t)packed & 3) || ((uintptr_t)scale & 1) || ((uintptr_t)zero & 1)) return TKV_EINVAL;
+  if ((uintptr_t)x & (x_is_fp32 ? 3 : 1)) return TKV_EINVAL;
   const int64_t rows = (int64_t)B * HKV * N;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   (void)hipGetLastError();
@@ -295,6 +297,7 @@ extern "C" int tkv_pack_codes(const uint8_t* codes, int64_t rows, int32_t D, int
   if (nbits != 2 && nbits != 4) return TKV_EINVAL;
   const int P = 8 / nbits;
   if (D % (4 * P)) return TKV_EUNSUPPORTED;  // whole packed dwords per row
+  if ((uintptr_t)packed & 3) return TKV_EINVAL;
   const int64_t n = rows * (D / P / 4);
   (void)hipGetLastError();
   pack_codes_kernel<<<dim3((unsigned)((n + 255) / 256)), 256, 0,
@@ -313,6 +316,7 @@ extern "C" int tkv_unpack_dequant(const uint8_t* packed, const uint16_t* scale,
   if (group_size <= 0 || D % group_size) return TKV_EINVAL;
   if (path != 0 && path != 1) return TKV_EINVAL;
   if (values_out && (!scale || !zero)) return TKV_EINVAL;
+  if ((uintptr_t)packed & 7) return TKV_EINVAL;  // dwordx2 loads of the K unpack path
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   (void)hipGetLastError();
 #define TKV_U(Dv, NBv, GSv) \
