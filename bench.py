@@ -1,0 +1,413 @@
+#!/usr/bin/env python
+"""Decode-step benchmark of the MI355X fused quantized-KV attention.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+
+Headline workload (``config.workload``): BASELINE.json config 4, the
+Llama-3-8B attention shape -- B=32, HQ=32, HKV=8, D=128, ctx 32768, fp16 q,
+K/V N(0,1) with 4 seeded x8 outlier channels per KV head, 4-bit group-size-32
+split-P caches.  One step = one decode step over the whole batch (split kernel
++ combine).  Two independently seeded cache copies (1.34 GB each, together
+more than 10x the 256 MB Infinity Cache) alternate step by step, so every step
+streams its cache from HBM ("cold cache").  Inputs are resident in HBM before
+the timed region starts.
+
+Prints ONE JSON line.  ``value`` is microseconds per decode step (lower is
+better), measured with HIP events on torch's current stream around the replay
+of a HIP graph holding exactly K steps, after W untimed warmup steps.
+``roofline`` relates the split kernel's algorithmic bytes (cache + q + out)
+to its own average duration (a graph of split-kernel launches only) and
+MI355X's 8 TB/s HBM peak.  ``cpu_baseline`` times the oracle's scalar C
+restatement of the reference's CPU path on a bounded sample of the same step.
+Unless ``--quick``, the line also carries the 2-bit and fp16-control numbers of
+the same shape and the Qwen2.5-1.5B table of BASELINE.json configs 2-3
+(cache-resident and DRAM-resident, ctx 512..16384).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "µs/decode step + achieved HBM GB/s (% peak), 4/2-bit vs fp16 control, cold cache"
+HBM_PEAK_GBS = 8000.0
+INFINITY_CACHE = 256 * 2 ** 20
+
+
+def _args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--quick", action="store_true",
+                    help="headline workload only (no 2-bit / control / Qwen table / CPU baseline)")
+    ap.add_argument("--num-splits", type=int, default=None)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=8.0)
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------------------
+# workload construction
+# ---------------------------------------------------------------------------
+
+
+def algorithmic_bytes(B, HQ, HKV, S, D, kbits, vbits, gs):
+    """Cache bytes + q (fp16) + out (fp32) of one decode step."""
+    from oracle.quant import row_bytes  # pure arithmetic on sizes; same formula as the docs
+
+    cache = B * HKV * S * (row_bytes(D, kbits, gs) + row_bytes(D, vbits, gs))
+    return cache, cache + B * HQ * D * (2 + 4)
+
+
+def llama_inputs(seed, B=32, HQ=32, HKV=8, S=32768, D=128, n_out=4, scale=8.0):
+    import torch
+
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    q = torch.randn(B, HQ, D, device="cuda", generator=g, dtype=torch.float16)
+    chans = torch.stack([torch.randperm(D, device="cuda", generator=g)[:n_out] for _ in range(HKV)])
+    mult = torch.ones(HKV, D, device="cuda", dtype=torch.float16)
+    mult.scatter_(1, chans, scale)
+    k = torch.randn(B, HKV, S, D, device="cuda", generator=g, dtype=torch.float16)
+    k.mul_(mult[None, :, None, :])
+    v = torch.randn(B, HKV, S, D, device="cuda", generator=g, dtype=torch.float16)
+    v.mul_(mult[None, :, None, :])
+    return q, k, v
+
+
+# ---------------------------------------------------------------------------
+# timing
+# ---------------------------------------------------------------------------
+
+
+def capture(calls):
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        calls[0]()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for f in calls:
+            f()
+    torch.cuda.synchronize()
+    return g
+
+
+def timed_steps(copies, steps, warmup, reps=3):
+    """µs per step of ``steps`` rotating calls in one graph (best of ``reps`` replays)
+    plus the wall-clock ms per step of the first timed replay."""
+    import torch
+
+    for i in range(warmup):
+        copies[i % len(copies)]()
+    torch.cuda.synchronize()
+    g = capture([copies[i % len(copies)] for i in range(steps)])
+    g.replay()  # untimed: graph upload
+    torch.cuda.synchronize()
+    us, walls = [], []
+    for _ in range(reps):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        s.record()
+        g.replay()
+        e.record()
+        torch.cuda.synchronize()
+        walls.append((time.perf_counter() - t0) * 1e3 / steps)
+        us.append(s.elapsed_time(e) * 1e3 / steps)
+    del g
+    return min(us), walls[0], us
+
+
+def per_call_us(calls, reps=5):
+    """Median µs per call of a graph that makes each call once (rotating caches)."""
+    import torch
+
+    g = capture(list(calls))
+    for _ in range(2):
+        g.replay()
+    torch.cuda.synchronize()
+    out = []
+    for _ in range(reps):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        g.replay()
+        e.record()
+        torch.cuda.synchronize()
+        out.append(s.elapsed_time(e) * 1e3 / len(calls))
+    del g
+    return statistics.median(out)
+
+
+# ---------------------------------------------------------------------------
+# callables
+# ---------------------------------------------------------------------------
+
+
+def fused_call(q, kq, vq, num_splits=None, split_only=False):
+    import torch
+
+    from tritonkv_amd import _lib
+    from tritonkv_amd.kernels.fused_decode_attn import _workspace_for, plan_splits
+
+    B, HQ, D = q.shape
+    _, HKV, S, _ = kq.packed.shape
+    _, ns, size = plan_splits(S, 64, num_splits, B, HKV, HQ // HKV)
+    out = torch.empty(B, HQ, D, device=q.device)
+    acc, mx, sm = _workspace_for({}, B, HQ, ns, D, q.device)
+    args = _lib.DecodeArgs(
+        q=q.data_ptr(), k=kq.packed.data_ptr(), k_scale=kq.scale.data_ptr(),
+        k_zero=kq.zero.data_ptr(), v=vq.packed.data_ptr(), v_scale=vq.scale.data_ptr(),
+        v_zero=vq.zero.data_ptr(), acc=_lib.ptr(acc), maxs=_lib.ptr(mx), sums=_lib.ptr(sm),
+        out=out.data_ptr(), B=B, HQ=HQ, HKV=HKV, S=S, D=D, k_nbits=kq.nbits, v_nbits=vq.nbits,
+        group_size=kq.group_size, sm_scale=D ** -0.5, split_size=size, num_splits=ns)
+    lib = _lib.load()
+    fn = lib.tkv_fused_decode_split if split_only else lib.tkv_fused_decode_attention
+
+    def call():
+        _lib.check(fn(args, torch.cuda.current_stream().cuda_stream), "fused")
+    call.keep = (out, acc, mx, sm, q, kq, vq)
+    call.num_splits = ns
+    return call
+
+
+def fp16_call(q, k, v, num_splits=None, split_only=False):
+    import torch
+
+    from tritonkv_amd import _lib
+    from tritonkv_amd.kernels.fused_decode_attn import _workspace_for, plan_splits
+
+    B, HQ, D = q.shape
+    _, HKV, S, _ = k.shape
+    _, ns, size = plan_splits(S, 64, num_splits, B, HKV, HQ // HKV)
+    out = torch.empty(B, HQ, D, device=q.device)
+    acc, mx, sm = _workspace_for({}, B, HQ, ns, D, q.device)
+    args = _lib.DecodeArgs(
+        q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(), acc=_lib.ptr(acc), maxs=_lib.ptr(mx),
+        sums=_lib.ptr(sm), out=out.data_ptr(), B=B, HQ=HQ, HKV=HKV, S=S, D=D, k_nbits=16,
+        v_nbits=16, group_size=D, sm_scale=D ** -0.5, split_size=size, num_splits=ns)
+    lib = _lib.load()
+    fn = lib.tkv_fp16_decode_split if split_only else lib.tkv_fp16_decode_attention
+
+    def call():
+        _lib.check(fn(args, torch.cuda.current_stream().cuda_stream), "fp16")
+    call.keep = (out, acc, mx, sm, q, k, v)
+    call.num_splits = ns
+    return call
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the oracle's scalar C restatement on a bounded sample
+# ---------------------------------------------------------------------------
+
+
+def cpu_baseline(q, kq, vq, budget_s):
+    import numpy as np
+
+    from oracle import c_oracle
+
+    B, HQ, D = q.shape
+    _, HKV, S, _ = kq.packed.shape
+    G = HQ // HKV
+    units_total = B * HKV
+    done, t_spent = 0, 0.0
+    b = 0
+    while b < B and t_spent < budget_s:
+        qb = q[b:b + 1].float().cpu().numpy()
+        host = [t[b:b + 1].cpu().numpy() for t in (kq.packed, kq.scale, kq.zero,
+                                                   vq.packed, vq.scale, vq.zero)]
+        for h in range(HKV):
+            sub = [a[:, h:h + 1] for a in host]
+            qh = np.ascontiguousarray(qb[:, h * G:(h + 1) * G])
+            t0 = time.perf_counter()
+            c_oracle.quantized_decode_attention(
+                qh, (sub[0], sub[1], sub[2], kq.nbits, kq.group_size),
+                (sub[3], sub[4], sub[5], vq.nbits, vq.group_size), D ** -0.5)
+            t_spent += time.perf_counter() - t0
+            done += 1
+            if t_spent >= budget_s:
+                break
+        b += 1
+    us_step = t_spent / done * units_total * 1e6
+    return {"value": round(us_step, 1), "unit": "us/decode step", "cores": 1, "kind": "port",
+            "sample": (f"oracle/tkv_oracle.c (scalar C, 1 thread): dequantize K,V to fp32 + fp32 "
+                       f"attention for {done} of the {units_total} (batch row, kv head) units of "
+                       f"one decode step ({t_spent:.1f} s), extrapolated x{units_total / done:.1f}")}
+
+
+# ---------------------------------------------------------------------------
+# Qwen2.5-1.5B table (BASELINE.json configs 2 and 3)
+# ---------------------------------------------------------------------------
+
+
+def qwen_table(ctxs=(512, 2048, 8192, 16384)):
+    import torch
+
+    from tritonkv_amd.quantize import QuantizedTensor, quantize_groupwise
+    from tritonkv_amd.timing import replicas_for
+
+    B, HQ, HKV, D, gs = 1, 12, 2, 128, 32
+    rows = []
+    for S in ctxs:
+        g = torch.Generator(device="cuda").manual_seed(1000 + S)
+        q = torch.randn(B, HQ, D, device="cuda", generator=g, dtype=torch.float16)
+        for method in ("fused4", "fused2", "fp16"):
+            nbits = {"fused4": 4, "fused2": 2, "fp16": 16}[method]
+            cache, step_bytes = algorithmic_bytes(B, HQ, HKV, S, D, nbits, nbits, gs)
+            R = replicas_for(cache)
+            kv = torch.randn(2, R, B, HKV, S, D, device="cuda", generator=g, dtype=torch.float16)
+            calls = []
+            if method == "fp16":
+                for i in range(R):
+                    calls.append(fp16_call(q, kv[0, i], kv[1, i]))
+            else:
+                kq = quantize_groupwise(kv[0], nbits, gs)
+                vq = quantize_groupwise(kv[1], nbits, gs)
+                del kv
+                for i in range(R):
+                    ki = QuantizedTensor(kq.packed[i], kq.scale[i], kq.zero[i], nbits, gs, D)
+                    vi = QuantizedTensor(vq.packed[i], vq.scale[i], vq.zero[i], nbits, gs, D)
+                    calls.append(fused_call(q, ki, vi))
+            hot = per_call_us([calls[0]] * 50)
+            cold = per_call_us(calls)
+            rows.append({"ctx": S, "method": method, "cache_bytes": cache, "replicas": R,
+                         "splits": calls[0].num_splits,
+                         "hot_us": round(hot, 3), "cold_us": round(cold, 3),
+                         "cold_gbps": round(step_bytes / cold / 1e3, 1),
+                         "cold_frac_of_hbm_peak": round(step_bytes / cold / 1e3 / HBM_PEAK_GBS, 4),
+                         "hot_effective_gbps": round(step_bytes / hot / 1e3, 1)})
+            print(f"# qwen ctx={S} {method}: hot {hot:.2f} us  cold {cold:.2f} us  (R={R})",
+                  file=sys.stderr, flush=True)
+            del calls
+            torch.cuda.empty_cache()
+    by = {(r["ctx"], r["method"]): r for r in rows}
+    effects = {str(S): {"quant_effect_cold_4b": round(by[(S, "fp16")]["cold_us"] / by[(S, "fused4")]["cold_us"], 3),
+                        "quant_effect_cold_2b": round(by[(S, "fp16")]["cold_us"] / by[(S, "fused2")]["cold_us"], 3),
+                        "quant_effect_hot_4b": round(by[(S, "fp16")]["hot_us"] / by[(S, "fused4")]["hot_us"], 3)}
+               for S in ctxs}
+    return {"rows": rows, "effects": effects}
+
+
+# ---------------------------------------------------------------------------
+
+
+def main() -> int:
+    a = _args()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU per box; the decode step shards "
+                          "by kv head with no communication (see DESIGN.md), and no figure at "
+                          f"{a.gpus} GPUs is produced"}))
+        return 2
+    import torch
+
+    from tritonkv_amd.kernels import triton_available
+    from tritonkv_amd.quantize import quantize_kv
+    from tritonkv_amd.timing import empty_kernel_floor
+
+    ok, why = triton_available()
+    if not ok:
+        print(json.dumps({"error": why}))
+        return 1
+    torch.backends.cuda.matmul.allow_tf32 = False
+    B, HQ, HKV, S, D, gs = 32, 32, 8, 32768, 128, 32
+    detail = {}
+
+    def build_copies(nbits):
+        out = []
+        for c in range(2):
+            q, k, v = llama_inputs(seed=10 + c)
+            if nbits == 16:
+                out.append((q, k, v))
+            else:
+                kq, vq = quantize_kv(k, v, nbits, gs)
+                del k, v
+                out.append((q, kq, vq))
+        torch.cuda.synchronize()
+        return out
+
+    # ---- headline: 4-bit --------------------------------------------------
+    copies4 = build_copies(4)
+    cache4, bytes4 = algorithmic_bytes(B, HQ, HKV, S, D, 4, 4, gs)
+    steps4 = [fused_call(*c, num_splits=a.num_splits) for c in copies4]
+    us4, wall4, samples4 = timed_steps(steps4, a.steps, a.warmup)
+    split4 = [fused_call(*c, num_splits=a.num_splits, split_only=True) for c in copies4]
+    split_us4, _, _ = timed_steps(split4, a.steps, 2)
+    achieved = bytes4 / split_us4 / 1e3
+    print(f"# llama 4-bit: step {us4:.2f} us, split kernel {split_us4:.2f} us, "
+          f"{achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%} of 8 TB/s), "
+          f"splits={steps4[0].num_splits}", file=sys.stderr, flush=True)
+    detail["fused4"] = {"us_per_step": round(us4, 2), "split_kernel_us": round(split_us4, 2),
+                        "cache_bytes": cache4, "algorithmic_bytes": bytes4,
+                        "gbps_step": round(bytes4 / us4 / 1e3, 1),
+                        "num_splits": steps4[0].num_splits}
+    cpu = None
+    if not a.quick and not a.no_cpu_baseline:
+        q0, kq0, vq0 = copies4[0]
+        cpu = cpu_baseline(q0, kq0, vq0, a.cpu_seconds)
+    del steps4, split4, copies4
+    torch.cuda.empty_cache()
+
+    if not a.quick:
+        for nbits, name in ((2, "fused2"), (16, "fp16")):
+            cps = build_copies(nbits)
+            cache, nbytes = algorithmic_bytes(B, HQ, HKV, S, D, nbits, nbits, gs)
+            mk = fp16_call if nbits == 16 else fused_call
+            us, _, _ = timed_steps([mk(*c) for c in cps], a.steps, a.warmup)
+            sp, _, _ = timed_steps([mk(*c, split_only=True) for c in cps], a.steps, 2)
+            detail[name] = {"us_per_step": round(us, 2), "split_kernel_us": round(sp, 2),
+                            "cache_bytes": cache, "algorithmic_bytes": nbytes,
+                            "gbps_split_kernel": round(nbytes / sp / 1e3, 1),
+                            "frac_of_hbm_peak": round(nbytes / sp / 1e3 / HBM_PEAK_GBS, 4)}
+            print(f"# llama {name}: step {us:.2f} us, split {sp:.2f} us", file=sys.stderr, flush=True)
+            del cps
+            torch.cuda.empty_cache()
+        detail["quant_effect_4b"] = round(detail["fp16"]["us_per_step"] / us4, 3)
+        detail["quant_effect_2b"] = round(detail["fp16"]["us_per_step"] / detail["fused2"]["us_per_step"], 3)
+        detail["empty_graph_node_us"] = round(empty_kernel_floor() * 1e3, 2)
+        detail["qwen2.5-1.5b"] = qwen_table()
+
+    line = {
+        "metric": METRIC,
+        "value": round(us4, 2),
+        "unit": "us/decode step",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(wall4, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4 codes x fp16 q (fp16 MFMA, fp32 accumulate)",
+        "data": "synthetic: seeded N(0,1) fp16 q/K/V, 4 x8 outlier channels per KV head",
+        "config": {"workload": "llama-3-8b attention decode step, B=32 HQ=32 HKV=8 D=128 ctx=32768, "
+                               "4-bit gs32 split-P K/V, DRAM-resident (2 rotating cache copies)",
+                   "batch": B, "ctx": S, "q_heads": HQ, "kv_heads": HKV, "head_dim": D,
+                   "nbits": 4, "group_size": gs, "cache_bytes_per_step": cache4,
+                   "parallelism": "single GPU (flash-decoding splits x kv heads)"},
+        "gbps": round(bytes4 / us4 / 1e3, 1),
+        "hbm_frac": round(bytes4 / us4 / 1e3 / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "quant_split_kernel<128,4,4,32,4>",
+                     "kernel_us": round(split_us4, 2)},
+        "cpu_baseline": cpu,
+        "detail": detail,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -9,7 +9,11 @@ Each ``.hip`` source is compiled to an object in parallel, then linked into
 * ``-O3`` without fast-math: the quantizer needs IEEE binary32 division and
   ``rintf`` for bit-exact parity with the reference;
 * ``-Xclang -target-feature -Xclang -packed-fp32-ops`` keeps the compiler from
-  emitting packed-fp32 VALU instructions.
+  emitting packed-fp32 VALU instructions;
+* ``-mllvm -amdgpu-mfma-vgpr-form`` keeps MFMA accumulators in the unified
+  VGPR file: without it the decode loop shuttled every accumulator through
+  AGPRs around each MFMA (~100 extra moves per 32-token chunk) and serialised
+  the per-group score MFMAs through one AGPR quad.
 """
 
 from __future__ import annotations
@@ -43,6 +47,7 @@ def _flags() -> list[str]:
         "-std=c++17",
         "-fPIC",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-mllvm", "-amdgpu-mfma-vgpr-form",
         "-I", os.path.join(ROOT, "include"),
         "-Wno-unused-result",
     ]

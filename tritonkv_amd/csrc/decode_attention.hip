@@ -517,41 +517,59 @@ fp16_split_kernel(SplitParams prm) {
 
 // ===========================================================================
 // Combine: out[b,h,:] = sum_s 2^(m_s - m*) acc_s / sum_s 2^(m_s - m*) l_s.
-// One wave per (b, h); splits visited in order, as _combine_splits does.
-// Empty splits (m_s = -inf, only possible with per-row lengths) are skipped.
+// One 256-thread workgroup per (b, h).  Thread (sg, dq) owns float4 column dq
+// of the splits s = sg, sg + SG, ...: it streams them with an online
+// log-sum-exp merge (all loads of an iteration are independent of the
+// previous one, so they stay in flight together), then the SG split groups
+// are merged through LDS.  Empty splits (m_s = -inf, only possible with
+// per-row lengths) contribute nothing.
 // ===========================================================================
-__global__ void __launch_bounds__(64) combine_kernel(const float* __restrict__ acc,
-                                                     const float* __restrict__ maxs,
-                                                     const float* __restrict__ sums,
-                                                     float* __restrict__ out, int ns, int D) {
+template <int D>
+__global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ acc,
+                                                      const float* __restrict__ maxs,
+                                                      const float* __restrict__ sums,
+                                                      float* __restrict__ out, int ns) {
+  constexpr int DQ = D / 4;     // float4 columns of a split row
+  constexpr int SG = 256 / DQ;  // split groups
+  __shared__ float sm_m[SG], sm_l[SG];
+  __shared__ f4 sm_a[SG][DQ];
   const int64_t row = blockIdx.x;
-  const int lane = threadIdx.x;
-  const float* mrow = maxs + row * ns;
-  const float* lrow = sums + row * ns;
-  const float* arow = acc + row * ns * D;
-  float mg = -INFINITY, lg = 0.0f;
-  float a0 = 0.0f, a1 = 0.0f;
-  const int d0 = 2 * lane;
-  const bool act = d0 < D;
-  for (int s = 0; s < ns; ++s) {
-    const float ms = mrow[s];
+  const int t = threadIdx.x, dq = t % DQ, sg = t / DQ;
+  float m = -INFINITY, l = 0.0f;
+  f4 a = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+  for (int s = sg; s < ns; s += SG) {
+    const int64_t ps = row * ns + s;
+    const float ms = maxs[ps];
+    const float ls = sums[ps];
+    const f4 as = reinterpret_cast<const f4*>(acc + ps * D)[dq];
     if (ms == -INFINITY) continue;
-    const float mn = fmaxf(mg, ms);
-    const float al = safe_exp2_diff(mg, mn);
+    const float mn = fmaxf(m, ms);
+    const float al = safe_exp2_diff(m, mn);
     const float be = __builtin_amdgcn_exp2f(ms - mn);
-    if (act) {
-      const float2 v = *reinterpret_cast<const float2*>(arow + (int64_t)s * D + d0);
-      a0 = a0 * al + v.x * be;
-      a1 = a1 * al + v.y * be;
-    }
-    lg = lg * al + lrow[s] * be;
-    mg = mn;
+    a = a * al + as * be;
+    l = l * al + ls * be;
+    m = mn;
   }
-  if (act) {
-    float2 o;
-    o.x = a0 / lg;
-    o.y = a1 / lg;
-    *reinterpret_cast<float2*>(out + row * D + d0) = o;
+  if (dq == 0) {
+    sm_m[sg] = m;
+    sm_l[sg] = l;
+  }
+  sm_a[sg][dq] = a;
+  __syncthreads();
+  if (sg == 0) {
+    float mstar = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < SG; ++g) mstar = fmaxf(mstar, sm_m[g]);
+    f4 o = f4{0.f, 0.f, 0.f, 0.f};
+    float lt = 0.0f;
+#pragma unroll
+    for (int g = 0; g < SG; ++g) {
+      const float f = safe_exp2_diff(sm_m[g], mstar);
+      o += sm_a[g][dq] * f;
+      lt += sm_l[g] * f;
+    }
+    reinterpret_cast<f4*>(out + row * D)[dq] = o / lt;
   }
 }
 
@@ -573,7 +591,7 @@ static int validate_common(const tkv_decode_args* a) {
   if (((uintptr_t)a->k_scale | (uintptr_t)a->k_zero | (uintptr_t)a->v_scale |
        (uintptr_t)a->v_zero | (uintptr_t)a->q) & 3)
     return TKV_EINVAL;
-  if (((uintptr_t)a->acc | (uintptr_t)a->out) & 7) return TKV_EINVAL;
+  if (((uintptr_t)a->acc | (uintptr_t)a->out) & 15) return TKV_EINVAL;  // float4 rows
   if (a->D != 64 && a->D != 128) return TKV_EUNSUPPORTED;
   return TKV_OK;
 }
@@ -640,7 +658,13 @@ static int dispatch_bits(const SplitParams& p, dim3 grid, int knb, int vnb, int 
 
 static int launch_combine(const float* acc, const float* maxs, const float* sums, float* out,
                           int B, int HQ, int ns, int D, hipStream_t st) {
-  combine_kernel<<<dim3((unsigned)(B * HQ)), dim3(64), 0, st>>>(acc, maxs, sums, out, ns, D);
+  const dim3 grid((unsigned)(B * HQ));
+  if (D == 128)
+    combine_kernel<128><<<grid, dim3(256), 0, st>>>(acc, maxs, sums, out, ns);
+  else if (D == 64)
+    combine_kernel<64><<<grid, dim3(256), 0, st>>>(acc, maxs, sums, out, ns);
+  else
+    return TKV_EUNSUPPORTED;
   return TKV_OK;
 }
 
@@ -717,8 +741,8 @@ extern "C" int tkv_combine_splits(const float* acc, const float* maxs, const flo
                                   int32_t D, tkv_stream_t stream) {
   using namespace tkv;
   if (!acc || !maxs || !sums || !out || B <= 0 || HQ <= 0 || num_splits <= 0) return TKV_EINVAL;
-  if (((uintptr_t)acc | (uintptr_t)out) & 7) return TKV_EINVAL;
-  if (D <= 0 || D > 128 || (D & 1)) return TKV_EUNSUPPORTED;
+  if (((uintptr_t)acc | (uintptr_t)out) & 15) return TKV_EINVAL;
+  if (D != 64 && D != 128) return TKV_EUNSUPPORTED;
   (void)hipGetLastError();
   launch_combine(acc, maxs, sums, out, B, HQ, num_splits, D, reinterpret_cast<hipStream_t>(stream));
   return status_of_launch();
