@@ -27,6 +27,8 @@
 //   * Per-token scale/zero rows of each chunk are staged in LDS by one
 //     coalesced load per lane; the partial (m, l, acc) of the NW waves is
 //     merged in LDS and written once per workgroup.
+#include <type_traits>
+
 #include "tkv_codec.h"
 #include "../../include/tkv.h"
 
@@ -144,72 +146,110 @@ __device__ void merge_and_store(const SplitParams& prm, MergeLds<D, NW>& lds, in
   }
 }
 
-// ---------------------------------------------------------------------------
-// Per-wave LDS staging of the chunk's scale/zero rows: 4 tensors (K scale,
-// K zero, V scale, V zero) x 32 tokens x NG fp16, one coalesced load per lane
-// and tensor.  Token rows past the split end are clamped to its last token
-// (their scores are masked, but their metadata must stay finite).
-// ---------------------------------------------------------------------------
-template <int NG>
-struct MetaLds {
-  uint32_t t[4][kChunk * NG / 2 > 0 ? kChunk * NG / 2 : 1];
-};
-
-template <int NG>
-__device__ __forceinline__ void stage_meta(MetaLds<NG>& ml, const uint16_t* const (&src)[4],
-                                           int64_t row0, int cb, int hi, int lane) {
-  if constexpr (NG >= 2) {
-    constexpr int DW = NG / 2;  // dwords per token row
-#pragma unroll
-    for (int idx = lane; idx < kChunk * DW; idx += 64) {
-      const int tok = idx / DW, dw = idx % DW;
-      const int row = min(cb + tok, hi - 1);
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-        ml.t[t][idx] = reinterpret_cast<const uint32_t*>(src[t] + (row0 + row) * NG)[dw];
-    }
-  } else {
-    uint16_t* h = reinterpret_cast<uint16_t*>(&ml.t[0][0]);
-    if (lane < kChunk) {
-      const int row = min(cb + lane, hi - 1);
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-        reinterpret_cast<uint16_t*>(&ml.t[t][0])[lane] = src[t][row0 + row];
-    }
-    (void)h;
-  }
-}
-
-// fp16 value of group g of token `tok` in tensor t.
-template <int NG>
-__device__ __forceinline__ float meta_val(const MetaLds<NG>& ml, int t, int tok, int g) {
-  const uint16_t bits = reinterpret_cast<const uint16_t*>(&ml.t[t][0])[tok * NG + g];
-  return (float)__builtin_bit_cast(_Float16, bits);
-}
-// fp16 pair (token tok, group g) and (token tok+1, group g) of tensor t.
-template <int NG>
-__device__ __forceinline__ uint32_t meta_pair(const MetaLds<NG>& ml, int t, int tok, int g) {
-  const uint16_t* h = reinterpret_cast<const uint16_t*>(&ml.t[t][0]);
-  return (uint32_t)h[tok * NG + g] | ((uint32_t)h[(tok + 1) * NG + g] << 16);
-}
-
 __device__ __forceinline__ void wave_lds_fence() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+__device__ __forceinline__ u2 lds_u2(const uint16_t* p) { return *reinterpret_cast<const u2*>(p); }
+
+// ---------------------------------------------------------------------------
+// Per-wave LDS staging of a chunk's fp16 scale/zero metadata.
+//
+// Four tensors per chunk (K scale, K zero, V scale, V zero), each 32 tokens x
+// NG groups.  Every lane loads its dwords of each tensor one chunk ahead, into
+// registers, and writes them at the start of the chunk's compute in the layout
+// its consumer reads with one ds_read_b64:
+//   ks [g][tok]   K scale, transposed -- the fold reads 4 consecutive tokens of a group
+//   kz [tok][g]   K zero, token rows  -- A operand (token rows) of the K zero MFMA
+//   vs [g][tok]   V scale, transposed -- P'_g = P * s_g pairs of consecutive tokens
+//   vz [16][tok]  V zero, transposed, rows g >= NG zero -- A operand of the V zero MFMA
+// ---------------------------------------------------------------------------
+template <int NG>
+struct MetaLds {
+  uint16_t ks[NG][kChunk];
+  uint16_t kz[kChunk][NG < 2 ? 2 : NG];
+  uint16_t vs[NG][kChunk];
+  uint16_t vz[16][kChunk];
+};
+
+template <int NG>
+struct MetaStage {
+  // dwords of one tensor a lane carries: 16*NG dwords over 64 lanes (NG >= 2),
+  // or one fp16 for lanes < 32 (NG == 1).
+  static constexpr int NDW = NG >= 2 ? (kChunk * NG / 2 + 63) / 64 : 1;
+  static constexpr int DW = NG >= 2 ? NG / 2 : 1;  // dwords per token row
+  __device__ static bool active(int lane, int k) {
+    return NG >= 2 ? (lane + 64 * k) < kChunk * DW : lane < kChunk;
+  }
+  __device__ static int token(int lane, int k) { return NG >= 2 ? (lane + 64 * k) / DW : lane; }
+  __device__ static int group0(int lane, int k) { return NG >= 2 ? 2 * ((lane + 64 * k) % DW) : 0; }
+};
+
+// Load one chunk's metadata dwords of the 4 tensors through their buffer
+// resources (one per tensor, covering this (b, kv head) block).  A chunk's
+// rows are contiguous, so lane l reads dword l (+64k) of the chunk; rows past
+// the block end read as 0.
+template <int NG>
+__device__ __forceinline__ void load_meta(uint32_t (&mr)[4][MetaStage<NG>::NDW],
+                                          const rsrc_t (&rm)[4], int cb, int lane) {
+  using MS = MetaStage<NG>;
+#pragma unroll
+  for (int k = 0; k < MS::NDW; ++k) {
+    if (!MS::active(lane, k)) continue;
+    const uint32_t off = NG >= 2 ? (uint32_t)(cb * NG * 2 + 4 * (lane + 64 * k))
+                                 : (uint32_t)((cb + lane) * 2);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) mr[t][k] = NG >= 2 ? buf_u32(rm[t], off) : buf_u16(rm[t], off);
+  }
+}
+
+template <int NG>
+__device__ __forceinline__ void write_meta(MetaLds<NG>& ml, const uint32_t (&mr)[4][MetaStage<NG>::NDW],
+                                           int lane) {
+  using MS = MetaStage<NG>;
+#pragma unroll
+  for (int k = 0; k < MS::NDW; ++k) {
+    if (!MS::active(lane, k)) continue;
+    const int tok = MS::token(lane, k), g = MS::group0(lane, k);
+    ml.ks[g][tok] = (uint16_t)mr[0][k];
+    ml.vs[g][tok] = (uint16_t)mr[2][k];
+    ml.vz[g][tok] = (uint16_t)mr[3][k];
+    if constexpr (NG >= 2) {
+      ml.ks[g + 1][tok] = (uint16_t)(mr[0][k] >> 16);
+      ml.vs[g + 1][tok] = (uint16_t)(mr[2][k] >> 16);
+      ml.vz[g + 1][tok] = (uint16_t)(mr[3][k] >> 16);
+      *reinterpret_cast<uint32_t*>(&ml.kz[tok][g]) = mr[1][k];
+    } else {
+      ml.kz[tok][0] = (uint16_t)mr[1][k];
+    }
+  }
+}
+
 // ===========================================================================
 // Fused quantized split kernel.
 // ===========================================================================
+template <int D, int KNB, int VNB, int GS>
+struct QuantTile {
+  using KL = KLayout<D, KNB, GS>;
+  using VL = VLayout<D, VNB, GS>;
+  using KX = typename std::conditional<KL::CB == 8, u2, uint32_t>::type;
+  KX kx[2][KL::NLOAD];
+  uint32_t vx[8][VL::NWIN];
+  uint32_t meta[4][MetaStage<D / GS>::NDW];
+};
+
 template <int D, int KNB, int VNB, int GS, int NW>
 __global__ void __launch_bounds__(NW * 64)
 quant_split_kernel(SplitParams prm) {
   using KL = KLayout<D, KNB, GS>;
   using VL = VLayout<D, VNB, GS>;
+  using Tile = QuantTile<D, KNB, VNB, GS>;
   constexpr int NG = D / GS;
   constexpr int NKM = KL::NKM;
   constexpr int NVM = VL::NVM;
+  static_assert(2 * NG <= 16, "zero-point MFMA holds hi/lo of at most 8 groups");
 
   __shared__ MergeLds<D, NW> mlds;
   __shared__ MetaLds<NG> meta[NW];
@@ -223,11 +263,62 @@ quant_split_kernel(SplitParams prm) {
   const int L = prm.seq_lens ? min(prm.seq_lens[b], prm.S) : prm.S;
   const int lo = split * prm.split_size;
   const int hi = min(lo + prm.split_size, L);
+  const int last = hi - 1;
 
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  // The wave index is wave-uniform; saying so lets every chunk address live in
+  // SGPRs and the loads use the scalar-base + lane-offset form.
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int r = lane & 15, j = lane >> 4;  // MFMA row/col index and lane-group
   const int n = r;                         // query head (column) of this lane
   const int64_t row0 = (int64_t)unit * prm.S;  // first cache row of this (b, kv head)
+  // Buffer resources over this (b, kv head) block: tokens >= S read as 0.
+  const rsrc_t rk = make_rsrc(prm.k + row0 * KL::DP, (uint32_t)prm.S * KL::DP);
+  const rsrc_t rv = make_rsrc(prm.v + row0 * VL::DP, (uint32_t)prm.S * VL::DP);
+  const rsrc_t rm[4] = {make_rsrc(prm.ks + row0 * NG, (uint32_t)prm.S * NG * 2),
+                        make_rsrc(prm.kz + row0 * NG, (uint32_t)prm.S * NG * 2),
+                        make_rsrc(prm.vs + row0 * NG, (uint32_t)prm.S * NG * 2),
+                        make_rsrc(prm.vz + row0 * NG, (uint32_t)prm.S * NG * 2)};
+  MetaLds<NG>& ml = meta[w];
+
+  // Lane parts of a chunk's K and V code offsets; the per-load remainder is a
+  // compile-time constant that folds into the instruction's offset field.
+  const uint32_t klane = r * KL::DP + KL::load_offset(0, j);  // + 16a*DP + L*KSTEP
+  const uint32_t vlane = 4 * j * VL::DP + 4 * (r / VL::LPD);
+
+  // A chunk's loads, in three parts so each can be reissued for the next chunk
+  // as soon as the current chunk has consumed the registers it fills.  Tail
+  // chunks need no clamping: rows past the split end are masked in the
+  // scores, rows past the block end read as 0.
+  auto load_k = [&](Tile& t, int cb) {
+    const uint32_t kb = klane + (uint32_t)cb * KL::DP;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int Lh = 0; Lh < KL::NLOAD; ++Lh) {
+        const uint32_t off = kb + 16 * a * KL::DP + (KL::load_offset(Lh, j) - KL::load_offset(0, j));
+        if constexpr (KL::CB == 8) t.kx[a][Lh] = buf_u2(rk, off);
+        else t.kx[a][Lh] = buf_u32(rk, off);
+      }
+  };
+  auto load_v = [&](Tile& t, int cb) {
+    const uint32_t vb = vlane + (uint32_t)cb * VL::DP;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int wi = 0; wi < VL::NWIN; ++wi)
+        t.vx[i][wi] = buf_u32(rv, vb + ((i < 4 ? 0 : 12) + i) * VL::DP + VL::W * wi);
+  };
+
+  Tile t;
+  const int cb0 = lo + kChunk * w;
+  if (cb0 < hi) {  // prologue loads overlap the Q^T setup below
+    load_meta<NG>(t.meta, rm, cb0, lane);
+    load_k(t, cb0);
+    load_v(t, cb0);
+  }
+
+  // zero rows g >= NG of this wave's transposed V zero tile (A operand rows)
+  for (int idx = lane; idx < (16 - NG) * kChunk; idx += 64) ml.vz[NG + idx / kChunk][idx % kChunk] = 0;
 
   // ---- Q^T operand in K slot order, pre-scaled by 2^-(slice*KNB) ---------
   u4 qf[NKM];
@@ -255,7 +346,27 @@ quant_split_kernel(SplitParams prm) {
       qf[m] = u4{wv[0], wv[1], wv[2], wv[3]};
     }
 #pragma unroll
-    for (int g = 0; g < NG; ++g) qz[g] = xor_sum16_32(qz[g]) * kTwoM24;
+    for (int g = 0; g < NG; ++g) qz[g] = xor_sum16_32(qz[g]);
+  }
+  // B operand of the K zero-point MFMA: k-slot k < NG holds fp16(Qz_k),
+  // NG <= k < 2NG the fp16 remainder Qz - fp16(Qz), so the product with the
+  // exact fp16 zero points keeps fp32 precision.
+  u2 qzb;
+  {
+    float hl[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = 4 * j + i;
+      float v = 0.0f;
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        const float hi16 = (float)(_Float16)qz[g];
+        if (k == g) v = hi16;
+        if (k == NG + g) v = qz[g] - hi16;
+      }
+      hl[i] = v;
+    }
+    qzb = u2{pack_h2(hl[0], hl[1]), pack_h2(hl[2], hl[3])};
   }
 
   // ---- per-lane constants of the V unpack -------------------------------
@@ -269,44 +380,23 @@ quant_split_kernel(SplitParams prm) {
   f4 accv[NVM];
 #pragma unroll
   for (int mv = 0; mv < NVM; ++mv) accv[mv] = f4{0.f, 0.f, 0.f, 0.f};
-  float ozp[NG];
-#pragma unroll
-  for (int g = 0; g < NG; ++g) ozp[g] = 0.0f;
+  f4 oz = f4{0.f, 0.f, 0.f, 0.f};  // sum_t z_V[t][g = 4j+i] P[t][n]
   float m_run = -INFINITY, l_run = 0.0f;
   const float lscale = prm.qk_scale * kTwo24;
 
-  const uint8_t* kbase = prm.k + row0 * KL::DP;
-  const uint8_t* vbase = prm.v + row0 * VL::DP;
-  const uint16_t* const msrc[4] = {prm.ks, prm.kz, prm.vs, prm.vz};
-  MetaLds<NG>& ml = meta[w];
-
-  for (int cb = lo + kChunk * w; cb < hi; cb += kChunk * NW) {
-    // ---- issue loads -------------------------------------------------------
-    wave_lds_fence();
-    stage_meta<NG>(ml, msrc, row0, cb, hi, lane);
-
-    typename std::conditional<KL::CB == 8, u2, uint32_t>::type kx[2][KL::NLOAD];
-#pragma unroll
-    for (int a = 0; a < 2; ++a) {
-      const int tr = min(cb + 16 * a + r, hi - 1);
-#pragma unroll
-      for (int Lh = 0; Lh < KL::NLOAD; ++Lh) {
-        const uint8_t* src = kbase + (int64_t)tr * KL::DP + KL::load_offset(Lh, j);
-        if constexpr (KL::CB == 8) kx[a][Lh] = ld_u2(src);
-        else kx[a][Lh] = ld_u32(src);
-      }
-    }
-    uint32_t vx[8][VL::NWIN];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int tr = min(cb + slot_token(j, i), hi - 1);
-#pragma unroll
-      for (int wi = 0; wi < VL::NWIN; ++wi)
-        vx[i][wi] = ld_u32(vbase + (int64_t)tr * VL::DP + VL::dword_offset(wi, r));
-    }
+  // One chunk: stage its metadata in LDS, then compute, reissuing each part
+  // of the next chunk's loads as soon as its registers are free.  The tail
+  // chunk (TAIL) masks the scores of tokens past the split end.
+  auto step = [&](Tile& cur, int cb, auto tail) {
+    constexpr bool TAIL = decltype(tail)::value;
+    const int cn = cb + kChunk * NW;
+    const bool more = !TAIL && cn < hi;
+    wave_lds_fence();  // previous chunk's LDS reads are done
+    write_meta<NG>(ml, cur.meta, lane);
+    if (more) load_meta<NG>(cur.meta, rm, cn, lane);
     wave_lds_fence();
 
-    // ---- scores S^T for the two 16-token tiles -----------------------------
+    // ---- scores S^T for the two 16-token tiles ---------------------------
     float x[8];
 #pragma unroll
     for (int a = 0; a < 2; ++a) {
@@ -317,45 +407,77 @@ quant_split_kernel(SplitParams prm) {
       for (int m = 0; m < NKM; ++m) {
         const int g = KL::group_of_step(m);
         if constexpr (KL::CB == 8)
-          c[g] = mfma_k32(k_extract8(kx[a][KL::load_of_step(m)], kmask[m]), qf[m], c[g]);
+          c[g] = mfma_k32(k_extract8(cur.kx[a][KL::load_of_step(m)], kmask[m]), qf[m], c[g]);
         else
-          c[g] = mfma_k16(k_extract4(kx[a][KL::load_of_step(m)], kmask[m]),
+          c[g] = mfma_k16(k_extract4(cur.kx[a][KL::load_of_step(m)], kmask[m]),
                           u2{qf[m][0], qf[m][1]}, c[g]);
       }
+      // zero-point part: sum_g z[t][g] Qz[g][n] (true units) by one MFMA
+      u2 za;
+      {
+        const uint16_t* zr = ml.kz[16 * a + r];
+        if constexpr (NG == 8) {
+          const u4 z8 = *reinterpret_cast<const u4*>(zr);
+          za = (j & 1) ? u2{z8[2], z8[3]} : u2{z8[0], z8[1]};
+        } else if constexpr (NG == 4) {
+          za = lds_u2(zr);
+        } else if constexpr (NG == 2) {
+          const uint32_t z2 = *reinterpret_cast<const uint32_t*>(zr);
+          za = u2{z2, z2};
+        } else {
+          const uint32_t z1 = zr[0];
+          za = u2{z1 | (z1 << 16), 0u};
+        }
+      }
+      const f4 yz = mfma_k16(za, qzb, f4{0.f, 0.f, 0.f, 0.f});
+      u2 sk[NG];
+#pragma unroll
+      for (int g = 0; g < NG; ++g) sk[g] = lds_u2(&ml.ks[g][16 * a + 4 * j]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int tok = 16 * a + 4 * j + i;
-        float sc = 0.0f;
+        float sc = yz[i] * kTwoM24;
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
-          sc = fmaf(meta_val<NG>(ml, 0, tok, g), c[g][i], sc);
-          sc = fmaf(meta_val<NG>(ml, 1, tok, g), qz[g], sc);
+          const float sv = (i & 1) ? half_hi(sk[g][i >> 1]) : half_lo(sk[g][i >> 1]);
+          sc = fmaf(sv, c[g][i], sc);
         }
-        x[4 * a + i] = (cb + tok < hi) ? sc : -INFINITY;
+        x[4 * a + i] = sc;
       }
     }
+    if constexpr (TAIL) {
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (cb + 16 * a + 4 * j + i > last) x[4 * a + i] = -INFINITY;
+    }
 
-    // ---- online softmax ----------------------------------------------------
+    if (more) load_k(cur, cn);
+
+    // ---- online softmax ---------------------------------------------------
     float alpha;
     ChunkProbs pr;
     if (softmax_chunk(x, lscale, m_run, l_run, alpha, pr)) {
 #pragma unroll
       for (int mv = 0; mv < NVM; ++mv) accv[mv] *= alpha;
-#pragma unroll
-      for (int g = 0; g < NG; ++g) ozp[g] *= alpha;
+      oz *= alpha;
     }
+    const u4 pb = u4{pr.ph[0], pr.ph[1], pr.ph[2], pr.ph[3]};
 
-    // ---- V: zero-point term and P'_g = P * s_g -----------------------------
+    // ---- V zero point: oz += Z^T P ------------------------------------------
+    {
+      const u2 z0 = lds_u2(&ml.vz[r][4 * j]);
+      const u2 z1 = lds_u2(&ml.vz[r][16 + 4 * j]);
+      oz = mfma_k32(u4{z0[0], z0[1], z1[0], z1[1]}, pb, oz);
+    }
+    // ---- P'_g = P * s_g ------------------------------------------------------
     u4 pg[NG];
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-      float oz = ozp[g];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) oz = fmaf(meta_val<NG>(ml, 3, slot_token(j, i), g), pr.p[i], oz);
-      ozp[g] = oz;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        pg[g][i] = pk_mul(pr.ph[i], meta_pair<NG>(ml, 2, slot_token(j, 2 * i), g));
+      const u2 s0 = lds_u2(&ml.vs[g][4 * j]);
+      const u2 s1 = lds_u2(&ml.vs[g][16 + 4 * j]);
+      pg[g] = u4{pk_mul(pb[0], s0[0]), pk_mul(pb[1], s0[1]), pk_mul(pb[2], s1[0]),
+                 pk_mul(pb[3], s1[1])};
     }
 
     // ---- O^T += V^T P'^T ---------------------------------------------------
@@ -365,7 +487,7 @@ quant_split_kernel(SplitParams prm) {
       for (int e = 0; e < VL::NE; ++e) {
         uint32_t pm[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) pm[i] = perm(vx[2 * i + 1][wi], vx[2 * i][wi], vsel[e]);
+        for (int i = 0; i < 4; ++i) pm[i] = perm(cur.vx[2 * i + 1][wi], cur.vx[2 * i][wi], vsel[e]);
 #pragma unroll
         for (int p = 0; p < VL::P; ++p) {
           const int mv = VL::mfma_index(p, wi, e);
@@ -375,20 +497,26 @@ quant_split_kernel(SplitParams prm) {
         }
       }
     }
-  }
+    if (more) load_v(cur, cn);
+  };
+
+  // Full chunks, then the split's partial last chunk (if any).
+  int cb = cb0;
+  for (; cb + kChunk <= hi; cb += kChunk * NW) step(t, cb, std::false_type{});
+  if (cb < hi) step(t, cb, std::true_type{});
 
   // ---- this wave's partial into LDS ---------------------------------------
   {
-    float ozt[NG];
-#pragma unroll
-    for (int g = 0; g < NG; ++g) ozt[g] = xor_sum16_32(ozp[g]);
     const float lt = xor_sum16_32(l_run);
+    float ozg[NG];  // Oz[g][n], held by lane-group g/4, element g%4
+#pragma unroll
+    for (int g = 0; g < NG; ++g) ozg[g] = __shfl(oz[g % 4], 16 * (g / 4) + n, 64);
 #pragma unroll
     for (int mv = 0; mv < NVM; ++mv) {
       const float fac = kTwo24 * __builtin_ldexpf(1.0f, -VL::slice_of(mv) * VNB);
-      const float oz = ozt[VL::group_of(mv)];
+      const float zv = ozg[VL::group_of(mv)];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) mlds.o[w][n][VL::dim_of(mv, 4 * j + i)] = fmaf(accv[mv][i], fac, oz);
+      for (int i = 0; i < 4; ++i) mlds.o[w][n][VL::dim_of(mv, 4 * j + i)] = fmaf(accv[mv][i], fac, zv);
     }
     if (j == 0) {
       mlds.m[w][n] = m_run;
@@ -403,11 +531,20 @@ quant_split_kernel(SplitParams prm) {
 // combine; K/V read as fp16 (kernels/fp16_decode_attn.py:16-22 -- the control
 // differs from the fused kernel only in how K/V are read).
 // ===========================================================================
+template <int D>
+struct Fp16Tile {
+  static constexpr int NKM = D / 32;
+  static constexpr int EPL = D / 16;
+  u4 kx[2][NKM];
+  uint32_t vx[8][EPL / 2];
+};
+
 template <int D, int NW>
 __global__ void __launch_bounds__(NW * 64)
 fp16_split_kernel(SplitParams prm) {
-  constexpr int NKM = D / 32;   // 16x16x32 steps over the head dim
-  constexpr int EPL = D / 16;   // V dims per lane (and V MFMAs)
+  using Tile = Fp16Tile<D>;
+  constexpr int NKM = Tile::NKM;  // 16x16x32 steps over the head dim
+  constexpr int EPL = Tile::EPL;  // V dims per lane (and V MFMAs)
   __shared__ MergeLds<D, NW> mlds;
 
   const int split = blockIdx.x;
@@ -419,11 +556,48 @@ fp16_split_kernel(SplitParams prm) {
   const int L = prm.seq_lens ? min(prm.seq_lens[b], prm.S) : prm.S;
   const int lo = split * prm.split_size;
   const int hi = min(lo + prm.split_size, L);
+  const int last = hi - 1;
 
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  // The wave index is wave-uniform; saying so lets every chunk address live in
+  // SGPRs and the loads use the scalar-base + lane-offset form.
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int r = lane & 15, j = lane >> 4;
   const int n = r;
   const int64_t row0 = (int64_t)unit * prm.S;
+  // Buffer resources over this (b, kv head) block: tokens >= S read as 0.
+  const rsrc_t rk = make_rsrc(reinterpret_cast<const _Float16*>(prm.k) + row0 * D, (uint32_t)prm.S * D * 2);
+  const rsrc_t rv = make_rsrc(reinterpret_cast<const _Float16*>(prm.v) + row0 * D, (uint32_t)prm.S * D * 2);
+  const uint32_t klane = (r * D + 8 * j) * 2;      // + (16a*D + 32m) * 2
+  const uint32_t vlane = (4 * j * D + EPL * r) * 2;  // + slot row * D * 2
+
+  auto load_k = [&](Tile& t, int cb) {
+    const uint32_t kb = klane + (uint32_t)cb * D * 2;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int m = 0; m < NKM; ++m) t.kx[a][m] = buf_u4(rk, kb + (16 * a * D + 32 * m) * 2);
+  };
+  auto load_v = [&](Tile& t, int cb) {
+    const uint32_t vb = vlane + (uint32_t)cb * D * 2;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t o = vb + ((i < 4 ? 0 : 12) + i) * D * 2;
+      if constexpr (EPL == 8) {
+        const u4 v4 = buf_u4(rv, o);
+        t.vx[i][0] = v4[0]; t.vx[i][1] = v4[1]; t.vx[i][2] = v4[2]; t.vx[i][3] = v4[3];
+      } else {
+        const u2 v2 = buf_u2(rv, o);
+        t.vx[i][0] = v2[0]; t.vx[i][1] = v2[1];
+      }
+    }
+  };
+
+  Tile t;
+  const int cb0 = lo + kChunk * w;
+  if (cb0 < hi) {
+    load_k(t, cb0);
+    load_v(t, cb0);
+  }
 
   u4 qf[NKM];
   {
@@ -450,40 +624,28 @@ fp16_split_kernel(SplitParams prm) {
   for (int mv = 0; mv < EPL; ++mv) accv[mv] = f4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.0f;
   const float lscale = prm.qk_scale;
-  const _Float16* kbase = reinterpret_cast<const _Float16*>(prm.k) + row0 * D;
-  const _Float16* vbase = reinterpret_cast<const _Float16*>(prm.v) + row0 * D;
 
-  for (int cb = lo + kChunk * w; cb < hi; cb += kChunk * NW) {
-    u4 kx[2][NKM];
-#pragma unroll
-    for (int a = 0; a < 2; ++a) {
-      const int tr = min(cb + 16 * a + r, hi - 1);
-#pragma unroll
-      for (int m = 0; m < NKM; ++m)
-        kx[a][m] = *reinterpret_cast<const u4*>(kbase + (int64_t)tr * D + 32 * m + 8 * j);
-    }
-    uint32_t vx[8][EPL / 2];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int tr = min(cb + slot_token(j, i), hi - 1);
-      const uint32_t* src = reinterpret_cast<const uint32_t*>(vbase + (int64_t)tr * D + EPL * r);
-#pragma unroll
-      for (int q = 0; q < EPL / 2; ++q) vx[i][q] = src[q];
-    }
-
+  auto step = [&](Tile& cur, int cb, auto tail) {
+    constexpr bool TAIL = decltype(tail)::value;
+    const int cn = cb + kChunk * NW;
+    const bool more = !TAIL && cn < hi;
     float x[8];
 #pragma unroll
     for (int a = 0; a < 2; ++a) {
       f4 c = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int m = 0; m < NKM; ++m) c = mfma_k32(kx[a][m], qf[m], c);
+      for (int m = 0; m < NKM; ++m) c = mfma_k32(cur.kx[a][m], qf[m], c);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tok = 16 * a + 4 * j + i;
-        x[4 * a + i] = (cb + tok < hi) ? c[i] : -INFINITY;
-      }
+      for (int i = 0; i < 4; ++i) x[4 * a + i] = c[i];
     }
-
+    if constexpr (TAIL) {
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (cb + 16 * a + 4 * j + i > last) x[4 * a + i] = -INFINITY;
+    }
+    if (more) load_k(cur, cn);
     float alpha;
     ChunkProbs pr;
     if (softmax_chunk(x, lscale, m_run, l_run, alpha, pr)) {
@@ -496,10 +658,16 @@ fp16_split_kernel(SplitParams prm) {
       const uint32_t sel = (mv & 1) ? 0x07060302u : 0x05040100u;
       u4 av;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) av[i] = perm(vx[2 * i + 1][mv / 2], vx[2 * i][mv / 2], sel);
+      for (int i = 0; i < 4; ++i) av[i] = perm(cur.vx[2 * i + 1][mv / 2], cur.vx[2 * i][mv / 2], sel);
       accv[mv] = mfma_k32(av, pb, accv[mv]);
     }
-  }
+    if (more) load_v(cur, cn);
+  };
+
+  // Full chunks, then the split's partial last chunk (if any).
+  int cb = cb0;
+  for (; cb + kChunk <= hi; cb += kChunk * NW) step(t, cb, std::false_type{});
+  if (cb < hi) step(t, cb, std::true_type{});
 
   {
     const float lt = xor_sum16_32(l_run);

@@ -103,6 +103,33 @@ __device__ __forceinline__ float safe_exp2_diff(float a, float b) {
   return (a == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(a - b);
 }
 
+// ---------------------------------------------------------------------------
+// Raw buffer loads.  A buffer resource (base, size) lives in SGPRs; each load
+// takes a 32-bit lane offset (VGPR) plus an immediate, so per-chunk addressing
+// costs one VALU add per offset family instead of a 64-bit add per load.  The
+// hardware range check returns 0 for any offset >= size, so a tile that runs
+// past the end of a cache block reads zeros instead of faulting.
+// 0x00020000 is the gfx9-family third descriptor dword (32-bit raw data).
+// ---------------------------------------------------------------------------
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ uint32_t buf_u32(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ u2 buf_u2(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+}
+__device__ __forceinline__ u4 buf_u4(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t buf_u16(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+
 // Global loads of 4/8/16 bytes through the vector memory path.
 __device__ __forceinline__ uint32_t ld_u32(const uint8_t* p) {
   return *reinterpret_cast<const uint32_t*>(p);
