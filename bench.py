@@ -52,6 +52,15 @@ def _args():
     ap.add_argument("--num-splits", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
+    ap.add_argument("--rocprof-summary", metavar="TRACE_DIR", default=None,
+                    help="no GPU work: summarise a rocprofv3 --kernel-trace --stats "
+                         "--output-format csv directory (plus --pmc-fetch/--pmc-write "
+                         "counter directories) as the text kept under profiles/")
+    ap.add_argument("--pmc-fetch", default=None)
+    ap.add_argument("--pmc-write", default=None)
+    ap.add_argument("--kernel", default="quant_split_kernel<128, 4, 4, 32",
+                    help="kernel-name substring the summary and traffic figures are for")
+    ap.add_argument("--command", default="", help="command line recorded in the summary")
     return ap.parse_args()
 
 
@@ -62,9 +71,9 @@ def _args():
 
 def algorithmic_bytes(B, HQ, HKV, S, D, kbits, vbits, gs):
     """Cache bytes + q (fp16) + out (fp32) of one decode step."""
-    from oracle.quant import row_bytes  # pure arithmetic on sizes; same formula as the docs
+    from tritonkv_amd.quantize import cache_row_bytes
 
-    cache = B * HKV * S * (row_bytes(D, kbits, gs) + row_bytes(D, vbits, gs))
+    cache = B * HKV * S * (cache_row_bytes(D, kbits, gs) + cache_row_bytes(D, vbits, gs))
     return cache, cache + B * HQ * D * (2 + 4)
 
 
@@ -106,8 +115,10 @@ def capture(calls):
 
 
 def timed_steps(copies, steps, warmup, reps=3):
-    """µs per step of ``steps`` rotating calls in one graph (best of ``reps`` replays)
-    plus the wall-clock ms per step of the first timed replay."""
+    """µs per step of ``steps`` rotating calls in one graph: the mean over
+    ``reps`` replays (every timed launch counts, as in a profiler's average),
+    plus the wall-clock ms per step of the first timed replay and the
+    per-replay figures."""
     import torch
 
     for i in range(warmup):
@@ -128,7 +139,7 @@ def timed_steps(copies, steps, warmup, reps=3):
         walls.append((time.perf_counter() - t0) * 1e3 / steps)
         us.append(s.elapsed_time(e) * 1e3 / steps)
     del g
-    return min(us), walls[0], us
+    return statistics.mean(us), walls[0], us
 
 
 def per_call_us(calls, reps=5):
@@ -156,56 +167,186 @@ def per_call_us(calls, reps=5):
 # ---------------------------------------------------------------------------
 
 
-def fused_call(q, kq, vq, num_splits=None, split_only=False):
+def fused_call(q, kq, vq, num_splits=None, split_only=False, waves=None, fused_combine=False):
     import torch
 
     from tritonkv_amd import _lib
-    from tritonkv_amd.kernels.fused_decode_attn import _workspace_for, plan_splits
+    from tritonkv_amd.kernels.fused_decode_attn import _workspace_for, choose_waves, plan_splits
 
     B, HQ, D = q.shape
     _, HKV, S, _ = kq.packed.shape
     _, ns, size = plan_splits(S, 64, num_splits, B, HKV, HQ // HKV)
     out = torch.empty(B, HQ, D, device=q.device)
-    acc, mx, sm = _workspace_for({}, B, HQ, ns, D, q.device)
+    acc, mx, sm, cnt = _workspace_for({}, B, HQ, ns, D, q.device, HKV)
+    wv = choose_waves(B, HKV, HQ // HKV, size, ns) if waves is None else waves
     args = _lib.DecodeArgs(
         q=q.data_ptr(), k=kq.packed.data_ptr(), k_scale=kq.scale.data_ptr(),
         k_zero=kq.zero.data_ptr(), v=vq.packed.data_ptr(), v_scale=vq.scale.data_ptr(),
         v_zero=vq.zero.data_ptr(), acc=_lib.ptr(acc), maxs=_lib.ptr(mx), sums=_lib.ptr(sm),
         out=out.data_ptr(), B=B, HQ=HQ, HKV=HKV, S=S, D=D, k_nbits=kq.nbits, v_nbits=vq.nbits,
-        group_size=kq.group_size, sm_scale=D ** -0.5, split_size=size, num_splits=ns)
+        group_size=kq.group_size, sm_scale=D ** -0.5, split_size=size, num_splits=ns,
+        counters=_lib.ptr(cnt) if (fused_combine and not split_only) else None, waves=wv)
     lib = _lib.load()
     fn = lib.tkv_fused_decode_split if split_only else lib.tkv_fused_decode_attention
 
     def call():
         _lib.check(fn(args, torch.cuda.current_stream().cuda_stream), "fused")
-    call.keep = (out, acc, mx, sm, q, kq, vq)
+    call.keep = (out, acc, mx, sm, cnt, q, kq, vq)
     call.num_splits = ns
+    call.kernel = (f"quant_split_kernel<{D}, {kq.nbits}, {vq.nbits}, {kq.group_size}, {wv}>")
     return call
 
 
-def fp16_call(q, k, v, num_splits=None, split_only=False):
+def fp16_call(q, k, v, num_splits=None, split_only=False, waves=None, fused_combine=False):
     import torch
 
     from tritonkv_amd import _lib
-    from tritonkv_amd.kernels.fused_decode_attn import _workspace_for, plan_splits
+    from tritonkv_amd.kernels.fused_decode_attn import _workspace_for, choose_waves, plan_splits
 
     B, HQ, D = q.shape
     _, HKV, S, _ = k.shape
     _, ns, size = plan_splits(S, 64, num_splits, B, HKV, HQ // HKV)
     out = torch.empty(B, HQ, D, device=q.device)
-    acc, mx, sm = _workspace_for({}, B, HQ, ns, D, q.device)
+    acc, mx, sm, cnt = _workspace_for({}, B, HQ, ns, D, q.device, HKV)
+    wv = choose_waves(B, HKV, HQ // HKV, size, ns) if waves is None else waves
     args = _lib.DecodeArgs(
         q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(), acc=_lib.ptr(acc), maxs=_lib.ptr(mx),
         sums=_lib.ptr(sm), out=out.data_ptr(), B=B, HQ=HQ, HKV=HKV, S=S, D=D, k_nbits=16,
-        v_nbits=16, group_size=D, sm_scale=D ** -0.5, split_size=size, num_splits=ns)
+        v_nbits=16, group_size=D, sm_scale=D ** -0.5, split_size=size, num_splits=ns,
+        counters=_lib.ptr(cnt) if (fused_combine and not split_only) else None, waves=wv)
     lib = _lib.load()
     fn = lib.tkv_fp16_decode_split if split_only else lib.tkv_fp16_decode_attention
 
     def call():
         _lib.check(fn(args, torch.cuda.current_stream().cuda_stream), "fp16")
-    call.keep = (out, acc, mx, sm, q, k, v)
+    call.keep = (out, acc, mx, sm, cnt, q, k, v)
     call.num_splits = ns
     return call
+
+
+def copy_probe(nbytes=1 << 30, reps=5):
+    """Device-to-device copy bandwidth (read + write bytes / time), median of reps.
+
+    Also the calibration kernel for rocprofv3 FETCH_SIZE / WRITE_SIZE: it reads
+    and writes exactly ``nbytes`` per dispatch.
+    """
+    import torch
+
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    out = []
+    for _ in range(reps):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        dst.copy_(src)
+        e.record()
+        torch.cuda.synchronize()
+        out.append(2 * nbytes / (s.elapsed_time(e) * 1e-3) / 1e9)
+    del src, dst
+    return statistics.median(out)
+
+
+# ---------------------------------------------------------------------------
+# rocprofv3 summaries (text kept under profiles/) and the traffic figure
+# ---------------------------------------------------------------------------
+
+COPY_PROBE_BYTES = 1 << 30
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "quant_split_kernel_llama3_8b_4bit.txt")
+
+
+def _csv_rows(directory, suffix):
+    import csv
+    import glob
+
+    files = sorted(glob.glob(os.path.join(directory, f"*{suffix}")))
+    if not files:
+        raise FileNotFoundError(f"no *{suffix} under {directory}")
+    with open(files[0], newline="") as fh:
+        return list(csv.DictReader(fh))
+
+
+def _short(name, width=96):
+    return name if len(name) <= width else name[:width - 3] + "..."
+
+
+def _counter_per_dispatch(directory, kernel):
+    """(mean counter value of ``kernel``'s largest-grid dispatches, n, name,
+    mean value of the 1 GiB copy-probe dispatches) from a --pmc directory."""
+    rows = _csv_rows(directory, "counter_collection.csv")
+    by = {}
+    for r in rows:
+        by.setdefault((r["Kernel_Name"], int(r["Grid_Size"])), []).append(float(r["Counter_Value"]))
+    mine = [(g, n, v) for (n, g), v in by.items() if kernel in n]
+    if not mine:
+        raise ValueError(f"no dispatch of {kernel!r} in {directory}")
+    g, name, vals = max(mine)
+    copies = [v for (n, _), v in by.items() if "copyBuffer" in n]
+    copy_kib = max(statistics.mean(v) for v in copies) if copies else None
+    return statistics.mean(vals), len(vals), name, copy_kib
+
+
+def rocprof_summary(a) -> int:
+    out = []
+    out.append(f"# rocprofv3 summary -- kernel {a.kernel}..., Llama-3-8B decode step "
+               f"(B=32 HQ=32 HKV=8 D=128 ctx=32768, 4-bit gs32), bench.py --quick")
+    if a.command:
+        out.append(f"command: {a.command}")
+    trace = _csv_rows(a.rocprof_summary, "kernel_trace.csv")
+    stats = _csv_rows(a.rocprof_summary, "kernel_stats.csv")
+    out.append("")
+    out.append("## kernel stats (rocprofv3 --stats, all dispatches of the run)")
+    out.append(f"{'calls':>6} {'avg_us':>10} {'min_us':>10} {'max_us':>10} {'pct':>6}  kernel")
+    for r in sorted(stats, key=lambda r: -float(r["TotalDurationNs"]))[:8]:
+        out.append(f"{int(r['Calls']):>6} {float(r['AverageNs']) / 1e3:>10.2f} "
+                   f"{float(r['MinNs']) / 1e3:>10.2f} {float(r['MaxNs']) / 1e3:>10.2f} "
+                   f"{float(r['Percentage']):>6.2f}  {_short(r['Name'])}")
+    out.append("")
+    out.append("## per-dispatch durations by grid (kernel trace)")
+    groups = {}
+    for r in trace:
+        grid = (int(r["Grid_Size_X"]), int(r["Grid_Size_Y"]), int(r["Grid_Size_Z"]))
+        wg = int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"]) * int(r["Workgroup_Size_Z"])
+        dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        groups.setdefault((r["Kernel_Name"], grid, wg), []).append(dur)
+    out.append(f"{'calls':>6} {'avg_us':>10} {'median_us':>10} {'grid':>18} {'wg':>5}  kernel")
+    for (name, grid, wg), d in sorted(groups.items(), key=lambda kv: -sum(kv[1]))[:10]:
+        out.append(f"{len(d):>6} {statistics.mean(d):>10.2f} {statistics.median(d):>10.2f} "
+                   f"{'x'.join(map(str, grid)):>18} {wg:>5}  {_short(name)}")
+    if a.pmc_fetch and a.pmc_write:
+        f_kib, nf, name, f_copy = _counter_per_dispatch(a.pmc_fetch, a.kernel)
+        w_kib, nw, _, w_copy = _counter_per_dispatch(a.pmc_write, a.kernel)
+        copy_kib = COPY_PROBE_BYTES / 1024
+        ff = copy_kib / f_copy if f_copy else 1.0
+        fw = copy_kib / w_copy if w_copy else 1.0
+        traffic = int(round((f_kib * ff + w_kib * fw) * 1024))
+        out.append("")
+        out.append("## HBM traffic (rocprofv3 --pmc FETCH_SIZE, then --pmc WRITE_SIZE; KiB/dispatch)")
+        out.append(f"kernel: {name}")
+        out.append(f"FETCH_SIZE  {f_kib:14.1f} KiB over {nf} dispatches; copy probe "
+                   f"({COPY_PROBE_BYTES} B read+write) reads {f_copy:.1f} KiB -> factor {ff:.4f}")
+        out.append(f"WRITE_SIZE  {w_kib:14.1f} KiB over {nw} dispatches; copy probe "
+                   f"writes {w_copy:.1f} KiB -> factor {fw:.4f}")
+        out.append(f"traffic_bytes_per_launch: {traffic}")
+    print("\n".join(out))
+    return 0
+
+
+def measured_traffic(kernel_name):
+    """HBM bytes per launch from the committed --pmc summary, if it was taken
+    of the same kernel instantiation; else None."""
+    try:
+        with open(TRAFFIC_PROFILE) as fh:
+            text = fh.read()
+    except OSError:
+        return None
+    kern = [ln.split(":", 1)[1].strip() for ln in text.splitlines() if ln.startswith("kernel: ")]
+    vals = [ln.split(":", 1)[1].strip() for ln in text.splitlines()
+            if ln.startswith("traffic_bytes_per_launch:")]
+    if not kern or not vals or kernel_name not in kern[-1]:
+        return None
+    return int(vals[-1])
 
 
 # ---------------------------------------------------------------------------
@@ -305,9 +446,11 @@ def qwen_table(ctxs=(512, 2048, 8192, 16384)):
 
 def main() -> int:
     a = _args()
+    if a.rocprof_summary:
+        return rocprof_summary(a)
     if a.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU per box; the decode step shards "
-                          "by kv head with no communication (see DESIGN.md), and no figure at "
+                          "by (batch, kv head) with no communication, and no figure at "
                           f"{a.gpus} GPUs is produced"}))
         return 2
     import torch
@@ -343,15 +486,22 @@ def main() -> int:
     steps4 = [fused_call(*c, num_splits=a.num_splits) for c in copies4]
     us4, wall4, samples4 = timed_steps(steps4, a.steps, a.warmup)
     split4 = [fused_call(*c, num_splits=a.num_splits, split_only=True) for c in copies4]
-    split_us4, _, _ = timed_steps(split4, a.steps, 2)
+    split_us4, _, split_samples4 = timed_steps(split4, a.steps, 2)
+    kernel4 = split4[0].kernel
     achieved = bytes4 / split_us4 / 1e3
     print(f"# llama 4-bit: step {us4:.2f} us, split kernel {split_us4:.2f} us, "
           f"{achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%} of 8 TB/s), "
           f"splits={steps4[0].num_splits}", file=sys.stderr, flush=True)
+    copy_gbs = copy_probe()
+    print(f"# device copy probe: {copy_gbs:.0f} GB/s (read+write)", file=sys.stderr, flush=True)
+    detail["device_copy_gbps"] = round(copy_gbs, 1)
     detail["fused4"] = {"us_per_step": round(us4, 2), "split_kernel_us": round(split_us4, 2),
+                        "frac_of_copy_bw": round(achieved / copy_gbs, 4),
                         "cache_bytes": cache4, "algorithmic_bytes": bytes4,
                         "gbps_step": round(bytes4 / us4 / 1e3, 1),
-                        "num_splits": steps4[0].num_splits}
+                        "num_splits": steps4[0].num_splits,
+                        "step_us_per_replay": [round(x, 2) for x in samples4],
+                        "split_kernel_us_per_replay": [round(x, 2) for x in split_samples4]}
     cpu = None
     if not a.quick and not a.no_cpu_baseline:
         q0, kq0, vq0 = copies4[0]
@@ -399,9 +549,10 @@ def main() -> int:
         "gbps": round(bytes4 / us4 / 1e3, 1),
         "hbm_frac": round(bytes4 / us4 / 1e3 / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "quant_split_kernel<128,4,4,32,4>",
-                     "kernel_us": round(split_us4, 2)},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(kernel4),
+                     "kernel": kernel4, "kernel_us": round(split_us4, 2),
+                     "algorithmic_bytes": bytes4},
         "cpu_baseline": cpu,
         "detail": detail,
     }

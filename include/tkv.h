@@ -47,7 +47,15 @@ enum {
  * The history [0, S) is cut into num_splits ranges of split_size tokens
  * (the last one ragged).  If num_splits == 1 the kernel writes out directly and
  * acc/maxs/sums may be NULL; otherwise it writes the partials and a combine
- * pass writes out. */
+ * pass writes out:
+ *   counters == NULL   a separate combine kernel (tkv_*_attention) merges them;
+ *   counters != NULL   the split kernel's last workgroup of each (b, kv head,
+ *                      block of 16 query heads) merges them itself, found by an
+ *                      atomic ticket in counters[(b*HKV + kv)*ceil(G/16) + blk].
+ *                      The caller zero-fills the B*HKV*ceil(G/16) int32 counters
+ *                      once; every call leaves them zero again.  Calls that
+ *                      share a counters buffer must not overlap in time.
+ * waves: workgroup size in 64-lane waves, 4 or 8 (0 = 4). */
 typedef struct tkv_decode_args {
   const void *q;
   int32_t q_is_fp32;
@@ -61,10 +69,12 @@ typedef struct tkv_decode_args {
   int32_t group_size;       /* 16, 32, 64 or 128, <= D; ignored by the fp16 path */
   float sm_scale;
   int32_t split_size, num_splits;
+  int32_t *counters;
+  int32_t waves;
 } tkv_decode_args;
 
 /* Fused 2/4-bit split-P decode attention: the split kernel, then (if
- * num_splits > 1) the log-sum-exp combine.
+ * num_splits > 1 and counters == NULL) the log-sum-exp combine kernel.
  * Replaces the two Triton launches of kernels/fused_decode_attn.py:525-568
  * (_fused_decode_attn_split :155-353 and _combine_splits :355-395). */
 int tkv_fused_decode_attention(const tkv_decode_args *args, tkv_stream_t stream);
@@ -73,8 +83,9 @@ int tkv_fused_decode_attention(const tkv_decode_args *args, tkv_stream_t stream)
  * Replaces kernels/fp16_decode_attn.py:207-239 (_fp16_decode_attn_split :47-135). */
 int tkv_fp16_decode_attention(const tkv_decode_args *args, tkv_stream_t stream);
 
-/* The split kernels alone (no combine): with num_splits == 1 they write out,
- * otherwise only the partials acc/maxs/sums.  Replace the single launches
+/* The split kernels alone (no combine launch): with num_splits == 1 they write
+ * out; otherwise the partials acc/maxs/sums, merged into out by the last
+ * workgroup when counters != NULL.  Replace the single launches
  * kernels/fused_decode_attn.py:525-556 and kernels/fp16_decode_attn.py:207-227;
  * used to time the split kernel by itself. */
 int tkv_fused_decode_split(const tkv_decode_args *args, tkv_stream_t stream);

@@ -45,7 +45,7 @@ def test_library_exports_every_declared_symbol():
     for name in _declared_symbols():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.tkv_abi_version() == 1
+    assert lib.tkv_abi_version() == 2
 
 
 def test_library_is_gfx950_only():
@@ -69,10 +69,11 @@ def test_decode_args_layout_matches_c():
     #include <stddef.h>
     #include "tkv.h"
     int main(void) {
-      printf("%zu %zu %zu %zu %zu %zu %zu\n", sizeof(tkv_decode_args),
+      printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu\n", sizeof(tkv_decode_args),
              offsetof(tkv_decode_args, q_is_fp32), offsetof(tkv_decode_args, seq_lens),
              offsetof(tkv_decode_args, B), offsetof(tkv_decode_args, sm_scale),
-             offsetof(tkv_decode_args, num_splits), sizeof(tkv_device_info_t));
+             offsetof(tkv_decode_args, num_splits), offsetof(tkv_decode_args, counters),
+             offsetof(tkv_decode_args, waves), sizeof(tkv_device_info_t));
       return 0;
     }"""
     with tempfile.TemporaryDirectory() as d:
@@ -84,7 +85,8 @@ def test_decode_args_layout_matches_c():
                                                check=True).stdout.split()]
     A = _lib.DecodeArgs
     assert vals == [ctypes.sizeof(A), A.q_is_fp32.offset, A.seq_lens.offset, A.B.offset,
-                    A.sm_scale.offset, A.num_splits.offset, ctypes.sizeof(_lib.DeviceInfo)]
+                    A.sm_scale.offset, A.num_splits.offset, A.counters.offset, A.waves.offset,
+                    ctypes.sizeof(_lib.DeviceInfo)]
 
 
 def test_c_entry_points_reject_bad_arguments_without_a_gpu():
@@ -111,7 +113,9 @@ def test_c_entry_points_reject_bad_arguments_without_a_gpu():
     assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
     a.split_size, a.group_size = 64, 48
     assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
-    a.group_size, a.D = 32, 96
+    a.group_size, a.waves = 32, 6
+    assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    a.waves, a.D = 8, 96
     assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EUNSUPPORTED
     assert _lib.status_string(_lib.TKV_EINVAL) == "invalid argument"
 

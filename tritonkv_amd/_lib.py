@@ -53,6 +53,8 @@ class DecodeArgs(ctypes.Structure):
         ("sm_scale", ctypes.c_float),
         ("split_size", ctypes.c_int32),
         ("num_splits", ctypes.c_int32),
+        ("counters", ctypes.c_void_p),
+        ("waves", ctypes.c_int32),
     ]
 
 

@@ -47,6 +47,7 @@ struct SplitParams {
   float* maxs;
   float* sums;
   float* out;
+  int* counters;  // fused-combine tickets, or null
   int HQ, HKV, S, G, num_splits, split_size, q_fp32;
   float qk_scale;  // sm_scale * log2(e)
 };
@@ -58,10 +59,6 @@ constexpr int kChunk = 32;  // tokens per wave iteration (two 16-row MFMA tiles)
 // accumulators of the two tiles hand P^T to the V MFMA without any shuffle.
 __device__ __forceinline__ int slot_token(int j, int i) { return (i < 4 ? 0 : 12) + 4 * j + i; }
 
-__device__ __forceinline__ float load_q(const SplitParams& p, int64_t idx) {
-  return p.q_fp32 ? static_cast<const float*>(p.q)[idx]
-                  : (float)static_cast<const _Float16*>(p.q)[idx];
-}
 
 // ---------------------------------------------------------------------------
 // Online softmax over one chunk.  x[8]: scores of this lane's 8 tokens for
@@ -111,6 +108,7 @@ struct MergeLds {
   float m[NW][16];
   float l[NW][16];
   float o[NW][16][D + 1];
+  int last;  // this workgroup holds the final ticket of its unit
 };
 
 template <int D, int NW>
@@ -144,6 +142,47 @@ __device__ void merge_and_store(const SplitParams& prm, MergeLds<D, NW>& lds, in
       }
     }
   }
+  if (prm.num_splits == 1 || prm.counters == nullptr) return;
+
+  // Fused combine.  Each workgroup releases its partials (agent scope: the
+  // reader may sit on another XCD with its own L2) and takes a ticket; the
+  // one that draws the last ticket acquires everyone's partials and merges
+  // the splits of its rows, then resets the counter for the next call.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __syncthreads();
+  const int cidx = (b * prm.HKV + h0 / prm.G) * ((prm.G + 15) / 16) + (h0 % prm.G) / 16;
+  if (tid == 0) {
+    const int t = __hip_atomic_fetch_add(prm.counters + cidx, 1, __ATOMIC_ACQ_REL,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    lds.last = (t == prm.num_splits - 1);
+  }
+  __syncthreads();
+  if (!lds.last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  constexpr int DQ = D / 4;
+  const int ns = prm.num_splits;
+  for (int idx = tid; idx < nh * DQ; idx += NW * 64) {
+    const int n = idx / DQ, dq = idx % DQ;
+    const int64_t row = (int64_t)b * prm.HQ + h0 + n;
+    float m = -INFINITY, l = 0.0f;
+    f4 a = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+    for (int s = 0; s < ns; ++s) {
+      const int64_t ps = row * ns + s;
+      const float ms = prm.maxs[ps];
+      const float ls = prm.sums[ps];
+      const f4 as = reinterpret_cast<const f4*>(prm.acc + ps * D)[dq];
+      if (ms == -INFINITY) continue;
+      const float mn = fmaxf(m, ms);
+      const float al = safe_exp2_diff(m, mn);
+      const float be = __builtin_amdgcn_exp2f(ms - mn);
+      a = a * al + as * be;
+      l = l * al + ls * be;
+      m = mn;
+    }
+    reinterpret_cast<f4*>(prm.out + row * D)[dq] = a / l;
+  }
+  if (tid == 0) __hip_atomic_store(prm.counters + cidx, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ void wave_lds_fence() {
@@ -321,6 +360,8 @@ quant_split_kernel(SplitParams prm) {
   for (int idx = lane; idx < (16 - NG) * kChunk; idx += 64) ml.vz[NG + idx / kChunk][idx % kChunk] = 0;
 
   // ---- Q^T operand in K slot order, pre-scaled by 2^-(slice*KNB) ---------
+  // Lane-group j's dims of step m are the contiguous run
+  // [m*KSTEP + CB*j, +CB): one vector load per step, then slot order.
   u4 qf[NKM];
   float qz[NG];
 #pragma unroll
@@ -328,20 +369,43 @@ quant_split_kernel(SplitParams prm) {
   {
     const bool hv = n < nh;
     const int64_t qrow = ((int64_t)b * prm.HQ + h0 + (hv ? n : 0)) * D;
+    float qv[NKM][KL::CB];
+    if (prm.q_fp32) {
+      const float* qp = static_cast<const float*>(prm.q) + qrow;
+#pragma unroll
+      for (int m = 0; m < NKM; ++m)
+#pragma unroll
+        for (int c = 0; c < KL::CB; c += 4) {
+          const f4 v = *reinterpret_cast<const f4*>(qp + m * KL::KSTEP + KL::CB * j + c);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) qv[m][c + e] = (float)(_Float16)v[e];
+        }
+    } else {
+      const _Float16* qp = static_cast<const _Float16*>(prm.q) + qrow;
+#pragma unroll
+      for (int m = 0; m < NKM; ++m) {
+        if constexpr (KL::CB == 8) {
+          const h8 v = *reinterpret_cast<const h8*>(qp + m * KL::KSTEP + KL::CB * j);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) qv[m][e] = (float)v[e];
+        } else {
+          const h4 v = *reinterpret_cast<const h4*>(qp + m * KL::KSTEP + KL::CB * j);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) qv[m][e] = (float)v[e];
+        }
+      }
+    }
 #pragma unroll
     for (int m = 0; m < NKM; ++m) {
       const int p = KL::slice_of(m, j);
       const float pre = __builtin_ldexpf(1.0f, -p * KNB);
       uint32_t wv[4] = {0, 0, 0, 0};
 #pragma unroll
-      for (int s = 0; s < KL::CB; s += 2) {
-        float q0 = 0.0f, q1 = 0.0f;
-        if (hv) {
-          q0 = (float)(_Float16)load_q(prm, qrow + KL::dim_of(m, j, s));
-          q1 = (float)(_Float16)load_q(prm, qrow + KL::dim_of(m, j, s + 1));
-        }
+      for (int s2 = 0; s2 < KL::CB; s2 += 2) {
+        const float q0 = hv ? qv[m][slot_byte(s2)] : 0.0f;
+        const float q1 = hv ? qv[m][slot_byte(s2 + 1)] : 0.0f;
         qz[KL::group_of_step(m)] += q0 + q1;
-        wv[s / 2] = pack_h2(q0 * pre, q1 * pre);
+        wv[s2 / 2] = pack_h2(q0 * pre, q1 * pre);
       }
       qf[m] = u4{wv[0], wv[1], wv[2], wv[3]};
     }
@@ -601,20 +665,29 @@ fp16_split_kernel(SplitParams prm) {
 
   u4 qf[NKM];
   {
+    // dims 32m + 8j .. +7 of head n: one vector load per MFMA step
     const bool hv = n < nh;
     const int64_t qrow = ((int64_t)b * prm.HQ + h0 + (hv ? n : 0)) * D;
 #pragma unroll
     for (int m = 0; m < NKM; ++m) {
+      float qv[8];
+      if (prm.q_fp32) {
+        const float* qp = static_cast<const float*>(prm.q) + qrow + 32 * m + 8 * j;
+        const f4 a0 = *reinterpret_cast<const f4*>(qp);
+        const f4 a1 = *reinterpret_cast<const f4*>(qp + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          qv[e] = a0[e];
+          qv[4 + e] = a1[e];
+        }
+      } else {
+        const h8 v = *reinterpret_cast<const h8*>(static_cast<const _Float16*>(prm.q) + qrow + 32 * m + 8 * j);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qv[e] = (float)v[e];
+      }
       uint32_t wv[4];
 #pragma unroll
-      for (int s = 0; s < 8; s += 2) {
-        float q0 = 0.0f, q1 = 0.0f;
-        if (hv) {
-          q0 = load_q(prm, qrow + 32 * m + 8 * j + s);
-          q1 = load_q(prm, qrow + 32 * m + 8 * j + s + 1);
-        }
-        wv[s / 2] = pack_h2(q0, q1);
-      }
+      for (int s2 = 0; s2 < 8; s2 += 2) wv[s2 / 2] = hv ? pack_h2(qv[s2], qv[s2 + 1]) : 0u;
       qf[m] = u4{wv[0], wv[1], wv[2], wv[3]};
     }
   }
@@ -744,8 +817,6 @@ __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ 
 // ===========================================================================
 // Host side: validation and dispatch.
 // ===========================================================================
-constexpr int kWaves = 4;
-
 static int validate_common(const tkv_decode_args* a) {
   if (!a || !a->q || !a->k || !a->v || !a->out) return TKV_EINVAL;
   if (a->B <= 0 || a->HQ <= 0 || a->HKV <= 0 || a->S <= 0 || a->D <= 0) return TKV_EINVAL;
@@ -757,9 +828,12 @@ static int validate_common(const tkv_decode_args* a) {
   // Vector loads: caches 16-byte aligned, metadata 4-byte, partials 8-byte.
   if (((uintptr_t)a->k | (uintptr_t)a->v) & 15) return TKV_EINVAL;
   if (((uintptr_t)a->k_scale | (uintptr_t)a->k_zero | (uintptr_t)a->v_scale |
-       (uintptr_t)a->v_zero | (uintptr_t)a->q) & 3)
+       (uintptr_t)a->v_zero) & 3)
     return TKV_EINVAL;
+  if ((uintptr_t)a->q & 15) return TKV_EINVAL;  // vector loads of q rows
   if (((uintptr_t)a->acc | (uintptr_t)a->out) & 15) return TKV_EINVAL;  // float4 rows
+  if (a->waves != 0 && a->waves != 4 && a->waves != 8) return TKV_EINVAL;
+  if ((uintptr_t)a->counters & 3) return TKV_EINVAL;
   if (a->D != 64 && a->D != 128) return TKV_EUNSUPPORTED;
   return TKV_OK;
 }
@@ -778,6 +852,7 @@ static SplitParams make_params(const tkv_decode_args* a) {
   p.maxs = a->maxs;
   p.sums = a->sums;
   p.out = a->out;
+  p.counters = a->counters;
   p.HQ = a->HQ;
   p.HKV = a->HKV;
   p.S = a->S;
@@ -795,19 +870,22 @@ static dim3 split_grid(const tkv_decode_args* a) {
 }
 
 template <int D, int KNB, int VNB, int GS>
-static void launch_quant(const SplitParams& p, dim3 grid, hipStream_t st) {
-  quant_split_kernel<D, KNB, VNB, GS, kWaves><<<grid, dim3(kWaves * 64), 0, st>>>(p);
+static void launch_quant(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
+  if (waves == 8)
+    quant_split_kernel<D, KNB, VNB, GS, 8><<<grid, dim3(8 * 64), 0, st>>>(p);
+  else
+    quant_split_kernel<D, KNB, VNB, GS, 4><<<grid, dim3(4 * 64), 0, st>>>(p);
 }
 
 template <int D, int KNB, int VNB>
-static int dispatch_gs(const SplitParams& p, dim3 grid, int gs, hipStream_t st) {
+static int dispatch_gs(const SplitParams& p, dim3 grid, int gs, int waves, hipStream_t st) {
   switch (gs) {
-    case 16: launch_quant<D, KNB, VNB, 16>(p, grid, st); return TKV_OK;
-    case 32: launch_quant<D, KNB, VNB, 32>(p, grid, st); return TKV_OK;
-    case 64: launch_quant<D, KNB, VNB, 64>(p, grid, st); return TKV_OK;
+    case 16: launch_quant<D, KNB, VNB, 16>(p, grid, waves, st); return TKV_OK;
+    case 32: launch_quant<D, KNB, VNB, 32>(p, grid, waves, st); return TKV_OK;
+    case 64: launch_quant<D, KNB, VNB, 64>(p, grid, waves, st); return TKV_OK;
     case 128:
       if constexpr (D >= 128) {
-        launch_quant<D, KNB, VNB, 128>(p, grid, st);
+        launch_quant<D, KNB, VNB, 128>(p, grid, waves, st);
         return TKV_OK;
       }
       return TKV_EUNSUPPORTED;
@@ -816,11 +894,12 @@ static int dispatch_gs(const SplitParams& p, dim3 grid, int gs, hipStream_t st) 
 }
 
 template <int D>
-static int dispatch_bits(const SplitParams& p, dim3 grid, int knb, int vnb, int gs, hipStream_t st) {
-  if (knb == 4 && vnb == 4) return dispatch_gs<D, 4, 4>(p, grid, gs, st);
-  if (knb == 2 && vnb == 2) return dispatch_gs<D, 2, 2>(p, grid, gs, st);
-  if (knb == 4 && vnb == 2) return dispatch_gs<D, 4, 2>(p, grid, gs, st);
-  if (knb == 2 && vnb == 4) return dispatch_gs<D, 2, 4>(p, grid, gs, st);
+static int dispatch_bits(const SplitParams& p, dim3 grid, int knb, int vnb, int gs, int waves,
+                         hipStream_t st) {
+  if (knb == 4 && vnb == 4) return dispatch_gs<D, 4, 4>(p, grid, gs, waves, st);
+  if (knb == 2 && vnb == 2) return dispatch_gs<D, 2, 2>(p, grid, gs, waves, st);
+  if (knb == 4 && vnb == 2) return dispatch_gs<D, 4, 2>(p, grid, gs, waves, st);
+  if (knb == 2 && vnb == 4) return dispatch_gs<D, 2, 4>(p, grid, gs, waves, st);
   return TKV_EUNSUPPORTED;
 }
 
@@ -856,8 +935,8 @@ static int launch_fused_split(const tkv_decode_args* a, hipStream_t st) {
   const SplitParams p = make_params(a);
   const dim3 grid = split_grid(a);
   (void)hipGetLastError();
-  rc = a->D == 128 ? dispatch_bits<128>(p, grid, a->k_nbits, a->v_nbits, gs, st)
-                   : dispatch_bits<64>(p, grid, a->k_nbits, a->v_nbits, gs, st);
+  rc = a->D == 128 ? dispatch_bits<128>(p, grid, a->k_nbits, a->v_nbits, gs, a->waves, st)
+                   : dispatch_bits<64>(p, grid, a->k_nbits, a->v_nbits, gs, a->waves, st);
   if (rc) return rc;
   return status_of_launch();
 }
@@ -868,15 +947,22 @@ static int launch_fp16_split(const tkv_decode_args* a, hipStream_t st) {
   const SplitParams p = make_params(a);
   const dim3 grid = split_grid(a);
   (void)hipGetLastError();
-  if (a->D == 128)
-    fp16_split_kernel<128, kWaves><<<grid, dim3(kWaves * 64), 0, st>>>(p);
-  else
-    fp16_split_kernel<64, kWaves><<<grid, dim3(kWaves * 64), 0, st>>>(p);
+  if (a->D == 128) {
+    if (a->waves == 8)
+      fp16_split_kernel<128, 8><<<grid, dim3(8 * 64), 0, st>>>(p);
+    else
+      fp16_split_kernel<128, 4><<<grid, dim3(4 * 64), 0, st>>>(p);
+  } else {
+    if (a->waves == 8)
+      fp16_split_kernel<64, 8><<<grid, dim3(8 * 64), 0, st>>>(p);
+    else
+      fp16_split_kernel<64, 4><<<grid, dim3(4 * 64), 0, st>>>(p);
+  }
   return status_of_launch();
 }
 
 static int finish_combine(const tkv_decode_args* a, hipStream_t st) {
-  if (a->num_splits <= 1) return TKV_OK;
+  if (a->num_splits <= 1 || a->counters) return TKV_OK;  // counters: merged in the split kernel
   (void)hipGetLastError();
   launch_combine(a->acc, a->maxs, a->sums, a->out, a->B, a->HQ, a->num_splits, a->D, st);
   return status_of_launch();

@@ -17,9 +17,11 @@ import torch
 
 from .. import _lib
 from .fused_decode_attn import (
+    _aligned16,
     _check_out,
     _seq_lens_arg,
     _workspace_for,
+    choose_waves,
     plan_splits,
     triton_available,
 )
@@ -58,13 +60,13 @@ def fp16_decode_attention(
     sm_scale = 1.0 / math.sqrt(D) if sm_scale is None else sm_scale
     _, num_splits, split_size = plan_splits(S, block_n, num_splits, B, HKV, group)
 
-    q = q.contiguous()
     if q.dtype not in (torch.float16, torch.float32):
         q = q.float()
-    k = k.contiguous() if k.dtype == torch.float16 else k.half().contiguous()
-    v = v.contiguous() if v.dtype == torch.float16 else v.half().contiguous()
+    q = _aligned16(q)
+    k = _aligned16(k if k.dtype == torch.float16 else k.half())
+    v = _aligned16(v if v.dtype == torch.float16 else v.half())
     out = _check_out(out, B, HQ, D, q.device)
-    acc, maxs, sums = _workspace_for(_workspace, B, HQ, num_splits, D, q.device)
+    acc, maxs, sums, counters = _workspace_for(_workspace, B, HQ, num_splits, D, q.device, HKV)
     lens = _seq_lens_arg(seq_lens, B, S, q.device)
 
     args = _lib.DecodeArgs(
@@ -72,7 +74,8 @@ def fp16_decode_attention(
         k=k.data_ptr(), v=v.data_ptr(), seq_lens=_lib.ptr(lens),
         acc=_lib.ptr(acc), maxs=_lib.ptr(maxs), sums=_lib.ptr(sums), out=out.data_ptr(),
         B=B, HQ=HQ, HKV=HKV, S=S, D=D, k_nbits=16, v_nbits=16, group_size=D,
-        sm_scale=float(sm_scale), split_size=split_size, num_splits=num_splits)
+        sm_scale=float(sm_scale), split_size=split_size, num_splits=num_splits,
+        counters=None, waves=choose_waves(B, HKV, group, split_size, num_splits))
     with torch.cuda.device(q.device):
         rc = _lib.load().tkv_fp16_decode_attention(args, _lib.stream_handle(q.device))
     _lib.check(rc, "fp16_decode_attention")

@@ -28,6 +28,10 @@ Differences a caller can observe, all deliberate:
 * ``allow_mixed_bits=True`` (new, keyword-only) lets K and V use different bit
   widths (e.g. 4-bit K, 2-bit V); without it the reference's ValueError is
   raised.  ``seq_lens`` (new) gives one context length per batch row.
+  ``fused_combine=True`` (new) merges split partials inside the split kernel
+  (last workgroup per unit) instead of a second launch; it is correct but
+  measured slower on MI355X (every workgroup's agent-scope release writes back
+  its L2), so it is off by default.
 """
 
 from __future__ import annotations
@@ -95,17 +99,31 @@ def pick_num_splits(B: int, HKV: int, n_blocks: int, target_programs: int | None
 def default_num_splits(B: int, HKV: int, G: int, S: int, block_n: int) -> int:
     """Split count used when the caller passes ``num_splits=None``.
 
-    Aims at two workgroups per compute unit (each workgroup is 4 waves and
-    streams at least 128 tokens), counting every (batch row, kv head, block of
-    16 query heads) as one unit of parallelism.  Returned in units of
-    ``block_n`` blocks so the reference's tightening applies unchanged.
+    Chosen from a sweep on MI355X (split count x workgroup size x combine mode,
+    Qwen2.5-1.5B shape at ctx 512..16384 and Llama-3-8B at B=32, ctx 32768):
+
+    * a batch that already offers one (b, kv head, 16-head block) unit per
+      compute unit or more runs unsplit -- no partials, no combine launch;
+    * otherwise about 64 workgroups in total, each streaming at least 128
+      tokens, and no split at all up to 1024 tokens, where one 8-wave
+      workgroup per unit beats any split-plus-combine on latency.
+
+    Returned in units of ``block_n`` blocks so the reference's tightening
+    applies unchanged.
     """
     cu = compute_units() or 256
     units = B * HKV * _cdiv(G, 16)
-    want = max(1, _cdiv(2 * cu, units))
-    n_blocks = _cdiv(S, block_n)
-    max_splits = max(1, _cdiv(S, max(_MIN_SPLIT_TOKENS, block_n)))
-    return max(1, min(want, max_splits, n_blocks))
+    if units >= cu or S <= 1024:
+        return 1
+    want = max(1, _cdiv(64, units))
+    max_splits = max(1, S // max(_MIN_SPLIT_TOKENS, block_n))
+    return max(1, min(want, max_splits, _cdiv(S, block_n)))
+
+
+def choose_waves(B: int, HKV: int, G: int, split_size: int, num_splits: int = 0) -> int:
+    """Waves per workgroup: 8 for unsplit runs (one workgroup per unit must
+    carry the whole history), 4 when the history is split."""
+    return 8 if num_splits == 1 else 4
 
 
 def plan_splits(S: int, block_n: int, num_splits: int | None, B: int, HKV: int, G: int):
@@ -120,23 +138,40 @@ def plan_splits(S: int, block_n: int, num_splits: int | None, B: int, HKV: int, 
     return block_n, num_splits, blocks_per_split * block_n
 
 
-def _workspace_for(ws: dict | None, B: int, HQ: int, num_splits: int, D: int, device):
-    """Partials buffers, reused under the reference's keys (:505-521)."""
+def _workspace_for(ws: dict | None, B: int, HQ: int, num_splits: int, D: int, device,
+                   HKV: int = 1):
+    """Partials buffers, reused under the reference's keys (:505-521).
+
+    Returns ``(acc, maxs, sums, counters)``.  ``counters`` holds one int32
+    ticket per (batch row, kv head, block of 16 query heads); it is zeroed once
+    when allocated and the kernels leave it zero, so the split kernel can merge
+    its own partials (no combine launch) and the call stays graph-capturable.
+    """
     ws = ws if ws is not None else {}
     if num_splits == 1:
         acc = ws.get("dummy_acc")
         if acc is None:
             acc = torch.empty((1, 1, 1, 1), device=device, dtype=torch.float32)
             ws["dummy_acc"] = acc
-        return None, None, None
+        return None, None, None, None
     key = (B, HQ, num_splits, D)
-    if ws.get("key") == key:
-        return ws["acc"], ws["maxs"], ws["sums"]
-    acc = torch.empty((B, HQ, num_splits, D), device=device, dtype=torch.float32)
-    maxs = torch.empty((B, HQ, num_splits), device=device, dtype=torch.float32)
-    sums = torch.empty((B, HQ, num_splits), device=device, dtype=torch.float32)
-    ws.update(key=key, acc=acc, maxs=maxs, sums=sums)
-    return acc, maxs, sums
+    if ws.get("key") != key:
+        acc = torch.empty((B, HQ, num_splits, D), device=device, dtype=torch.float32)
+        maxs = torch.empty((B, HQ, num_splits), device=device, dtype=torch.float32)
+        sums = torch.empty((B, HQ, num_splits), device=device, dtype=torch.float32)
+        ws.update(key=key, acc=acc, maxs=maxs, sums=sums)
+    n_counters = B * HKV * _cdiv(HQ // HKV, 16)
+    cnt = ws.get("counters")
+    if cnt is None or cnt.numel() < n_counters or cnt.device != torch.device(device):
+        cnt = torch.zeros(n_counters, device=device, dtype=torch.int32)
+        ws["counters"] = cnt
+    return ws["acc"], ws["maxs"], ws["sums"], cnt
+
+
+def _aligned16(t: torch.Tensor) -> torch.Tensor:
+    """Contiguous and 16-byte aligned (the kernels load rows as 16-byte vectors)."""
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
 def _check_out(out, B, HQ, D, device):
@@ -173,6 +208,7 @@ def fused_decode_attention(
     *,
     seq_lens: torch.Tensor | None = None,
     allow_mixed_bits: bool = False,
+    fused_combine: bool = False,
 ) -> torch.Tensor:
     """Single decode step of attention, computed directly on packed low-bit K/V.
 
@@ -207,13 +243,13 @@ def fused_decode_attention(
     sm_scale = 1.0 / math.sqrt(D) if sm_scale is None else sm_scale
     _, num_splits, split_size = plan_splits(S, block_n, num_splits, B, HKV, group)
 
-    q = q.contiguous()
     if q.dtype not in (torch.float16, torch.float32):
         q = q.float()
-    kp, ks, kz = kq.packed.contiguous(), kq.scale.contiguous(), kq.zero.contiguous()
-    vp, vs, vz = vq.packed.contiguous(), vq.scale.contiguous(), vq.zero.contiguous()
+    q = _aligned16(q)
+    kp, ks, kz = _aligned16(kq.packed), _aligned16(kq.scale), _aligned16(kq.zero)
+    vp, vs, vz = _aligned16(vq.packed), _aligned16(vq.scale), _aligned16(vq.zero)
     out = _check_out(out, B, HQ, D, q.device)
-    acc, maxs, sums = _workspace_for(_workspace, B, HQ, num_splits, D, q.device)
+    acc, maxs, sums, counters = _workspace_for(_workspace, B, HQ, num_splits, D, q.device, HKV)
     lens = _seq_lens_arg(seq_lens, B, S, q.device)
 
     args = _lib.DecodeArgs(
@@ -223,7 +259,9 @@ def fused_decode_attention(
         seq_lens=_lib.ptr(lens), acc=_lib.ptr(acc), maxs=_lib.ptr(maxs), sums=_lib.ptr(sums),
         out=out.data_ptr(), B=B, HQ=HQ, HKV=HKV, S=S, D=D,
         k_nbits=kq.nbits, v_nbits=vq.nbits, group_size=kq.group_size,
-        sm_scale=float(sm_scale), split_size=split_size, num_splits=num_splits)
+        sm_scale=float(sm_scale), split_size=split_size, num_splits=num_splits,
+        counters=_lib.ptr(counters) if fused_combine else None,
+        waves=choose_waves(B, HKV, group, split_size, num_splits))
     with torch.cuda.device(q.device):
         rc = _lib.load().tkv_fused_decode_attention(args, _lib.stream_handle(q.device))
     _lib.check(rc, "fused_decode_attention")
