@@ -46,7 +46,8 @@ def _args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=1000,
+                    help="untimed steps (graph replays) right before the timed ones")
     ap.add_argument("--quick", action="store_true",
                     help="headline workload only (no 2-bit / control / Qwen table / CPU baseline)")
     ap.add_argument("--num-splits", type=int, default=None)
@@ -116,16 +117,20 @@ def capture(calls):
 
 def timed_steps(copies, steps, warmup, reps=3):
     """µs per step of ``steps`` rotating calls in one graph: the mean over
-    ``reps`` replays (every timed launch counts, as in a profiler's average),
-    plus the wall-clock ms per step of the first timed replay and the
-    per-replay figures."""
+    ``reps`` timed replays (every timed launch counts, as in a profiler's
+    average), plus the wall-clock ms per step of the first timed replay and the
+    per-replay figures.
+
+    The ``warmup`` untimed steps are replays of the same graph issued right
+    before the timed ones: on MI355X the first ~100-250 ms of streaming after
+    an idle gap (such as the graph capture) run up to 10% below the sustained
+    rate, so warming up eagerly before the capture does not carry over.
+    """
     import torch
 
-    for i in range(warmup):
-        copies[i % len(copies)]()
-    torch.cuda.synchronize()
     g = capture([copies[i % len(copies)] for i in range(steps)])
-    g.replay()  # untimed: graph upload
+    for _ in range(max(1, math.ceil(warmup / steps))):
+        g.replay()
     torch.cuda.synchronize()
     us, walls = [], []
     for _ in range(reps):
@@ -486,7 +491,7 @@ def main() -> int:
     steps4 = [fused_call(*c, num_splits=a.num_splits) for c in copies4]
     us4, wall4, samples4 = timed_steps(steps4, a.steps, a.warmup)
     split4 = [fused_call(*c, num_splits=a.num_splits, split_only=True) for c in copies4]
-    split_us4, _, split_samples4 = timed_steps(split4, a.steps, 2)
+    split_us4, _, split_samples4 = timed_steps(split4, a.steps, a.warmup)
     kernel4 = split4[0].kernel
     achieved = bytes4 / split_us4 / 1e3
     print(f"# llama 4-bit: step {us4:.2f} us, split kernel {split_us4:.2f} us, "
@@ -515,7 +520,7 @@ def main() -> int:
             cache, nbytes = algorithmic_bytes(B, HQ, HKV, S, D, nbits, nbits, gs)
             mk = fp16_call if nbits == 16 else fused_call
             us, _, _ = timed_steps([mk(*c) for c in cps], a.steps, a.warmup)
-            sp, _, _ = timed_steps([mk(*c, split_only=True) for c in cps], a.steps, 2)
+            sp, _, _ = timed_steps([mk(*c, split_only=True) for c in cps], a.steps, a.warmup)
             detail[name] = {"us_per_step": round(us, 2), "split_kernel_us": round(sp, 2),
                             "cache_bytes": cache, "algorithmic_bytes": nbytes,
                             "gbps_split_kernel": round(nbytes / sp / 1e3, 1),
