@@ -54,6 +54,13 @@ struct SplitParams {
 
 constexpr int kChunk = 32;  // tokens per wave iteration (two 16-row MFMA tiles)
 
+// Cache policies of the streamed loads.
+constexpr int kPolQK = kPolicyDefault;   // quantized K codes
+constexpr int kPolQV = kPolicyDefault;   // quantized V codes
+constexpr int kPolMeta = kPolicyDefault; // scale / zero rows
+constexpr int kPolF16 = kPolicyNT;       // fp16 control K and V rows
+constexpr int kPolDma = kPolicyNT;       // LDS-staged kernel: K/V code and metadata ranges
+
 // Token of k-slot i (0..7) of lane-group j within a chunk: the rows 4j..4j+3
 // of tile 0 followed by those of tile 1 -- the order in which the S^T
 // accumulators of the two tiles hand P^T to the V MFMA without any shuffle.
@@ -103,16 +110,35 @@ __device__ __forceinline__ bool softmax_chunk(const float (&x)[8], float lscale,
 // Workgroup merge of the NW waves' (m, l, O) and the final store.
 // o_lds[w][n][d] holds each wave's unnormalised output for head n.
 // ---------------------------------------------------------------------------
-template <int D, int NW>
-struct MergeLds {
-  float m[NW][16];
-  float l[NW][16];
-  float o[NW][16][D + 1];
-  int last;  // this workgroup holds the final ticket of its unit
+// Where a kernel keeps each wave's partial in LDS: output row n of wave w at
+// o + w * stride + n * (D + 1), its running max and sum at m / l + w * stride + n.
+struct MergeView {
+  float* o;
+  float* m;
+  float* l;
+  int stride;  // floats between consecutive waves
+  int* last;   // this workgroup holds the final ticket of its unit
+};
+
+template <int D>
+struct WavePartial {
+  float o[16][D + 1];
+  float m[16];
+  float l[16];
 };
 
 template <int D, int NW>
-__device__ void merge_and_store(const SplitParams& prm, MergeLds<D, NW>& lds, int b, int h0,
+struct MergeLds {
+  WavePartial<D> wp[NW];
+  int last;
+  __device__ MergeView view() {
+    constexpr int stride = sizeof(WavePartial<D>) / 4;
+    return MergeView{&wp[0].o[0][0], &wp[0].m[0], &wp[0].l[0], stride, &last};
+  }
+};
+
+template <int D, int NW>
+__device__ void merge_and_store(const SplitParams& prm, const MergeView& mv, int b, int h0,
                                 int nh, int split) {
   __syncthreads();
   const int tid = threadIdx.x;
@@ -120,14 +146,14 @@ __device__ void merge_and_store(const SplitParams& prm, MergeLds<D, NW>& lds, in
     const int n = idx / D, d = idx % D;
     float mstar = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) mstar = fmaxf(mstar, lds.m[w][n]);
+    for (int w = 0; w < NW; ++w) mstar = fmaxf(mstar, mv.m[w * mv.stride + n]);
     float o = 0.0f, l = 0.0f;
     if (mstar != -INFINITY) {
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
-        const float f = safe_exp2_diff(lds.m[w][n], mstar);
-        o = fmaf(f, lds.o[w][n][d], o);
-        l = fmaf(f, lds.l[w][n], l);
+        const float f = safe_exp2_diff(mv.m[w * mv.stride + n], mstar);
+        o = fmaf(f, mv.o[w * mv.stride + n * (D + 1) + d], o);
+        l = fmaf(f, mv.l[w * mv.stride + n], l);
       }
     }
     const int64_t row = (int64_t)b * prm.HQ + h0 + n;
@@ -154,10 +180,10 @@ __device__ void merge_and_store(const SplitParams& prm, MergeLds<D, NW>& lds, in
   if (tid == 0) {
     const int t = __hip_atomic_fetch_add(prm.counters + cidx, 1, __ATOMIC_ACQ_REL,
                                          __HIP_MEMORY_SCOPE_AGENT);
-    lds.last = (t == prm.num_splits - 1);
+    *mv.last = (t == prm.num_splits - 1);
   }
   __syncthreads();
-  if (!lds.last) return;
+  if (!*mv.last) return;
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   constexpr int DQ = D / 4;
   const int ns = prm.num_splits;
@@ -240,7 +266,8 @@ __device__ __forceinline__ void load_meta(uint32_t (&mr)[4][MetaStage<NG>::NDW],
     const uint32_t off = NG >= 2 ? (uint32_t)(cb * NG * 2 + 4 * (lane + 64 * k))
                                  : (uint32_t)((cb + lane) * 2);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) mr[t][k] = NG >= 2 ? buf_u32(rm[t], off) : buf_u16(rm[t], off);
+    for (int t = 0; t < 4; ++t)
+      mr[t][k] = NG >= 2 ? buf_u32<kPolMeta>(rm[t], off) : buf_u16<kPolMeta>(rm[t], off);
   }
 }
 
@@ -263,6 +290,96 @@ __device__ __forceinline__ void write_meta(MetaLds<NG>& ml, const uint32_t (&mr)
     } else {
       ml.kz[tok][0] = (uint16_t)mr[1][k];
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Q^T as the B operand of the score MFMAs, in K slot order and pre-scaled by
+// 2^-(slice*KNB), plus the B operand of the K zero-point MFMA.  Lane-group j's
+// dims of step m are the contiguous run [m*KSTEP + CB*j, +CB): one vector load
+// per step, then slot order.  Lanes of heads >= nh hold zeros.
+// ---------------------------------------------------------------------------
+template <int D, int KNB, int GS>
+struct QOperands {
+  u4 qf[KLayout<D, KNB, GS>::NKM];
+  u2 qzb;
+};
+
+template <int D, int KNB, int GS>
+__device__ __forceinline__ void load_q_operands(const SplitParams& prm, int b, int h0, int n, int nh,
+                                                int j, QOperands<D, KNB, GS>& qo) {
+  using KL = KLayout<D, KNB, GS>;
+  constexpr int NG = D / GS;
+  constexpr int NKM = KL::NKM;
+  u4* qf = qo.qf;
+  u2& qzb = qo.qzb;
+  float qz[NG];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) qz[g] = 0.0f;
+  {
+    const bool hv = n < nh;
+    const int64_t qrow = ((int64_t)b * prm.HQ + h0 + (hv ? n : 0)) * D;
+    float qv[NKM][KL::CB];
+    if (prm.q_fp32) {
+      const float* qp = static_cast<const float*>(prm.q) + qrow;
+#pragma unroll
+      for (int m = 0; m < NKM; ++m)
+#pragma unroll
+        for (int c = 0; c < KL::CB; c += 4) {
+          const f4 v = *reinterpret_cast<const f4*>(qp + m * KL::KSTEP + KL::CB * j + c);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) qv[m][c + e] = (float)(_Float16)v[e];
+        }
+    } else {
+      const _Float16* qp = static_cast<const _Float16*>(prm.q) + qrow;
+#pragma unroll
+      for (int m = 0; m < NKM; ++m) {
+        if constexpr (KL::CB == 8) {
+          const h8 v = *reinterpret_cast<const h8*>(qp + m * KL::KSTEP + KL::CB * j);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) qv[m][e] = (float)v[e];
+        } else {
+          const h4 v = *reinterpret_cast<const h4*>(qp + m * KL::KSTEP + KL::CB * j);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) qv[m][e] = (float)v[e];
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < NKM; ++m) {
+      const int p = KL::slice_of(m, j);
+      const float pre = __builtin_ldexpf(1.0f, -p * KNB);
+      uint32_t wv[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int s2 = 0; s2 < KL::CB; s2 += 2) {
+        const float q0 = hv ? qv[m][slot_byte(s2)] : 0.0f;
+        const float q1 = hv ? qv[m][slot_byte(s2 + 1)] : 0.0f;
+        qz[KL::group_of_step(m)] += q0 + q1;
+        wv[s2 / 2] = pack_h2(q0 * pre, q1 * pre);
+      }
+      qf[m] = u4{wv[0], wv[1], wv[2], wv[3]};
+    }
+#pragma unroll
+    for (int g = 0; g < NG; ++g) qz[g] = xor_sum16_32(qz[g]);
+  }
+  // B operand of the K zero-point MFMA: k-slot k < NG holds fp16(Qz_k),
+  // NG <= k < 2NG the fp16 remainder Qz - fp16(Qz), so the product with the
+  // exact fp16 zero points keeps fp32 precision.
+  {
+    float hl[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = 4 * j + i;
+      float v = 0.0f;
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        const float hi16 = (float)(_Float16)qz[g];
+        if (k == g) v = hi16;
+        if (k == NG + g) v = qz[g] - hi16;
+      }
+      hl[i] = v;
+    }
+    qzb = u2{pack_h2(hl[0], hl[1]), pack_h2(hl[2], hl[3])};
   }
 }
 
@@ -335,8 +452,8 @@ quant_split_kernel(SplitParams prm) {
 #pragma unroll
       for (int Lh = 0; Lh < KL::NLOAD; ++Lh) {
         const uint32_t off = kb + 16 * a * KL::DP + (KL::load_offset(Lh, j) - KL::load_offset(0, j));
-        if constexpr (KL::CB == 8) t.kx[a][Lh] = buf_u2(rk, off);
-        else t.kx[a][Lh] = buf_u32(rk, off);
+        if constexpr (KL::CB == 8) t.kx[a][Lh] = buf_u2<kPolQK>(rk, off);
+        else t.kx[a][Lh] = buf_u32<kPolQK>(rk, off);
       }
   };
   auto load_v = [&](Tile& t, int cb) {
@@ -345,7 +462,7 @@ quant_split_kernel(SplitParams prm) {
     for (int i = 0; i < 8; ++i)
 #pragma unroll
       for (int wi = 0; wi < VL::NWIN; ++wi)
-        t.vx[i][wi] = buf_u32(rv, vb + ((i < 4 ? 0 : 12) + i) * VL::DP + VL::W * wi);
+        t.vx[i][wi] = buf_u32<kPolQV>(rv, vb + ((i < 4 ? 0 : 12) + i) * VL::DP + VL::W * wi);
   };
 
   Tile t;
@@ -359,79 +476,10 @@ quant_split_kernel(SplitParams prm) {
   // zero rows g >= NG of this wave's transposed V zero tile (A operand rows)
   for (int idx = lane; idx < (16 - NG) * kChunk; idx += 64) ml.vz[NG + idx / kChunk][idx % kChunk] = 0;
 
-  // ---- Q^T operand in K slot order, pre-scaled by 2^-(slice*KNB) ---------
-  // Lane-group j's dims of step m are the contiguous run
-  // [m*KSTEP + CB*j, +CB): one vector load per step, then slot order.
-  u4 qf[NKM];
-  float qz[NG];
-#pragma unroll
-  for (int g = 0; g < NG; ++g) qz[g] = 0.0f;
-  {
-    const bool hv = n < nh;
-    const int64_t qrow = ((int64_t)b * prm.HQ + h0 + (hv ? n : 0)) * D;
-    float qv[NKM][KL::CB];
-    if (prm.q_fp32) {
-      const float* qp = static_cast<const float*>(prm.q) + qrow;
-#pragma unroll
-      for (int m = 0; m < NKM; ++m)
-#pragma unroll
-        for (int c = 0; c < KL::CB; c += 4) {
-          const f4 v = *reinterpret_cast<const f4*>(qp + m * KL::KSTEP + KL::CB * j + c);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) qv[m][c + e] = (float)(_Float16)v[e];
-        }
-    } else {
-      const _Float16* qp = static_cast<const _Float16*>(prm.q) + qrow;
-#pragma unroll
-      for (int m = 0; m < NKM; ++m) {
-        if constexpr (KL::CB == 8) {
-          const h8 v = *reinterpret_cast<const h8*>(qp + m * KL::KSTEP + KL::CB * j);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) qv[m][e] = (float)v[e];
-        } else {
-          const h4 v = *reinterpret_cast<const h4*>(qp + m * KL::KSTEP + KL::CB * j);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) qv[m][e] = (float)v[e];
-        }
-      }
-    }
-#pragma unroll
-    for (int m = 0; m < NKM; ++m) {
-      const int p = KL::slice_of(m, j);
-      const float pre = __builtin_ldexpf(1.0f, -p * KNB);
-      uint32_t wv[4] = {0, 0, 0, 0};
-#pragma unroll
-      for (int s2 = 0; s2 < KL::CB; s2 += 2) {
-        const float q0 = hv ? qv[m][slot_byte(s2)] : 0.0f;
-        const float q1 = hv ? qv[m][slot_byte(s2 + 1)] : 0.0f;
-        qz[KL::group_of_step(m)] += q0 + q1;
-        wv[s2 / 2] = pack_h2(q0 * pre, q1 * pre);
-      }
-      qf[m] = u4{wv[0], wv[1], wv[2], wv[3]};
-    }
-#pragma unroll
-    for (int g = 0; g < NG; ++g) qz[g] = xor_sum16_32(qz[g]);
-  }
-  // B operand of the K zero-point MFMA: k-slot k < NG holds fp16(Qz_k),
-  // NG <= k < 2NG the fp16 remainder Qz - fp16(Qz), so the product with the
-  // exact fp16 zero points keeps fp32 precision.
-  u2 qzb;
-  {
-    float hl[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int k = 4 * j + i;
-      float v = 0.0f;
-#pragma unroll
-      for (int g = 0; g < NG; ++g) {
-        const float hi16 = (float)(_Float16)qz[g];
-        if (k == g) v = hi16;
-        if (k == NG + g) v = qz[g] - hi16;
-      }
-      hl[i] = v;
-    }
-    qzb = u2{pack_h2(hl[0], hl[1]), pack_h2(hl[2], hl[3])};
-  }
+  QOperands<D, KNB, GS> qo;
+  load_q_operands<D, KNB, GS>(prm, b, h0, n, nh, j, qo);
+  const u4* qf = qo.qf;
+  const u2 qzb = qo.qzb;
 
   // ---- per-lane constants of the V unpack -------------------------------
   uint32_t vsel[VL::NE];
@@ -580,14 +628,438 @@ quant_split_kernel(SplitParams prm) {
       const float fac = kTwo24 * __builtin_ldexpf(1.0f, -VL::slice_of(mv) * VNB);
       const float zv = ozg[VL::group_of(mv)];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) mlds.o[w][n][VL::dim_of(mv, 4 * j + i)] = fmaf(accv[mv][i], fac, zv);
+      for (int i = 0; i < 4; ++i) mlds.wp[w].o[n][VL::dim_of(mv, 4 * j + i)] = fmaf(accv[mv][i], fac, zv);
     }
     if (j == 0) {
-      mlds.m[w][n] = m_run;
-      mlds.l[w][n] = lt;
+      mlds.wp[w].m[n] = m_run;
+      mlds.wp[w].l[n] = lt;
     }
   }
-  merge_and_store<D, NW>(prm, mlds, b, h0, nh, split);
+  merge_and_store<D, NW>(prm, mlds.view(), b, h0, nh, split);
+}
+
+// ===========================================================================
+// Fused quantized split kernel, LDS-staged variant.
+//
+// Every chunk (32 tokens) of K codes, V codes and the four metadata tensors is
+// copied by direct-to-LDS buffer loads (buffer_load_dword{,x4} ... lds) into a
+// per-wave ring of NSTAGE stages, NSTAGE-1 chunks ahead of the compute.  Each
+// load instruction moves whole 16-byte lanes of a contiguous range, so every
+// line of the cache is fetched once with the non-temporal policy, and the
+// prefetch depth costs LDS instead of VGPRs.  The MFMA operands are then
+// gathered from LDS:
+//   K, V codes  stage layout [u][t]: 16-byte unit u of token t's row at
+//               (u * 32 + t) * 16 -- a lane's rows of one unit are 16 bytes
+//               apart, so the operand reads of a wave spread over the banks;
+//   metadata    the global layout [t][g] of each tensor, one dword DMA per
+//               lane; pairs of tokens are gathered with v_perm_b32.
+// The math is that of quant_split_kernel.
+// ===========================================================================
+template <int D, int KNB, int VNB, int GS>
+struct StageGeom {
+  using KL = KLayout<D, KNB, GS>;
+  using VL = VLayout<D, VNB, GS>;
+  static constexpr int NG = D / GS;
+  // fp16 slots per token row of a staged metadata tensor: the global row of NG
+  // values, except NG == 1, whose rows are copied one fp16 per dword (a dword
+  // copy of 2-byte rows could straddle the end of the buffer range).
+  static constexpr int MROW = NG >= 2 ? NG : 2;
+  static constexpr int KB = kChunk * KL::DP;    // K code bytes per chunk
+  static constexpr int VB = kChunk * VL::DP;    // V code bytes per chunk
+  static constexpr int MB = kChunk * MROW * 2;  // bytes of one staged metadata tensor
+  static constexpr int K_OFF = 0;
+  static constexpr int V_OFF = K_OFF + KB;
+  static constexpr int M_OFF = V_OFF + VB;    // ks, kz, vs, vz at M_OFF + t * MB
+  static constexpr int BYTES = M_OFF + 4 * MB;
+  static constexpr int NKI = (KB + 1023) / 1024;  // 16-byte-lane DMA instructions for K
+  static constexpr int NVI = (VB + 1023) / 1024;
+  static constexpr int NMI = (MB + 255) / 256;    // dword-lane DMA instructions per tensor
+  static constexpr int NINSTR = NKI + NVI + 4 * NMI;
+  static_assert(KB % 512 == 0 && VB % 512 == 0 && MB % 64 == 0, "chunk sizes");
+};
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+__device__ __forceinline__ lds_ptr_t to_lds(void* p) {
+  return (lds_ptr_t)(uintptr_t)(uint32_t)(uintptr_t)p;
+}
+
+// Direct-to-LDS buffer loads of 16 / 4 bytes per lane (lane L writes
+// lds + L * size).  Plain functions per cache policy: the builtin is device-only.
+__device__ __forceinline__ void dma16_default(rsrc_t r, lds_ptr_t lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, off, 0, 0, kPolicyDefault);
+}
+__device__ __forceinline__ void dma16_nt(rsrc_t r, lds_ptr_t lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, off, 0, 0, kPolicyNT);
+}
+__device__ __forceinline__ void dma4_default(rsrc_t r, lds_ptr_t lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 4, off, 0, 0, kPolicyDefault);
+}
+__device__ __forceinline__ void dma4_nt(rsrc_t r, lds_ptr_t lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 4, off, 0, 0, kPolicyNT);
+}
+// 2 bytes per lane, zero-extended into a dword at lds + 4 * L.
+__device__ __forceinline__ void dma2_default(rsrc_t r, lds_ptr_t lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 2, off, 0, 0, kPolicyDefault);
+}
+__device__ __forceinline__ void dma2_nt(rsrc_t r, lds_ptr_t lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 2, off, 0, 0, kPolicyNT);
+}
+template <int POL>
+__device__ __forceinline__ void dma16(rsrc_t r, lds_ptr_t lds, uint32_t off) {
+  if constexpr (POL == kPolicyNT) dma16_nt(r, lds, off);
+  else dma16_default(r, lds, off);
+}
+template <int POL>
+__device__ __forceinline__ void dma4(rsrc_t r, lds_ptr_t lds, uint32_t off) {
+  if constexpr (POL == kPolicyNT) dma4_nt(r, lds, off);
+  else dma4_default(r, lds, off);
+}
+template <int POL>
+__device__ __forceinline__ void dma2(rsrc_t r, lds_ptr_t lds, uint32_t off) {
+  if constexpr (POL == kPolicyNT) dma2_nt(r, lds, off);
+  else dma2_default(r, lds, off);
+}
+
+// vmcnt-only wait (gfx9 encoding: vmcnt[3:0] | expcnt 7 | lgkmcnt 15 | vmcnt[5:4]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+__device__ __forceinline__ void wait_lgkmcnt0() {
+  __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));
+}
+
+// Issue the DMA of one chunk into a stage.  `valid` false turns every lane's
+// offset out of the buffer range, so the instructions still retire (keeping
+// the vmcnt arithmetic static) but read nothing and write zeros.
+template <int D, int KNB, int VNB, int GS>
+__device__ __forceinline__ void issue_chunk(uint8_t* stage, const rsrc_t& rk, const rsrc_t& rv,
+                                            const rsrc_t (&rm)[4], int cb, bool valid, int lane) {
+  using SG = StageGeom<D, KNB, VNB, GS>;
+  using KL = typename SG::KL;
+  using VL = typename SG::VL;
+  constexpr uint32_t kOut = 0x80000000u;
+  // K / V: lane L of instruction q fills unit position p = 64q + L, i.e. unit
+  // u = p / 32 of token t = p % 32.
+#pragma unroll
+  for (int q = 0; q < SG::NKI; ++q) {
+    const int p = 64 * q + lane, u = p >> 5, t = p & 31;
+    const uint32_t off = valid ? (uint32_t)(cb + t) * KL::DP + 16 * u : kOut;
+    if (SG::KB >= 1024 || lane < SG::KB / 16)
+      dma16<kPolDma>(rk, to_lds(stage + SG::K_OFF + 1024 * q), off);
+  }
+#pragma unroll
+  for (int q = 0; q < SG::NVI; ++q) {
+    const int p = 64 * q + lane, u = p >> 5, t = p & 31;
+    const uint32_t off = valid ? (uint32_t)(cb + t) * VL::DP + 16 * u : kOut;
+    if (SG::VB >= 1024 || lane < SG::VB / 16)
+      dma16<kPolDma>(rv, to_lds(stage + SG::V_OFF + 1024 * q), off);
+  }
+  // metadata: the chunk's [t][g] rows are contiguous; lane L copies dword L
+  // (NG == 1: the fp16 of token L, into dword L).
+#pragma unroll
+  for (int tsr = 0; tsr < 4; ++tsr)
+#pragma unroll
+    for (int q = 0; q < SG::NMI; ++q) {
+      uint8_t* dst = stage + SG::M_OFF + tsr * SG::MB + 256 * q;
+      if constexpr (SG::NG == 1) {
+        const uint32_t off = valid ? (uint32_t)(cb + lane) * 2 : kOut;
+        if (lane < kChunk) dma2<kPolDma>(rm[tsr], to_lds(dst), off);
+      } else {
+        const uint32_t off = valid ? (uint32_t)cb * SG::NG * 2 + 4 * (64 * q + lane) : kOut;
+        if (SG::MB >= 256 || lane < SG::MB / 4) dma4<kPolDma>(rm[tsr], to_lds(dst), off);
+      }
+    }
+}
+
+template <int D, int KNB, int VNB, int GS, int NW, int NSTAGE>
+struct LdsKernelSmem {
+  using SG = StageGeom<D, KNB, VNB, GS>;
+  static constexpr int RING = NSTAGE * SG::BYTES;
+  // After the loop the ring holds the wave's partial (and, in wave 0, the
+  // workgroup's combine ticket flag right behind it).
+  static constexpr int OUT = (int)sizeof(WavePartial<D>) + 16;
+  static constexpr int WAVE = ((RING > OUT ? RING : OUT) + 15) / 16 * 16;
+};
+
+template <int D, int KNB, int VNB, int GS, int NW, int NSTAGE>
+__global__ void __launch_bounds__(NW * 64)
+quant_split_lds_kernel(SplitParams prm) {
+  using SG = StageGeom<D, KNB, VNB, GS>;
+  using KL = typename SG::KL;
+  using VL = typename SG::VL;
+  using SM = LdsKernelSmem<D, KNB, VNB, GS, NW, NSTAGE>;
+  constexpr int NG = SG::NG;
+  constexpr int NKM = KL::NKM;
+  constexpr int NVM = VL::NVM;
+  constexpr int NI = SG::NINSTR;
+  static_assert(2 * NG <= 16, "zero-point MFMA holds hi/lo of at most 8 groups");
+  static_assert((NSTAGE - 1) * NI < 64, "vmcnt range");
+
+  __shared__ __attribute__((aligned(16))) uint8_t smem[NW * SM::WAVE];
+
+  const int split = blockIdx.x;
+  const int unit = blockIdx.y;
+  const int b = unit / prm.HKV, hk = unit % prm.HKV;
+  const int hb0 = blockIdx.z * 16;
+  const int nh = min(16, prm.G - hb0);
+  const int h0 = hk * prm.G + hb0;
+  const int L = prm.seq_lens ? min(prm.seq_lens[b], prm.S) : prm.S;
+  const int lo = split * prm.split_size;
+  const int hi = min(lo + prm.split_size, L);
+  const int last = hi - 1;
+
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int r = lane & 15, j = lane >> 4;
+  const int n = r;
+  const int64_t row0 = (int64_t)unit * prm.S;
+  const rsrc_t rk = make_rsrc(prm.k + row0 * KL::DP, (uint32_t)prm.S * KL::DP);
+  const rsrc_t rv = make_rsrc(prm.v + row0 * VL::DP, (uint32_t)prm.S * VL::DP);
+  const rsrc_t rm[4] = {make_rsrc(prm.ks + row0 * NG, (uint32_t)prm.S * NG * 2),
+                        make_rsrc(prm.kz + row0 * NG, (uint32_t)prm.S * NG * 2),
+                        make_rsrc(prm.vs + row0 * NG, (uint32_t)prm.S * NG * 2),
+                        make_rsrc(prm.vz + row0 * NG, (uint32_t)prm.S * NG * 2)};
+  uint8_t* ring = smem + w * SM::WAVE;
+
+  // Chunk k of this wave starts at token lo + 32 * (w + NW * k).
+  const int cb0 = lo + kChunk * w;
+  const int cstride = kChunk * NW;
+#pragma unroll
+  for (int k = 0; k < NSTAGE - 1; ++k) {
+    const int cb = cb0 + k * cstride;
+    issue_chunk<D, KNB, VNB, GS>(ring + k * SG::BYTES, rk, rv, rm, cb, cb < hi, lane);
+  }
+
+  QOperands<D, KNB, GS> qo;
+  load_q_operands<D, KNB, GS>(prm, b, h0, n, nh, j, qo);
+  const u4* qf = qo.qf;
+  const u2 qzb = qo.qzb;
+
+  uint32_t vsel[VL::NE];
+#pragma unroll
+  for (int e = 0; e < VL::NE; ++e) vsel[e] = VL::perm_sel(VL::byte_in_dword(e, r));
+  uint32_t kmask[NKM];
+#pragma unroll
+  for (int m = 0; m < NKM; ++m) kmask[m] = slice_mask<KNB>(KL::slice_of(m, j));
+
+  // Per-lane LDS byte offsets inside a stage.
+  // K operand of tile a, load Lh: row 16a + r, byte load_offset(Lh, j).
+  uint32_t koff[KL::NLOAD];
+#pragma unroll
+  for (int Lh = 0; Lh < KL::NLOAD; ++Lh) {
+    const int ob = KL::load_offset(Lh, j);
+    koff[Lh] = SG::K_OFF + ((ob >> 4) * 32 + r) * 16 + (ob & 15);
+  }
+  // V operand of slot i, window wi: token slot_token(j, i), dword dword_offset(wi, r).
+  uint32_t voff[VL::NWIN];
+#pragma unroll
+  for (int wi = 0; wi < VL::NWIN; ++wi) {
+    const int ob = VL::dword_offset(wi, r);
+    voff[wi] = SG::V_OFF + ((ob >> 4) * 32 + 4 * j) * 16 + (ob & 15);
+  }
+  // V zero point rows r < NG of the zero MFMA's A operand, zeros for r >= NG.
+  // Lane r < NG gathers group r's zero points of two tokens into one fp16
+  // pair with a single v_perm (low or high half of each token's dword); the
+  // selector of lanes r >= NG yields constant zero bytes.
+  const int zr = r < NG ? r : 0;
+  const uint32_t zsel = r < NG ? ((r & 1) ? 0x07060302u : 0x05040100u) : 0x0C0C0C0Cu;
+
+  f4 accv[NVM];
+#pragma unroll
+  for (int mv = 0; mv < NVM; ++mv) accv[mv] = f4{0.f, 0.f, 0.f, 0.f};
+  f4 oz = f4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.0f;
+  const float lscale = prm.qk_scale * kTwo24;
+
+  auto half_at = [&](const uint8_t* base, int idx) -> uint32_t {  // fp16 bits of element idx
+    return *reinterpret_cast<const uint16_t*>(base + 2 * idx);
+  };
+  // The dword holding element (t, g) of a staged [t][MROW] metadata tensor.
+  auto dword_at = [&](const uint8_t* base, int t, int g) -> uint32_t {
+    return *reinterpret_cast<const uint32_t*>(base + 2 * (t * SG::MROW + (g & ~1)));
+  };
+
+  // Chunk k of the wave uses stage k % NSTAGE; the loop below is unrolled by
+  // NSTAGE so every stage offset is a compile-time constant.
+  auto step = [&](int cb, auto tail, auto stage) {
+    constexpr bool TAIL = decltype(tail)::value;
+    constexpr int SK = decltype(stage)::value;
+    // refill the stage consumed by the previous chunk, NSTAGE-1 chunks ahead
+    {
+      const int cn = cb + (NSTAGE - 1) * cstride;
+      wait_lgkmcnt0();  // the previous chunk's LDS reads of that stage are done
+      asm volatile("" ::: "memory");
+      issue_chunk<D, KNB, VNB, GS>(ring + ((SK + NSTAGE - 1) % NSTAGE) * SG::BYTES, rk, rv, rm, cn,
+                                   !TAIL && cn < hi, lane);
+    }
+    wait_vmcnt<(NSTAGE - 1) * NI>();
+    asm volatile("" ::: "memory");  // no LDS read of this stage above the wait
+    const uint8_t* st = ring + SK * SG::BYTES;
+    const uint8_t* mks = st + SG::M_OFF;
+    const uint8_t* mkz = mks + SG::MB;
+    const uint8_t* mvs = mkz + SG::MB;
+    const uint8_t* mvz = mvs + SG::MB;
+
+    // ---- scores S^T for the two 16-token tiles ---------------------------
+    float x[8];
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      f4 c[NG];
+#pragma unroll
+      for (int g = 0; g < NG; ++g) c[g] = f4{0.f, 0.f, 0.f, 0.f};
+      typename std::conditional<KL::CB == 8, u2, uint32_t>::type kx[KL::NLOAD];
+#pragma unroll
+      for (int Lh = 0; Lh < KL::NLOAD; ++Lh) {
+        if constexpr (KL::CB == 8) kx[Lh] = *reinterpret_cast<const u2*>(st + koff[Lh] + 256 * a);
+        else kx[Lh] = *reinterpret_cast<const uint32_t*>(st + koff[Lh] + 256 * a);
+      }
+#pragma unroll
+      for (int m = 0; m < NKM; ++m) {
+        const int g = KL::group_of_step(m);
+        if constexpr (KL::CB == 8)
+          c[g] = mfma_k32(k_extract8(kx[KL::load_of_step(m)], kmask[m]), qf[m], c[g]);
+        else
+          c[g] = mfma_k16(k_extract4(kx[KL::load_of_step(m)], kmask[m]), u2{qf[m][0], qf[m][1]}, c[g]);
+      }
+      // zero-point part: A row = token 16a + r, k-slots = its NG zero points
+      u2 za;
+      {
+        const uint8_t* zr = mkz + (16 * a + r) * SG::MROW * 2;
+        if constexpr (NG == 8) {
+          const u4 z8 = *reinterpret_cast<const u4*>(zr);
+          za = (j & 1) ? u2{z8[2], z8[3]} : u2{z8[0], z8[1]};
+        } else if constexpr (NG == 4) {
+          za = *reinterpret_cast<const u2*>(zr);
+        } else if constexpr (NG == 2) {
+          const uint32_t z2 = *reinterpret_cast<const uint32_t*>(zr);
+          za = u2{z2, z2};
+        } else {
+          const uint32_t z1 = *reinterpret_cast<const uint16_t*>(zr);
+          za = u2{z1 | (z1 << 16), 0u};
+        }
+      }
+      const f4 yz = mfma_k16(za, qzb, f4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * a + 4 * j + i;
+        float sc = yz[i] * kTwoM24;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          const float sv = (float)__builtin_bit_cast(_Float16, (uint16_t)half_at(mks, t * SG::MROW + g));
+          sc = fmaf(sv, c[g][i], sc);
+        }
+        x[4 * a + i] = sc;
+      }
+    }
+    if constexpr (TAIL) {
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (cb + 16 * a + 4 * j + i > last) x[4 * a + i] = -INFINITY;
+    }
+
+    // ---- online softmax ---------------------------------------------------
+    float alpha;
+    ChunkProbs pr;
+    if (softmax_chunk(x, lscale, m_run, l_run, alpha, pr)) {
+#pragma unroll
+      for (int mv = 0; mv < NVM; ++mv) accv[mv] *= alpha;
+      oz *= alpha;
+    }
+    const u4 pb = u4{pr.ph[0], pr.ph[1], pr.ph[2], pr.ph[3]};
+
+    // ---- V zero point: oz += Z^T P (A rows = groups, k = the lane's 8 tokens)
+    {
+      uint32_t zp[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int t0 = slot_token(j, 2 * q), t1 = slot_token(j, 2 * q + 1);
+        zp[q] = perm(dword_at(mvz, t1, zr), dword_at(mvz, t0, zr), zsel);
+      }
+      oz = mfma_k32(u4{zp[0], zp[1], zp[2], zp[3]}, pb, oz);
+    }
+    // ---- P'_g = P * s_g ------------------------------------------------------
+    u4 pg[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      uint32_t sp[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int t0 = slot_token(j, 2 * q), t1 = slot_token(j, 2 * q + 1);
+        sp[q] = perm(dword_at(mvs, t1, g), dword_at(mvs, t0, g), (g & 1) ? 0x07060302u : 0x05040100u);
+      }
+      pg[g] = u4{pk_mul(pb[0], sp[0]), pk_mul(pb[1], sp[1]), pk_mul(pb[2], sp[2]), pk_mul(pb[3], sp[3])};
+    }
+
+    // ---- O^T += V^T P'^T ---------------------------------------------------
+#pragma unroll
+    for (int wi = 0; wi < VL::NWIN; ++wi) {
+      uint32_t vx[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        vx[i] = *reinterpret_cast<const uint32_t*>(st + voff[wi] + 16 * ((i < 4 ? 0 : 12) + i));
+#pragma unroll
+      for (int e = 0; e < VL::NE; ++e) {
+        uint32_t pm[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pm[i] = perm(vx[2 * i + 1], vx[2 * i], vsel[e]);
+#pragma unroll
+        for (int p = 0; p < VL::P; ++p) {
+          const int mv = VL::mfma_index(p, wi, e);
+          const uint32_t msk = slice_mask<VNB>(p);
+          const u4 av = u4{pm[0] & msk, pm[1] & msk, pm[2] & msk, pm[3] & msk};
+          accv[mv] = mfma_k32(av, pg[VL::group_of(mv)], accv[mv]);
+        }
+      }
+    }
+  };
+
+  // Pairs of full chunks (stages 0 and 1), then what is left: at most one
+  // full chunk and the split's partial last chunk.  A single loop exit keeps
+  // the accumulators in place across the unrolled copies.
+  static_assert(NSTAGE == 2, "the chunk loop is unrolled for a two-stage ring");
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  int cb = cb0;
+  for (; cb + cstride + kChunk <= hi; cb += 2 * cstride) {
+    step(cb, std::false_type{}, S0{});
+    step(cb + cstride, std::false_type{}, S1{});
+  }
+  if (cb + kChunk <= hi) {
+    step(cb, std::false_type{}, S0{});
+    if (cb + cstride < hi) step(cb + cstride, std::true_type{}, S1{});
+  } else if (cb < hi) {
+    step(cb, std::true_type{}, S0{});
+  }
+  wait_vmcnt<0>();  // retire the trailing (out-of-range) prefetches
+  wave_lds_fence();
+
+  // ---- this wave's partial into its own ring region -------------------------
+  WavePartial<D>& wp = *reinterpret_cast<WavePartial<D>*>(ring);
+  {
+    const float lt = xor_sum16_32(l_run);
+    float ozg[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) ozg[g] = __shfl(oz[g % 4], 16 * (g / 4) + n, 64);
+#pragma unroll
+    for (int mv = 0; mv < NVM; ++mv) {
+      const float fac = kTwo24 * __builtin_ldexpf(1.0f, -VL::slice_of(mv) * VNB);
+      const float zv = ozg[VL::group_of(mv)];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wp.o[n][VL::dim_of(mv, 4 * j + i)] = fmaf(accv[mv][i], fac, zv);
+    }
+    if (j == 0) {
+      wp.m[n] = m_run;
+      wp.l[n] = lt;
+    }
+  }
+  WavePartial<D>& wp0 = *reinterpret_cast<WavePartial<D>*>(smem);
+  const MergeView view{&wp0.o[0][0], &wp0.m[0], &wp0.l[0], SM::WAVE / 4,
+                       reinterpret_cast<int*>(smem + sizeof(WavePartial<D>))};
+  merge_and_store<D, NW>(prm, view, b, h0, nh, split);
 }
 
 // ===========================================================================
@@ -639,7 +1111,7 @@ fp16_split_kernel(SplitParams prm) {
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
-      for (int m = 0; m < NKM; ++m) t.kx[a][m] = buf_u4(rk, kb + (16 * a * D + 32 * m) * 2);
+      for (int m = 0; m < NKM; ++m) t.kx[a][m] = buf_u4<kPolF16>(rk, kb + (16 * a * D + 32 * m) * 2);
   };
   auto load_v = [&](Tile& t, int cb) {
     const uint32_t vb = vlane + (uint32_t)cb * D * 2;
@@ -647,10 +1119,10 @@ fp16_split_kernel(SplitParams prm) {
     for (int i = 0; i < 8; ++i) {
       const uint32_t o = vb + ((i < 4 ? 0 : 12) + i) * D * 2;
       if constexpr (EPL == 8) {
-        const u4 v4 = buf_u4(rv, o);
+        const u4 v4 = buf_u4<kPolF16>(rv, o);
         t.vx[i][0] = v4[0]; t.vx[i][1] = v4[1]; t.vx[i][2] = v4[2]; t.vx[i][3] = v4[3];
       } else {
-        const u2 v2 = buf_u2(rv, o);
+        const u2 v2 = buf_u2<kPolF16>(rv, o);
         t.vx[i][0] = v2[0]; t.vx[i][1] = v2[1];
       }
     }
@@ -747,13 +1219,13 @@ fp16_split_kernel(SplitParams prm) {
 #pragma unroll
     for (int mv = 0; mv < EPL; ++mv)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) mlds.o[w][n][EPL * (4 * j + i) + mv] = accv[mv][i];
+      for (int i = 0; i < 4; ++i) mlds.wp[w].o[n][EPL * (4 * j + i) + mv] = accv[mv][i];
     if (j == 0) {
-      mlds.m[w][n] = m_run;
-      mlds.l[w][n] = lt;
+      mlds.wp[w].m[n] = m_run;
+      mlds.wp[w].l[n] = lt;
     }
   }
-  merge_and_store<D, NW>(prm, mlds, b, h0, nh, split);
+  merge_and_store<D, NW>(prm, mlds.view(), b, h0, nh, split);
 }
 
 // ===========================================================================
@@ -869,12 +1341,22 @@ static dim3 split_grid(const tkv_decode_args* a) {
   return dim3((unsigned)a->num_splits, (unsigned)(a->B * a->HKV), (unsigned)((G + 15) / 16));
 }
 
+constexpr bool kLdsStaged = true;  // LDS-staged (DMA) kernel instead of register prefetch
+constexpr int kStages = 2;          // its ring depth per wave
+
 template <int D, int KNB, int VNB, int GS>
 static void launch_quant(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
-  if (waves == 8)
-    quant_split_kernel<D, KNB, VNB, GS, 8><<<grid, dim3(8 * 64), 0, st>>>(p);
-  else
-    quant_split_kernel<D, KNB, VNB, GS, 4><<<grid, dim3(4 * 64), 0, st>>>(p);
+  if constexpr (kLdsStaged) {
+    if (waves == 8)
+      quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages><<<grid, dim3(8 * 64), 0, st>>>(p);
+    else
+      quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages><<<grid, dim3(4 * 64), 0, st>>>(p);
+  } else {
+    if (waves == 8)
+      quant_split_kernel<D, KNB, VNB, GS, 8><<<grid, dim3(8 * 64), 0, st>>>(p);
+    else
+      quant_split_kernel<D, KNB, VNB, GS, 4><<<grid, dim3(4 * 64), 0, st>>>(p);
+  }
 }
 
 template <int D, int KNB, int VNB>

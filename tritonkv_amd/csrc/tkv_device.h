@@ -117,17 +117,26 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                            0x00020000);
 }
+
+// Cache-policy operand of a load (bit 1 = NT, non-temporal, on gfx94x/gfx950).
+constexpr int kPolicyDefault = 0;
+constexpr int kPolicyNT = 2;
+
+template <int POL = kPolicyDefault>
 __device__ __forceinline__ uint32_t buf_u32(rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, POL);
 }
+template <int POL = kPolicyDefault>
 __device__ __forceinline__ u2 buf_u2(rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+  return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, POL);
 }
+template <int POL = kPolicyDefault>
 __device__ __forceinline__ u4 buf_u4(rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, POL);
 }
+template <int POL = kPolicyDefault>
 __device__ __forceinline__ uint32_t buf_u16(rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, POL);
 }
 
 // Global loads of 4/8/16 bytes through the vector memory path.
