@@ -79,6 +79,7 @@ struct ChunkProbs {
   float p[8];
 };
 
+template <bool TRACK_L = true>
 __device__ __forceinline__ bool softmax_chunk(const float (&x)[8], float lscale, float& m,
                                               float& l, float& alpha, ChunkProbs& out) {
   float mx = x[0];
@@ -92,15 +93,15 @@ __device__ __forceinline__ bool softmax_chunk(const float (&x)[8], float lscale,
     const float mn = fmaxf(m, mx);
     alpha = safe_exp2_diff(m, mn);
     m = mn;
-    l *= alpha;
+    if constexpr (TRACK_L) l *= alpha;
   }
   float sum = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     out.p[i] = __builtin_amdgcn_exp2f(fmaf(x[i], lscale, -m));
-    sum += out.p[i];
+    if constexpr (TRACK_L) sum += out.p[i];
   }
-  l += sum;
+  if constexpr (TRACK_L) l += sum;
 #pragma unroll
   for (int i = 0; i < 4; ++i) out.ph[i] = pack_h2(out.p[2 * i], out.p[2 * i + 1]);
   return any_moved;
@@ -832,6 +833,7 @@ quant_split_lds_kernel(SplitParams prm) {
     issue_chunk<D, KNB, VNB, GS>(ring + k * SG::BYTES, rk, rv, rm, cb, cb < hi, lane);
   }
 
+
   QOperands<D, KNB, GS> qo;
   load_q_operands<D, KNB, GS>(prm, b, h0, n, nh, j, qo);
   const u4* qf = qo.qf;
@@ -843,6 +845,8 @@ quant_split_lds_kernel(SplitParams prm) {
   uint32_t kmask[NKM];
 #pragma unroll
   for (int m = 0; m < NKM; ++m) kmask[m] = slice_mask<KNB>(KL::slice_of(m, j));
+
+  constexpr bool kVChain = NG == 1;  // all slices of a V byte in one group
 
   // Per-lane LDS byte offsets inside a stage.
   // K operand of tile a, load Lh: row 16a + r, byte load_offset(Lh, j).
@@ -863,8 +867,12 @@ quant_split_lds_kernel(SplitParams prm) {
   // Lane r < NG gathers group r's zero points of two tokens into one fp16
   // pair with a single v_perm (low or high half of each token's dword); the
   // selector of lanes r >= NG yields constant zero bytes.
+  // Row NG of that operand is all ones (fp16 1.0 pairs), so the same MFMA also
+  // accumulates sum_t p_t, the softmax denominator, from the very fp16
+  // probabilities the PV products use.
   const int zr = r < NG ? r : 0;
   const uint32_t zsel = r < NG ? ((r & 1) ? 0x07060302u : 0x05040100u) : 0x0C0C0C0Cu;
+  const uint32_t zones = r == NG ? 0x3C003C00u : 0u;
 
   f4 accv[NVM];
 #pragma unroll
@@ -964,7 +972,7 @@ quant_split_lds_kernel(SplitParams prm) {
     // ---- online softmax ---------------------------------------------------
     float alpha;
     ChunkProbs pr;
-    if (softmax_chunk(x, lscale, m_run, l_run, alpha, pr)) {
+    if (softmax_chunk<false>(x, lscale, m_run, l_run, alpha, pr)) {
 #pragma unroll
       for (int mv = 0; mv < NVM; ++mv) accv[mv] *= alpha;
       oz *= alpha;
@@ -977,7 +985,7 @@ quant_split_lds_kernel(SplitParams prm) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int t0 = slot_token(j, 2 * q), t1 = slot_token(j, 2 * q + 1);
-        zp[q] = perm(dword_at(mvz, t1, zr), dword_at(mvz, t0, zr), zsel);
+        zp[q] = perm(dword_at(mvz, t1, zr), dword_at(mvz, t0, zr), zsel) | zones;
       }
       oz = mfma_k32(u4{zp[0], zp[1], zp[2], zp[3]}, pb, oz);
     }
@@ -1006,11 +1014,18 @@ quant_split_lds_kernel(SplitParams prm) {
         uint32_t pm[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) pm[i] = perm(vx[2 * i + 1], vx[2 * i], vsel[e]);
+        // With one group per row (NG == 1) every slice of a byte shares the
+        // same P', so slice p's MFMA may take the byte with only the slices
+        // below p cleared (p = 0: the raw byte): its accumulator holds the
+        // codes of slices >= p at their bit positions, and slice p alone is
+        // recovered after the loop as acc[p] - acc[p + 1] -- one AND fewer
+        // per byte pair.  Otherwise each slice is isolated by its own mask.
 #pragma unroll
         for (int p = 0; p < VL::P; ++p) {
           const int mv = VL::mfma_index(p, wi, e);
-          const uint32_t msk = slice_mask<VNB>(p);
-          const u4 av = u4{pm[0] & msk, pm[1] & msk, pm[2] & msk, pm[3] & msk};
+          const uint32_t msk = kVChain ? hi_slices_mask<VNB>(p) : slice_mask<VNB>(p);
+          const u4 av = (kVChain && p == 0) ? u4{pm[0], pm[1], pm[2], pm[3]}
+                                            : u4{pm[0] & msk, pm[1] & msk, pm[2] & msk, pm[3] & msk};
           accv[mv] = mfma_k32(av, pg[VL::group_of(mv)], accv[mv]);
         }
       }
@@ -1040,16 +1055,19 @@ quant_split_lds_kernel(SplitParams prm) {
   // ---- this wave's partial into its own ring region -------------------------
   WavePartial<D>& wp = *reinterpret_cast<WavePartial<D>*>(ring);
   {
-    const float lt = xor_sum16_32(l_run);
+    const float lt = __shfl(oz[NG % 4], 16 * (NG / 4) + n, 64);  // the ones row
     float ozg[NG];
 #pragma unroll
     for (int g = 0; g < NG; ++g) ozg[g] = __shfl(oz[g % 4], 16 * (g / 4) + n, 64);
 #pragma unroll
     for (int mv = 0; mv < NVM; ++mv) {
-      const float fac = kTwo24 * __builtin_ldexpf(1.0f, -VL::slice_of(mv) * VNB);
+      const int p = VL::slice_of(mv);
+      const float fac = kTwo24 * __builtin_ldexpf(1.0f, -p * VNB);
       const float zv = ozg[VL::group_of(mv)];
+      f4 a = accv[mv];
+      if (kVChain && p + 1 < VL::P) a -= accv[VL::mfma_index(p + 1, VL::window_of(mv), VL::e_of(mv))];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) wp.o[n][VL::dim_of(mv, 4 * j + i)] = fmaf(accv[mv][i], fac, zv);
+      for (int i = 0; i < 4; ++i) wp.o[n][VL::dim_of(mv, 4 * j + i)] = fmaf(a[i], fac, zv);
     }
     if (j == 0) {
       wp.m[n] = m_run;

@@ -55,6 +55,12 @@ __device__ __forceinline__ constexpr uint32_t slice_mask(int p) {
   return ((((1u << NBITS) - 1u) << (p * NBITS)) * 0x00010001u);
 }
 
+// Bits of slices p.. of every byte held in the low byte of each fp16 half.
+template <int NBITS>
+__device__ __forceinline__ constexpr uint32_t hi_slices_mask(int p) {
+  return ((0xFFu << (p * NBITS)) & 0xFFu) * 0x00010001u;
+}
+
 // Slot order of the four bytes of a dword after extraction: slots 0,1 come
 // from bytes 0,2 and slots 2,3 from bytes 1,3.
 __device__ __forceinline__ constexpr int slot_byte(int s) {
