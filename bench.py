@@ -198,7 +198,7 @@ def fused_call(q, kq, vq, num_splits=None, split_only=False, waves=None, fused_c
         _lib.check(fn(args, torch.cuda.current_stream().cuda_stream), "fused")
     call.keep = (out, acc, mx, sm, cnt, q, kq, vq)
     call.num_splits = ns
-    call.kernel = (f"quant_split_kernel<{D}, {kq.nbits}, {vq.nbits}, {kq.group_size}, {wv}>")
+    call.kernel = (f"quant_split_lds_kernel<{D}, {kq.nbits}, {vq.nbits}, {kq.group_size}, {wv}, 2>")
     return call
 
 
@@ -226,6 +226,29 @@ def fp16_call(q, k, v, num_splits=None, split_only=False, waves=None, fused_comb
         _lib.check(fn(args, torch.cuda.current_stream().cuda_stream), "fp16")
     call.keep = (out, acc, mx, sm, cnt, q, k, v)
     call.num_splits = ns
+    return call
+
+
+def torch_nosplit_call(q, k, v):
+    """No-split fp16 baseline in plain torch: one batched GEMM for the scores
+    (K pre-transposed once, outside the timed region, so the right operand is
+    contiguous), an fp32 softmax, one batched GEMM for the output."""
+    import torch
+
+    B, HQ, D = q.shape
+    _, HKV, S, _ = k.shape
+    G = HQ // HKV
+    kT = k.transpose(-1, -2).contiguous()  # (B, HKV, D, S)
+    vc = v.contiguous()
+    qg = q.view(B, HKV, G, D)
+    scale = D ** -0.5
+
+    def call():
+        s = torch.matmul(qg, kT)  # (B, HKV, G, S)
+        p = torch.softmax(s.float() * scale, dim=-1).half()
+        return torch.matmul(p, vc).view(B, HQ, D)
+    call.keep = (q, kT, vc)
+    call.num_splits = 1
     return call
 
 
@@ -393,6 +416,121 @@ def cpu_baseline(q, kq, vq, budget_s):
                        f"one decode step ({t_spent:.1f} s), extrapolated x{units_total / done:.1f}")}
 
 
+def cpu_config1(reps=50):
+    """the reference's CPU decode step at the Qwen shape,
+    ctx 512 -- dequantise K, V (4-bit gs32) to fp32, then fp32 attention -- as
+    restated by the oracle (numpy dequantise, torch CPU attention), timed on
+    this host with all its cores and with one thread; median of ``reps``."""
+    import numpy as np
+    import torch
+
+    from oracle import inputs as oinp
+    from oracle import quant as oq
+
+    q, k, v = oinp.make_random_kv(1, 12, 2, 512, 128, seed=0, outlier_frac=0.0)
+    kq, vq = oq.quantize_kv(k.numpy(), v.numpy(), 4, 32)
+    qf = torch.from_numpy(q.float().numpy())
+
+    def step():
+        kd = torch.from_numpy(oq.dequantize_groupwise(kq))
+        vd = torch.from_numpy(oq.dequantize_groupwise(vq))
+        kd = kd.repeat_interleave(6, dim=1)
+        vd = vd.repeat_interleave(6, dim=1)
+        s_ = torch.einsum("bhd,bhsd->bhs", qf, kd) * (128 ** -0.5)
+        return torch.einsum("bhs,bhsd->bhd", torch.softmax(s_, dim=-1), vd)
+
+    out = {}
+    threads0 = torch.get_num_threads()
+    ncores = len(os.sched_getaffinity(0))
+    for name, nt in (("all_cores", ncores), ("one_thread", 1)):
+        torch.set_num_threads(nt)
+        for _ in range(5):
+            step()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter_ns()
+            step()
+            ts.append((time.perf_counter_ns() - t0) / 1e3)
+        ts.sort()
+        out[name] = {"us_median": round(statistics.median(ts), 1),
+                     "us_iqr": round(ts[3 * len(ts) // 4] - ts[len(ts) // 4], 1), "threads": nt}
+    torch.set_num_threads(threads0)
+    try:
+        cpu = next(ln.split(":", 1)[1].strip() for ln in open("/proc/cpuinfo") if ln.startswith("model name"))
+    except (OSError, StopIteration):
+        cpu = "unknown"
+    out["cpu"] = cpu
+    out["sample"] = ("Qwen2.5-1.5B attention, B=1 HQ=12 HKV=2 D=128 ctx=512, N(0,1) fp16 q/K/V seed 0, "
+                     "4-bit gs32 split-P; numpy dequantise + torch CPU fp32 attention")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# 70B-style ragged batch (BASELINE.json config 5)
+# ---------------------------------------------------------------------------
+
+
+def ragged_70b(steps, warmup, seed=2024):
+    """B=64, HQ=64, HKV=8, D=128; per-sequence length S_b ~ U[1024, 131072]
+    (seeded); K 4-bit / V 2-bit, group 32.  One step appends one new token per
+    sequence (GPU quantize + pack of K and V at position S_b) and then decodes
+    over S_b + 1 tokens.  Storage is padded to 131072 + 64 tokens; only the
+    sum of S_b + 1 counts as cache bytes."""
+    import torch
+
+    from tritonkv_amd.kernels import fused_decode_attention
+    from tritonkv_amd.quantize import QuantizedTensor, append_kv, cache_row_bytes, empty_cache
+
+    B, HQ, HKV, D, gs, cap = 64, 64, 8, 128, 32, 131072 + 64
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(1024, 131072 + 1, (B,), generator=g, dtype=torch.int32)
+    kc = empty_cache(B, HKV, cap, D, 4, gs, "cuda")
+    vc = empty_cache(B, HKV, cap, D, 2, gs, "cuda")
+    gd = torch.Generator(device="cuda").manual_seed(seed + 1)
+    for b in range(B):
+        for cache in (kc, vc):
+            x = torch.randn(1, HKV, int(lens[b]), D, device="cuda", generator=gd, dtype=torch.float16)
+            append_kv(QuantizedTensor(cache.packed[b:b + 1], cache.scale[b:b + 1], cache.zero[b:b + 1],
+                                      cache.nbits, gs, D), x)
+            del x
+    q = torch.randn(B, HQ, D, device="cuda", generator=gd, dtype=torch.float16)
+    k_new = torch.randn(B, HKV, 1, D, device="cuda", generator=gd, dtype=torch.float16)
+    v_new = torch.randn(B, HKV, 1, D, device="cuda", generator=gd, dtype=torch.float16)
+    pos = lens.to("cuda")
+    lens1 = (lens + 1).to("cuda")
+    out = torch.empty(B, HQ, D, device="cuda")
+    ws = {}
+
+    def decode():
+        fused_decode_attention(q, kc, vc, seq_lens=lens1, allow_mixed_bits=True, out=out, _workspace=ws)
+
+    def step():
+        append_kv(kc, k_new, pos)
+        append_kv(vc, v_new, pos)
+        decode()
+
+    torch.cuda.synchronize()
+    row = cache_row_bytes(D, 4, gs) + cache_row_bytes(D, 2, gs)
+    tokens = int(lens1.sum())
+    decode_bytes = tokens * HKV * row + B * HQ * D * (2 + 4)
+    append_bytes = B * HKV * (2 * D * 2 + row)
+    us, _, _ = timed_steps([step], steps, warmup)
+    dus, _, _ = timed_steps([decode], steps, warmup)
+    total = decode_bytes + append_bytes
+    res = {"us_per_step": round(us, 2), "decode_us": round(dus, 2),
+           "append_us": round(us - dus, 2), "sum_tokens": tokens,
+           "algorithmic_bytes": total,
+           "gbps_step": round(total / us / 1e3, 1),
+           "frac_of_hbm_peak_step": round(total / us / 1e3 / HBM_PEAK_GBS, 4),
+           "frac_of_hbm_peak_decode": round(decode_bytes / dus / 1e3 / HBM_PEAK_GBS, 4),
+           "lengths": "S_b ~ U[1024, 131072], torch.Generator().manual_seed(%d)" % seed}
+    print(f"# ragged 70b K4/V2: step {us:.1f} us (decode {dus:.1f} us), "
+          f"{total / us / 1e3:.0f} GB/s", file=sys.stderr, flush=True)
+    del kc, vc, ws
+    torch.cuda.empty_cache()
+    return res
+
+
 # ---------------------------------------------------------------------------
 # Qwen2.5-1.5B table (BASELINE.json configs 2 and 3)
 # ---------------------------------------------------------------------------
@@ -409,8 +547,8 @@ def qwen_table(ctxs=(512, 2048, 8192, 16384)):
     for S in ctxs:
         g = torch.Generator(device="cuda").manual_seed(1000 + S)
         q = torch.randn(B, HQ, D, device="cuda", generator=g, dtype=torch.float16)
-        for method in ("fused4", "fused2", "fp16"):
-            nbits = {"fused4": 4, "fused2": 2, "fp16": 16}[method]
+        for method in ("fused4", "fused2", "fp16", "fp16_nosplit", "torch_fp16"):
+            nbits = {"fused4": 4, "fused2": 2}.get(method, 16)
             cache, step_bytes = algorithmic_bytes(B, HQ, HKV, S, D, nbits, nbits, gs)
             R = replicas_for(cache)
             kv = torch.randn(2, R, B, HKV, S, D, device="cuda", generator=g, dtype=torch.float16)
@@ -418,6 +556,12 @@ def qwen_table(ctxs=(512, 2048, 8192, 16384)):
             if method == "fp16":
                 for i in range(R):
                     calls.append(fp16_call(q, kv[0, i], kv[1, i]))
+            elif method == "fp16_nosplit":
+                for i in range(R):
+                    calls.append(fp16_call(q, kv[0, i], kv[1, i], num_splits=1))
+            elif method == "torch_fp16":
+                for i in range(R):
+                    calls.append(torch_nosplit_call(q, kv[0, i], kv[1, i]))
             else:
                 kq = quantize_groupwise(kv[0], nbits, gs)
                 vq = quantize_groupwise(kv[1], nbits, gs)
@@ -439,9 +583,16 @@ def qwen_table(ctxs=(512, 2048, 8192, 16384)):
             del calls
             torch.cuda.empty_cache()
     by = {(r["ctx"], r["method"]): r for r in rows}
-    effects = {str(S): {"quant_effect_cold_4b": round(by[(S, "fp16")]["cold_us"] / by[(S, "fused4")]["cold_us"], 3),
-                        "quant_effect_cold_2b": round(by[(S, "fp16")]["cold_us"] / by[(S, "fused2")]["cold_us"], 3),
-                        "quant_effect_hot_4b": round(by[(S, "fp16")]["hot_us"] / by[(S, "fused4")]["hot_us"], 3)}
+
+    def ratio(S, num, den, col):
+        return round(by[(S, num)][col] / by[(S, den)][col], 3)
+
+    effects = {str(S): {"quant_effect_cold_4b": ratio(S, "fp16", "fused4", "cold_us"),
+                        "quant_effect_cold_2b": ratio(S, "fp16", "fused2", "cold_us"),
+                        "quant_effect_hot_4b": ratio(S, "fp16", "fused4", "hot_us"),
+                        "flash_decode_effect_cold_vs_torch": ratio(S, "torch_fp16", "fp16", "cold_us"),
+                        "flash_decode_effect_cold_vs_nosplit": ratio(S, "fp16_nosplit", "fp16", "cold_us"),
+                        "flash_decode_effect_hot_vs_torch": ratio(S, "torch_fp16", "fp16", "hot_us")}
                for S in ctxs}
     return {"rows": rows, "effects": effects}
 
@@ -472,14 +623,14 @@ def main() -> int:
     B, HQ, HKV, S, D, gs = 32, 32, 8, 32768, 128, 32
     detail = {}
 
-    def build_copies(nbits):
+    def build_copies(nbits, g_s=gs):
         out = []
         for c in range(2):
             q, k, v = llama_inputs(seed=10 + c)
             if nbits == 16:
                 out.append((q, k, v))
             else:
-                kq, vq = quantize_kv(k, v, nbits, gs)
+                kq, vq = quantize_kv(k, v, nbits, g_s)
                 del k, v
                 out.append((q, kq, vq))
         torch.cuda.synchronize()
@@ -511,13 +662,15 @@ def main() -> int:
     if not a.quick and not a.no_cpu_baseline:
         q0, kq0, vq0 = copies4[0]
         cpu = cpu_baseline(q0, kq0, vq0, a.cpu_seconds)
+        cpu["config1_reference_cpu_step"] = cpu_config1()
     del steps4, split4, copies4
     torch.cuda.empty_cache()
 
     if not a.quick:
-        for nbits, name in ((2, "fused2"), (16, "fp16")):
-            cps = build_copies(nbits)
-            cache, nbytes = algorithmic_bytes(B, HQ, HKV, S, D, nbits, nbits, gs)
+        for nbits, g_s, name in ((2, 32, "fused2"), (16, 32, "fp16"), (4, 128, "fused4_gs128"),
+                                 (2, 128, "fused2_gs128")):
+            cps = build_copies(nbits, g_s)
+            cache, nbytes = algorithmic_bytes(B, HQ, HKV, S, D, nbits, nbits, g_s)
             mk = fp16_call if nbits == 16 else fused_call
             us, _, _ = timed_steps([mk(*c) for c in cps], a.steps, a.warmup)
             sp, _, _ = timed_steps([mk(*c, split_only=True) for c in cps], a.steps, a.warmup)
@@ -532,6 +685,7 @@ def main() -> int:
         detail["quant_effect_2b"] = round(detail["fp16"]["us_per_step"] / detail["fused2"]["us_per_step"], 3)
         detail["empty_graph_node_us"] = round(empty_kernel_floor() * 1e3, 2)
         detail["qwen2.5-1.5b"] = qwen_table()
+        detail["ragged_70b_k4v2"] = ragged_70b(a.steps, a.warmup)
 
     line = {
         "metric": METRIC,

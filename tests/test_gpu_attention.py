@@ -233,6 +233,78 @@ def test_ragged_sequence_lengths():
         assert_close_to_reference(got, ref, f"ragged ns={ns}")
 
 
+def test_append_then_decode_ragged_batch():
+    """The 70B-style decode step at reduced size: per-row lengths, K 4-bit /
+    V 2-bit, one new token appended by the GPU quantizer at position S_b, then
+    attention over S_b + 1 tokens -- against the oracle on the caches the step
+    produced, and with the appended rows checked against the oracle quantizer."""
+    from tritonkv_amd.quantize import QuantizedTensor, append_kv, empty_cache
+
+    B, HQ, HKV, D, gs, cap = 4, 32, 4, 128, 32, 3072
+    lens = torch.tensor([3000, 1, 1234, 2047], dtype=torch.int32)
+    q, k, v = oinp.make_random_kv(B, HQ, HKV, cap, D, seed=23)
+    q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
+    kc = empty_cache(B, HKV, cap, D, 4, gs, DEV)
+    vc = empty_cache(B, HKV, cap, D, 2, gs, DEV)
+    for t in (kc.packed, vc.packed, kc.scale, kc.zero, vc.scale, vc.zero):
+        t.view(torch.uint8).fill_(0xFF)  # never-written slots: fp16 NaN scale/zero
+    for b in range(B):
+        L = int(lens[b])
+        for cache, x in ((kc, k), (vc, v)):
+            view = QuantizedTensor(cache.packed[b:b + 1], cache.scale[b:b + 1], cache.zero[b:b + 1],
+                                   cache.nbits, gs, D)
+            append_kv(view, x[b:b + 1, :, :L].contiguous())
+    k_new = k[:, :, -1:].contiguous()
+    v_new = v[:, :, -1:].contiguous()
+    append_kv(kc, k_new, lens.to(DEV))
+    append_kv(vc, v_new, lens.to(DEV))
+    lens1 = lens + 1
+    for ns in (None, 1, 7):
+        got = _fused(q, kc, vc, seq_lens=lens1.to(DEV), allow_mixed_bits=True, num_splits=ns)
+        assert torch.isfinite(got).all(), ns
+        clean = []
+        for cache in (kc, vc):  # the oracle sees zeros where the kernel saw NaN garbage
+            c = QuantizedTensor(cache.packed.clone(), cache.scale.clone(), cache.zero.clone(),
+                                cache.nbits, gs, D)
+            for b in range(B):
+                L = int(lens1[b])
+                c.packed[b, :, L:] = 0
+                c.scale[b, :, L:] = 0
+                c.zero[b, :, L:] = 0
+            clean.append(c)
+        ref = oracle_attention_on_quant(q, clean[0], clean[1], seq_lens=lens1.numpy())
+        assert_close_to_reference(got, ref, f"append + ragged decode ns={ns}")
+    # the appended token of every row is what the oracle quantizer makes of it
+    for cache, x in ((kc, k_new), (vc, v_new)):
+        want = oq.quantize_groupwise(x.cpu().numpy(), cache.nbits, gs)
+        for b in range(B):
+            L = int(lens[b])
+            assert np.array_equal(cache.packed[b, :, L].cpu().numpy(), want.packed[b, :, 0])
+            assert np.array_equal(cache.scale[b, :, L].cpu().numpy().view(np.uint16),
+                                  want.scale[b, :, 0].view(np.uint16))
+            assert np.array_equal(cache.zero[b, :, L].cpu().numpy().view(np.uint16),
+                                  want.zero[b, :, 0].view(np.uint16))
+
+
+def test_fp16_control_ignores_nan_rows_past_each_length():
+    from tritonkv_amd.kernels import fp16_decode_attention
+
+    B, HQ, HKV, S, D = 3, 16, 2, 700, 128
+    q, k, v = oinp.make_random_kv(B, HQ, HKV, S, D, seed=29)
+    lens = torch.tensor([700, 45, 333], dtype=torch.int32)
+    kg, vg = k.clone(), v.clone()
+    for b in range(B):
+        kg[b, :, int(lens[b]):] = float("nan")
+        vg[b, :, int(lens[b]):] = float("inf")
+    for ns in (None, 1, 5):
+        got = fp16_decode_attention(q.to(DEV), kg.to(DEV), vg.to(DEV), seq_lens=lens.to(DEV),
+                                    num_splits=ns).cpu().numpy()
+        assert np.isfinite(got).all(), ns
+        ref = oatt.reference_decode_attention_f64(q.float().numpy(), k.float().numpy(),
+                                                  v.float().numpy(), seq_lens=lens.numpy())
+        assert np.abs(got - ref).max() <= 2e-3, ns
+
+
 @pytest.mark.parametrize("S", [1, 17, 1000, 8192, 16384])
 @pytest.mark.parametrize("shape", [(1, 12, 2, 128), (2, 32, 8, 64)])
 def test_fp16_control_matches_fp32_reference(S, shape):

@@ -24,9 +24,9 @@
 //   * Online softmax in base 2 (logit = score * sm_scale * log2 e), wave-level
 //     max via cross-lane shuffles; the rescale of the accumulators is skipped
 //     when no head's running max moved.
-//   * Per-token scale/zero rows of each chunk are staged in LDS by one
-//     coalesced load per lane; the partial (m, l, acc) of the NW waves is
-//     merged in LDS and written once per workgroup.
+//   * Each chunk's codes and scale/zero rows reach LDS by direct-to-LDS loads
+//     (quantized kernel) or registers (fp16 control); the partial (m, l, acc)
+//     of the NW waves is merged in LDS and written once per workgroup.
 #include <type_traits>
 
 #include "tkv_codec.h"
@@ -55,9 +55,6 @@ struct SplitParams {
 constexpr int kChunk = 32;  // tokens per wave iteration (two 16-row MFMA tiles)
 
 // Cache policies of the streamed loads.
-constexpr int kPolQK = kPolicyDefault;   // quantized K codes
-constexpr int kPolQV = kPolicyDefault;   // quantized V codes
-constexpr int kPolMeta = kPolicyDefault; // scale / zero rows
 constexpr int kPolF16 = kPolicyNT;       // fp16 control K and V rows
 constexpr int kPolDma = kPolicyNT;       // LDS-staged kernel: K/V code and metadata ranges
 
@@ -218,81 +215,6 @@ __device__ __forceinline__ void wave_lds_fence() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-__device__ __forceinline__ u2 lds_u2(const uint16_t* p) { return *reinterpret_cast<const u2*>(p); }
-
-// ---------------------------------------------------------------------------
-// Per-wave LDS staging of a chunk's fp16 scale/zero metadata.
-//
-// Four tensors per chunk (K scale, K zero, V scale, V zero), each 32 tokens x
-// NG groups.  Every lane loads its dwords of each tensor one chunk ahead, into
-// registers, and writes them at the start of the chunk's compute in the layout
-// its consumer reads with one ds_read_b64:
-//   ks [g][tok]   K scale, transposed -- the fold reads 4 consecutive tokens of a group
-//   kz [tok][g]   K zero, token rows  -- A operand (token rows) of the K zero MFMA
-//   vs [g][tok]   V scale, transposed -- P'_g = P * s_g pairs of consecutive tokens
-//   vz [16][tok]  V zero, transposed, rows g >= NG zero -- A operand of the V zero MFMA
-// ---------------------------------------------------------------------------
-template <int NG>
-struct MetaLds {
-  uint16_t ks[NG][kChunk];
-  uint16_t kz[kChunk][NG < 2 ? 2 : NG];
-  uint16_t vs[NG][kChunk];
-  uint16_t vz[16][kChunk];
-};
-
-template <int NG>
-struct MetaStage {
-  // dwords of one tensor a lane carries: 16*NG dwords over 64 lanes (NG >= 2),
-  // or one fp16 for lanes < 32 (NG == 1).
-  static constexpr int NDW = NG >= 2 ? (kChunk * NG / 2 + 63) / 64 : 1;
-  static constexpr int DW = NG >= 2 ? NG / 2 : 1;  // dwords per token row
-  __device__ static bool active(int lane, int k) {
-    return NG >= 2 ? (lane + 64 * k) < kChunk * DW : lane < kChunk;
-  }
-  __device__ static int token(int lane, int k) { return NG >= 2 ? (lane + 64 * k) / DW : lane; }
-  __device__ static int group0(int lane, int k) { return NG >= 2 ? 2 * ((lane + 64 * k) % DW) : 0; }
-};
-
-// Load one chunk's metadata dwords of the 4 tensors through their buffer
-// resources (one per tensor, covering this (b, kv head) block).  A chunk's
-// rows are contiguous, so lane l reads dword l (+64k) of the chunk; rows past
-// the block end read as 0.
-template <int NG>
-__device__ __forceinline__ void load_meta(uint32_t (&mr)[4][MetaStage<NG>::NDW],
-                                          const rsrc_t (&rm)[4], int cb, int lane) {
-  using MS = MetaStage<NG>;
-#pragma unroll
-  for (int k = 0; k < MS::NDW; ++k) {
-    if (!MS::active(lane, k)) continue;
-    const uint32_t off = NG >= 2 ? (uint32_t)(cb * NG * 2 + 4 * (lane + 64 * k))
-                                 : (uint32_t)((cb + lane) * 2);
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-      mr[t][k] = NG >= 2 ? buf_u32<kPolMeta>(rm[t], off) : buf_u16<kPolMeta>(rm[t], off);
-  }
-}
-
-template <int NG>
-__device__ __forceinline__ void write_meta(MetaLds<NG>& ml, const uint32_t (&mr)[4][MetaStage<NG>::NDW],
-                                           int lane) {
-  using MS = MetaStage<NG>;
-#pragma unroll
-  for (int k = 0; k < MS::NDW; ++k) {
-    if (!MS::active(lane, k)) continue;
-    const int tok = MS::token(lane, k), g = MS::group0(lane, k);
-    ml.ks[g][tok] = (uint16_t)mr[0][k];
-    ml.vs[g][tok] = (uint16_t)mr[2][k];
-    ml.vz[g][tok] = (uint16_t)mr[3][k];
-    if constexpr (NG >= 2) {
-      ml.ks[g + 1][tok] = (uint16_t)(mr[0][k] >> 16);
-      ml.vs[g + 1][tok] = (uint16_t)(mr[2][k] >> 16);
-      ml.vz[g + 1][tok] = (uint16_t)(mr[3][k] >> 16);
-      *reinterpret_cast<uint32_t*>(&ml.kz[tok][g]) = mr[1][k];
-    } else {
-      ml.kz[tok][0] = (uint16_t)mr[1][k];
-    }
-  }
-}
 
 // ---------------------------------------------------------------------------
 // Q^T as the B operand of the score MFMAs, in K slot order and pre-scaled by
@@ -386,261 +308,6 @@ __device__ __forceinline__ void load_q_operands(const SplitParams& prm, int b, i
 
 // ===========================================================================
 // Fused quantized split kernel.
-// ===========================================================================
-template <int D, int KNB, int VNB, int GS>
-struct QuantTile {
-  using KL = KLayout<D, KNB, GS>;
-  using VL = VLayout<D, VNB, GS>;
-  using KX = typename std::conditional<KL::CB == 8, u2, uint32_t>::type;
-  KX kx[2][KL::NLOAD];
-  uint32_t vx[8][VL::NWIN];
-  uint32_t meta[4][MetaStage<D / GS>::NDW];
-};
-
-template <int D, int KNB, int VNB, int GS, int NW>
-__global__ void __launch_bounds__(NW * 64)
-quant_split_kernel(SplitParams prm) {
-  using KL = KLayout<D, KNB, GS>;
-  using VL = VLayout<D, VNB, GS>;
-  using Tile = QuantTile<D, KNB, VNB, GS>;
-  constexpr int NG = D / GS;
-  constexpr int NKM = KL::NKM;
-  constexpr int NVM = VL::NVM;
-  static_assert(2 * NG <= 16, "zero-point MFMA holds hi/lo of at most 8 groups");
-
-  __shared__ MergeLds<D, NW> mlds;
-  __shared__ MetaLds<NG> meta[NW];
-
-  const int split = blockIdx.x;
-  const int unit = blockIdx.y;
-  const int b = unit / prm.HKV, hk = unit % prm.HKV;
-  const int hb0 = blockIdx.z * 16;
-  const int nh = min(16, prm.G - hb0);
-  const int h0 = hk * prm.G + hb0;
-  const int L = prm.seq_lens ? min(prm.seq_lens[b], prm.S) : prm.S;
-  const int lo = split * prm.split_size;
-  const int hi = min(lo + prm.split_size, L);
-  const int last = hi - 1;
-
-  // The wave index is wave-uniform; saying so lets every chunk address live in
-  // SGPRs and the loads use the scalar-base + lane-offset form.
-  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int r = lane & 15, j = lane >> 4;  // MFMA row/col index and lane-group
-  const int n = r;                         // query head (column) of this lane
-  const int64_t row0 = (int64_t)unit * prm.S;  // first cache row of this (b, kv head)
-  // Buffer resources over this (b, kv head) block: tokens >= S read as 0.
-  const rsrc_t rk = make_rsrc(prm.k + row0 * KL::DP, (uint32_t)prm.S * KL::DP);
-  const rsrc_t rv = make_rsrc(prm.v + row0 * VL::DP, (uint32_t)prm.S * VL::DP);
-  const rsrc_t rm[4] = {make_rsrc(prm.ks + row0 * NG, (uint32_t)prm.S * NG * 2),
-                        make_rsrc(prm.kz + row0 * NG, (uint32_t)prm.S * NG * 2),
-                        make_rsrc(prm.vs + row0 * NG, (uint32_t)prm.S * NG * 2),
-                        make_rsrc(prm.vz + row0 * NG, (uint32_t)prm.S * NG * 2)};
-  MetaLds<NG>& ml = meta[w];
-
-  // Lane parts of a chunk's K and V code offsets; the per-load remainder is a
-  // compile-time constant that folds into the instruction's offset field.
-  const uint32_t klane = r * KL::DP + KL::load_offset(0, j);  // + 16a*DP + L*KSTEP
-  const uint32_t vlane = 4 * j * VL::DP + 4 * (r / VL::LPD);
-
-  // A chunk's loads, in three parts so each can be reissued for the next chunk
-  // as soon as the current chunk has consumed the registers it fills.  Tail
-  // chunks need no clamping: rows past the split end are masked in the
-  // scores, rows past the block end read as 0.
-  auto load_k = [&](Tile& t, int cb) {
-    const uint32_t kb = klane + (uint32_t)cb * KL::DP;
-#pragma unroll
-    for (int a = 0; a < 2; ++a)
-#pragma unroll
-      for (int Lh = 0; Lh < KL::NLOAD; ++Lh) {
-        const uint32_t off = kb + 16 * a * KL::DP + (KL::load_offset(Lh, j) - KL::load_offset(0, j));
-        if constexpr (KL::CB == 8) t.kx[a][Lh] = buf_u2<kPolQK>(rk, off);
-        else t.kx[a][Lh] = buf_u32<kPolQK>(rk, off);
-      }
-  };
-  auto load_v = [&](Tile& t, int cb) {
-    const uint32_t vb = vlane + (uint32_t)cb * VL::DP;
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int wi = 0; wi < VL::NWIN; ++wi)
-        t.vx[i][wi] = buf_u32<kPolQV>(rv, vb + ((i < 4 ? 0 : 12) + i) * VL::DP + VL::W * wi);
-  };
-
-  Tile t;
-  const int cb0 = lo + kChunk * w;
-  if (cb0 < hi) {  // prologue loads overlap the Q^T setup below
-    load_meta<NG>(t.meta, rm, cb0, lane);
-    load_k(t, cb0);
-    load_v(t, cb0);
-  }
-
-  // zero rows g >= NG of this wave's transposed V zero tile (A operand rows)
-  for (int idx = lane; idx < (16 - NG) * kChunk; idx += 64) ml.vz[NG + idx / kChunk][idx % kChunk] = 0;
-
-  QOperands<D, KNB, GS> qo;
-  load_q_operands<D, KNB, GS>(prm, b, h0, n, nh, j, qo);
-  const u4* qf = qo.qf;
-  const u2 qzb = qo.qzb;
-
-  // ---- per-lane constants of the V unpack -------------------------------
-  uint32_t vsel[VL::NE];
-#pragma unroll
-  for (int e = 0; e < VL::NE; ++e) vsel[e] = VL::perm_sel(VL::byte_in_dword(e, r));
-  uint32_t kmask[NKM];
-#pragma unroll
-  for (int m = 0; m < NKM; ++m) kmask[m] = slice_mask<KNB>(KL::slice_of(m, j));
-
-  f4 accv[NVM];
-#pragma unroll
-  for (int mv = 0; mv < NVM; ++mv) accv[mv] = f4{0.f, 0.f, 0.f, 0.f};
-  f4 oz = f4{0.f, 0.f, 0.f, 0.f};  // sum_t z_V[t][g = 4j+i] P[t][n]
-  float m_run = -INFINITY, l_run = 0.0f;
-  const float lscale = prm.qk_scale * kTwo24;
-
-  // One chunk: stage its metadata in LDS, then compute, reissuing each part
-  // of the next chunk's loads as soon as its registers are free.  The tail
-  // chunk (TAIL) masks the scores of tokens past the split end.
-  auto step = [&](Tile& cur, int cb, auto tail) {
-    constexpr bool TAIL = decltype(tail)::value;
-    const int cn = cb + kChunk * NW;
-    const bool more = !TAIL && cn < hi;
-    wave_lds_fence();  // previous chunk's LDS reads are done
-    write_meta<NG>(ml, cur.meta, lane);
-    if (more) load_meta<NG>(cur.meta, rm, cn, lane);
-    wave_lds_fence();
-
-    // ---- scores S^T for the two 16-token tiles ---------------------------
-    float x[8];
-#pragma unroll
-    for (int a = 0; a < 2; ++a) {
-      f4 c[NG];
-#pragma unroll
-      for (int g = 0; g < NG; ++g) c[g] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int m = 0; m < NKM; ++m) {
-        const int g = KL::group_of_step(m);
-        if constexpr (KL::CB == 8)
-          c[g] = mfma_k32(k_extract8(cur.kx[a][KL::load_of_step(m)], kmask[m]), qf[m], c[g]);
-        else
-          c[g] = mfma_k16(k_extract4(cur.kx[a][KL::load_of_step(m)], kmask[m]),
-                          u2{qf[m][0], qf[m][1]}, c[g]);
-      }
-      // zero-point part: sum_g z[t][g] Qz[g][n] (true units) by one MFMA
-      u2 za;
-      {
-        const uint16_t* zr = ml.kz[16 * a + r];
-        if constexpr (NG == 8) {
-          const u4 z8 = *reinterpret_cast<const u4*>(zr);
-          za = (j & 1) ? u2{z8[2], z8[3]} : u2{z8[0], z8[1]};
-        } else if constexpr (NG == 4) {
-          za = lds_u2(zr);
-        } else if constexpr (NG == 2) {
-          const uint32_t z2 = *reinterpret_cast<const uint32_t*>(zr);
-          za = u2{z2, z2};
-        } else {
-          const uint32_t z1 = zr[0];
-          za = u2{z1 | (z1 << 16), 0u};
-        }
-      }
-      const f4 yz = mfma_k16(za, qzb, f4{0.f, 0.f, 0.f, 0.f});
-      u2 sk[NG];
-#pragma unroll
-      for (int g = 0; g < NG; ++g) sk[g] = lds_u2(&ml.ks[g][16 * a + 4 * j]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float sc = yz[i] * kTwoM24;
-#pragma unroll
-        for (int g = 0; g < NG; ++g) {
-          const float sv = (i & 1) ? half_hi(sk[g][i >> 1]) : half_lo(sk[g][i >> 1]);
-          sc = fmaf(sv, c[g][i], sc);
-        }
-        x[4 * a + i] = sc;
-      }
-    }
-    if constexpr (TAIL) {
-#pragma unroll
-      for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (cb + 16 * a + 4 * j + i > last) x[4 * a + i] = -INFINITY;
-    }
-
-    if (more) load_k(cur, cn);
-
-    // ---- online softmax ---------------------------------------------------
-    float alpha;
-    ChunkProbs pr;
-    if (softmax_chunk(x, lscale, m_run, l_run, alpha, pr)) {
-#pragma unroll
-      for (int mv = 0; mv < NVM; ++mv) accv[mv] *= alpha;
-      oz *= alpha;
-    }
-    const u4 pb = u4{pr.ph[0], pr.ph[1], pr.ph[2], pr.ph[3]};
-
-    // ---- V zero point: oz += Z^T P ------------------------------------------
-    {
-      const u2 z0 = lds_u2(&ml.vz[r][4 * j]);
-      const u2 z1 = lds_u2(&ml.vz[r][16 + 4 * j]);
-      oz = mfma_k32(u4{z0[0], z0[1], z1[0], z1[1]}, pb, oz);
-    }
-    // ---- P'_g = P * s_g ------------------------------------------------------
-    u4 pg[NG];
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      const u2 s0 = lds_u2(&ml.vs[g][4 * j]);
-      const u2 s1 = lds_u2(&ml.vs[g][16 + 4 * j]);
-      pg[g] = u4{pk_mul(pb[0], s0[0]), pk_mul(pb[1], s0[1]), pk_mul(pb[2], s1[0]),
-                 pk_mul(pb[3], s1[1])};
-    }
-
-    // ---- O^T += V^T P'^T ---------------------------------------------------
-#pragma unroll
-    for (int wi = 0; wi < VL::NWIN; ++wi) {
-#pragma unroll
-      for (int e = 0; e < VL::NE; ++e) {
-        uint32_t pm[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) pm[i] = perm(cur.vx[2 * i + 1][wi], cur.vx[2 * i][wi], vsel[e]);
-#pragma unroll
-        for (int p = 0; p < VL::P; ++p) {
-          const int mv = VL::mfma_index(p, wi, e);
-          const uint32_t msk = slice_mask<VNB>(p);
-          const u4 av = u4{pm[0] & msk, pm[1] & msk, pm[2] & msk, pm[3] & msk};
-          accv[mv] = mfma_k32(av, pg[VL::group_of(mv)], accv[mv]);
-        }
-      }
-    }
-    if (more) load_v(cur, cn);
-  };
-
-  // Full chunks, then the split's partial last chunk (if any).
-  int cb = cb0;
-  for (; cb + kChunk <= hi; cb += kChunk * NW) step(t, cb, std::false_type{});
-  if (cb < hi) step(t, cb, std::true_type{});
-
-  // ---- this wave's partial into LDS ---------------------------------------
-  {
-    const float lt = xor_sum16_32(l_run);
-    float ozg[NG];  // Oz[g][n], held by lane-group g/4, element g%4
-#pragma unroll
-    for (int g = 0; g < NG; ++g) ozg[g] = __shfl(oz[g % 4], 16 * (g / 4) + n, 64);
-#pragma unroll
-    for (int mv = 0; mv < NVM; ++mv) {
-      const float fac = kTwo24 * __builtin_ldexpf(1.0f, -VL::slice_of(mv) * VNB);
-      const float zv = ozg[VL::group_of(mv)];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) mlds.wp[w].o[n][VL::dim_of(mv, 4 * j + i)] = fmaf(accv[mv][i], fac, zv);
-    }
-    if (j == 0) {
-      mlds.wp[w].m[n] = m_run;
-      mlds.wp[w].l[n] = lt;
-    }
-  }
-  merge_and_store<D, NW>(prm, mlds.view(), b, h0, nh, split);
-}
-
-// ===========================================================================
-// Fused quantized split kernel, LDS-staged variant.
 //
 // Every chunk (32 tokens) of K codes, V codes and the four metadata tensors is
 // copied by direct-to-LDS buffer loads (buffer_load_dword{,x4} ... lds) into a
@@ -654,7 +321,7 @@ quant_split_kernel(SplitParams prm) {
 //               apart, so the operand reads of a wave spread over the banks;
 //   metadata    the global layout [t][g] of each tensor, one dword DMA per
 //               lane; pairs of tokens are gathered with v_perm_b32.
-// The math is that of quant_split_kernel.
+// Scores, softmax and PV follow the design notes at the top of this file.
 // ===========================================================================
 template <int D, int KNB, int VNB, int GS>
 struct StageGeom {
@@ -881,6 +548,12 @@ quant_split_lds_kernel(SplitParams prm) {
   float m_run = -INFINITY, l_run = 0.0f;
   const float lscale = prm.qk_scale * kTwo24;
 
+  // In the tail chunk, rows past the sequence hold whatever the cache holds
+  // there (possibly NaN/Inf bit patterns in scale/zero): their V scale and
+  // zero-point pairs are cleared, since p = 0 alone would not cancel them.
+  auto tail_pair_mask = [&](int tok0, int tok1) -> uint32_t {
+    return (tok0 <= last ? 0x0000FFFFu : 0u) | (tok1 <= last ? 0xFFFF0000u : 0u);
+  };
   auto half_at = [&](const uint8_t* base, int idx) -> uint32_t {  // fp16 bits of element idx
     return *reinterpret_cast<const uint16_t*>(base + 2 * idx);
   };
@@ -985,7 +658,9 @@ quant_split_lds_kernel(SplitParams prm) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int t0 = slot_token(j, 2 * q), t1 = slot_token(j, 2 * q + 1);
-        zp[q] = perm(dword_at(mvz, t1, zr), dword_at(mvz, t0, zr), zsel) | zones;
+        zp[q] = perm(dword_at(mvz, t1, zr), dword_at(mvz, t0, zr), zsel);
+        if constexpr (TAIL) zp[q] &= tail_pair_mask(cb + t0, cb + t1);
+        zp[q] |= zones;
       }
       oz = mfma_k32(u4{zp[0], zp[1], zp[2], zp[3]}, pb, oz);
     }
@@ -998,6 +673,7 @@ quant_split_lds_kernel(SplitParams prm) {
       for (int q = 0; q < 4; ++q) {
         const int t0 = slot_token(j, 2 * q), t1 = slot_token(j, 2 * q + 1);
         sp[q] = perm(dword_at(mvs, t1, g), dword_at(mvs, t0, g), (g & 1) ? 0x07060302u : 0x05040100u);
+        if constexpr (TAIL) sp[q] &= tail_pair_mask(cb + t0, cb + t1);
       }
       pg[g] = u4{pk_mul(pb[0], sp[0]), pk_mul(pb[1], sp[1]), pk_mul(pb[2], sp[2]), pk_mul(pb[3], sp[3])};
     }
@@ -1216,6 +892,15 @@ fp16_split_kernel(SplitParams prm) {
       for (int mv = 0; mv < EPL; ++mv) accv[mv] *= alpha;
     }
     const u4 pb = u4{pr.ph[0], pr.ph[1], pr.ph[2], pr.ph[3]};
+    if constexpr (TAIL) {
+      // Rows past the sequence are whatever the cache holds there (possibly
+      // NaN/Inf bit patterns); p = 0 alone would not cancel them in the MFMA.
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (cb + slot_token(j, i) > last)
+#pragma unroll
+          for (int e = 0; e < EPL / 2; ++e) cur.vx[i][e] = 0u;
+    }
 #pragma unroll
     for (int mv = 0; mv < EPL; ++mv) {
       const uint32_t sel = (mv & 1) ? 0x07060302u : 0x05040100u;
@@ -1359,22 +1044,14 @@ static dim3 split_grid(const tkv_decode_args* a) {
   return dim3((unsigned)a->num_splits, (unsigned)(a->B * a->HKV), (unsigned)((G + 15) / 16));
 }
 
-constexpr bool kLdsStaged = true;  // LDS-staged (DMA) kernel instead of register prefetch
-constexpr int kStages = 2;          // its ring depth per wave
+constexpr int kStages = 2;  // ring depth per wave of the quantized split kernel
 
 template <int D, int KNB, int VNB, int GS>
 static void launch_quant(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
-  if constexpr (kLdsStaged) {
-    if (waves == 8)
-      quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages><<<grid, dim3(8 * 64), 0, st>>>(p);
-    else
-      quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages><<<grid, dim3(4 * 64), 0, st>>>(p);
-  } else {
-    if (waves == 8)
-      quant_split_kernel<D, KNB, VNB, GS, 8><<<grid, dim3(8 * 64), 0, st>>>(p);
-    else
-      quant_split_kernel<D, KNB, VNB, GS, 4><<<grid, dim3(4 * 64), 0, st>>>(p);
-  }
+  if (waves == 8)
+    quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages><<<grid, dim3(8 * 64), 0, st>>>(p);
+  else
+    quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages><<<grid, dim3(4 * 64), 0, st>>>(p);
 }
 
 template <int D, int KNB, int VNB>
