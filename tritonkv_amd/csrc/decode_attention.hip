@@ -316,9 +316,10 @@ __device__ __forceinline__ void load_q_operands(const SplitParams& prm, int b, i
 // line of the cache is fetched once with the non-temporal policy, and the
 // prefetch depth costs LDS instead of VGPRs.  The MFMA operands are then
 // gathered from LDS:
-//   K, V codes  stage layout [u][t]: 16-byte unit u of token t's row at
-//               (u * 32 + t) * 16 -- a lane's rows of one unit are 16 bytes
-//               apart, so the operand reads of a wave spread over the banks;
+//   K, V codes  blocks of 16 tokens, each block [16-byte unit][token]: every
+//               DMA instruction still copies one contiguous kilobyte, and the
+//               16 rows of an MFMA tile read from one unit are 16 consecutive
+//               entries, so the operand reads spread over the banks;
 //   metadata    the global layout [t][g] of each tensor, one dword DMA per
 //               lane; pairs of tokens are gathered with v_perm_b32.
 // Scores, softmax and PV follow the design notes at the top of this file.
@@ -344,6 +345,24 @@ struct StageGeom {
   static constexpr int NMI = (MB + 255) / 256;    // dword-lane DMA instructions per tensor
   static constexpr int NINSTR = NKI + NVI + 4 * NMI;
   static_assert(KB % 512 == 0 && VB % 512 == 0 && MB % 64 == 0, "chunk sizes");
+
+  // Staged K/V code layout: blocks of 16 tokens, each block [unit][token]:
+  // 16-byte unit u of token t sits at position
+  //   (t / 16) * 16 * NU + 16 * u + t % 16          (NU = DP / 16 units per row)
+  // so a block is one contiguous 16 * DP bytes of the cache, and the 16 rows an
+  // MFMA tile reads from one unit are 16 consecutive 16-byte entries.
+  template <int DP>
+  __device__ static constexpr int pos_of(int t, int u) {
+    return (t >> 4) * 16 * (DP / 16) + 16 * u + (t & 15);
+  }
+  template <int DP>
+  __device__ static constexpr int token_of(int pos) {
+    return 16 * (pos / (16 * (DP / 16))) + (pos & 15);
+  }
+  template <int DP>
+  __device__ static constexpr int unit_of(int pos) {
+    return (pos % (16 * (DP / 16))) >> 4;
+  }
 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -409,18 +428,21 @@ __device__ __forceinline__ void issue_chunk(uint8_t* stage, const rsrc_t& rk, co
   using KL = typename SG::KL;
   using VL = typename SG::VL;
   constexpr uint32_t kOut = 0x80000000u;
-  // K / V: lane L of instruction q fills unit position p = 64q + L, i.e. unit
-  // u = p / 32 of token t = p % 32.
+  // K / V: instruction q copies the contiguous kilobyte [1024q, 1024q + 1024)
+  // of the chunk (whole lines).  Lane L takes the 16-byte unit that belongs at
+  // stage position 64q + L of the layout described at the top of this kernel.
 #pragma unroll
   for (int q = 0; q < SG::NKI; ++q) {
-    const int p = 64 * q + lane, u = p >> 5, t = p & 31;
+    const int t = SG::template token_of<KL::DP>(64 * q + lane);
+    const int u = SG::template unit_of<KL::DP>(64 * q + lane);
     const uint32_t off = valid ? (uint32_t)(cb + t) * KL::DP + 16 * u : kOut;
     if (SG::KB >= 1024 || lane < SG::KB / 16)
       dma16<kPolDma>(rk, to_lds(stage + SG::K_OFF + 1024 * q), off);
   }
 #pragma unroll
   for (int q = 0; q < SG::NVI; ++q) {
-    const int p = 64 * q + lane, u = p >> 5, t = p & 31;
+    const int t = SG::template token_of<VL::DP>(64 * q + lane);
+    const int u = SG::template unit_of<VL::DP>(64 * q + lane);
     const uint32_t off = valid ? (uint32_t)(cb + t) * VL::DP + 16 * u : kOut;
     if (SG::VB >= 1024 || lane < SG::VB / 16)
       dma16<kPolDma>(rv, to_lds(stage + SG::V_OFF + 1024 * q), off);
@@ -521,14 +543,14 @@ quant_split_lds_kernel(SplitParams prm) {
 #pragma unroll
   for (int Lh = 0; Lh < KL::NLOAD; ++Lh) {
     const int ob = KL::load_offset(Lh, j);
-    koff[Lh] = SG::K_OFF + ((ob >> 4) * 32 + r) * 16 + (ob & 15);
+    koff[Lh] = SG::K_OFF + SG::template pos_of<KL::DP>(r, ob >> 4) * 16 + (ob & 15);
   }
   // V operand of slot i, window wi: token slot_token(j, i), dword dword_offset(wi, r).
   uint32_t voff[VL::NWIN];
 #pragma unroll
   for (int wi = 0; wi < VL::NWIN; ++wi) {
     const int ob = VL::dword_offset(wi, r);
-    voff[wi] = SG::V_OFF + ((ob >> 4) * 32 + 4 * j) * 16 + (ob & 15);
+    voff[wi] = SG::V_OFF + SG::template pos_of<VL::DP>(4 * j, ob >> 4) * 16 + (ob & 15);
   }
   // V zero point rows r < NG of the zero MFMA's A operand, zeros for r >= NG.
   // Lane r < NG gathers group r's zero points of two tokens into one fp16
@@ -593,8 +615,10 @@ quant_split_lds_kernel(SplitParams prm) {
       typename std::conditional<KL::CB == 8, u2, uint32_t>::type kx[KL::NLOAD];
 #pragma unroll
       for (int Lh = 0; Lh < KL::NLOAD; ++Lh) {
-        if constexpr (KL::CB == 8) kx[Lh] = *reinterpret_cast<const u2*>(st + koff[Lh] + 256 * a);
-        else kx[Lh] = *reinterpret_cast<const uint32_t*>(st + koff[Lh] + 256 * a);
+        // tile a = rows 16a.. = block a: 16 * NU entries further
+        constexpr int kTile = 16 * (KL::DP / 16) * 16;
+        if constexpr (KL::CB == 8) kx[Lh] = *reinterpret_cast<const u2*>(st + koff[Lh] + kTile * a);
+        else kx[Lh] = *reinterpret_cast<const uint32_t*>(st + koff[Lh] + kTile * a);
       }
 #pragma unroll
       for (int m = 0; m < NKM; ++m) {
@@ -684,7 +708,9 @@ quant_split_lds_kernel(SplitParams prm) {
       uint32_t vx[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i)
-        vx[i] = *reinterpret_cast<const uint32_t*>(st + voff[wi] + 16 * ((i < 4 ? 0 : 12) + i));
+        // slot i: token 4j + i (block 0) or 16 + 4j + i - 4 (block 1)
+        vx[i] = *reinterpret_cast<const uint32_t*>(
+            st + voff[wi] + (i < 4 ? 0 : 16 * (VL::DP / 16) * 16) + 16 * (i & 3));
 #pragma unroll
       for (int e = 0; e < VL::NE; ++e) {
         uint32_t pm[4];
