@@ -62,6 +62,9 @@ def _args():
     ap.add_argument("--kernel", default="quant_split_kernel<128, 4, 4, 32",
                     help="kernel-name substring the summary and traffic figures are for")
     ap.add_argument("--command", default="", help="command line recorded in the summary")
+    ap.add_argument("--regime-probe", choices=("hot", "cold"), default=None,
+                    help="no timing: 60 eager Qwen2.5-1.5B ctx-16384 4-bit decode calls on one "
+                         "cache (hot) or rotating copies >= 768 MB (cold), for rocprofv3 --pmc")
     return ap.parse_args()
 
 
@@ -600,10 +603,41 @@ def qwen_table(ctxs=(512, 2048, 8192, 16384)):
 # ---------------------------------------------------------------------------
 
 
+def regime_probe(mode):
+    """Eager decode calls at the Qwen2.5-1.5B shape, ctx 16384, 4-bit gs32, on one
+    cache ('hot') or on rotating copies totalling >= 768 MB ('cold')."""
+    import torch
+
+    from tritonkv_amd.quantize import QuantizedTensor, quantize_groupwise
+    from tritonkv_amd.timing import replicas_for
+
+    B, HQ, HKV, D, S, gs = 1, 12, 2, 128, 16384, 32
+    g = torch.Generator(device="cuda").manual_seed(7)
+    q = torch.randn(B, HQ, D, device="cuda", generator=g, dtype=torch.float16)
+    cache, _ = algorithmic_bytes(B, HQ, HKV, S, D, 4, 4, gs)
+    R = 1 if mode == "hot" else replicas_for(cache)
+    kv = torch.randn(2, R, B, HKV, S, D, device="cuda", generator=g, dtype=torch.float16)
+    kq, vq = quantize_groupwise(kv[0], 4, gs), quantize_groupwise(kv[1], 4, gs)
+    del kv
+    calls = [fused_call(q, QuantizedTensor(kq.packed[i], kq.scale[i], kq.zero[i], 4, gs, D),
+                        QuantizedTensor(vq.packed[i], vq.scale[i], vq.zero[i], 4, gs, D))
+             for i in range(R)]
+    for c in calls[:min(R, 8)]:
+        c()
+    torch.cuda.synchronize()
+    for i in range(60):
+        calls[i % R]()
+    torch.cuda.synchronize()
+    print(json.dumps({"regime": mode, "replicas": R, "calls": 60}))
+    return 0
+
+
 def main() -> int:
     a = _args()
     if a.rocprof_summary:
         return rocprof_summary(a)
+    if a.regime_probe:
+        return regime_probe(a.regime_probe)
     if a.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU per box; the decode step shards "
                           "by (batch, kv head) with no communication, and no figure at "
