@@ -71,6 +71,14 @@ typedef struct tkv_decode_args {
   int32_t split_size, num_splits;
   int32_t *counters;
   int32_t waves;
+  /* Paged caches (quantized path only): page_size > 0 makes k, k_scale, k_zero,
+   * v, v_scale, v_zero pools laid out (num_pages, HKV, page_size, ...), and
+   * logical page p of batch row b is pool page block_table[b * block_table_stride + p]
+   * (entries outside [0, num_pages) are clamped into the pool).  page_size must
+   * be a multiple of 32 and S == block_table_stride * page_size.  page_size == 0:
+   * contiguous (B, HKV, S, ...) caches and the block table is unused. */
+  const int32_t *block_table;
+  int32_t block_table_stride, page_size, num_pages;
 } tkv_decode_args;
 
 /* Fused 2/4-bit split-P decode attention: the split kernel, then (if
@@ -110,6 +118,20 @@ int tkv_quantize_pack(const void *x, int32_t x_is_fp32, int32_t B, int32_t HKV, 
                       int32_t S_cap, uint8_t *packed, uint16_t *scale, uint16_t *zero,
                       tkv_stream_t stream);
 
+/* tkv_quantize_pack into a paged cache: row b's N tokens go to logical
+ * positions [positions[b], positions[b] + N), i.e. pool page
+ * block_table[b * block_table_stride + t / page_size], slot t % page_size, of
+ * pools laid out (num_pages, HKV, page_size, ...).  Positions past
+ * block_table_stride * page_size, and table entries outside [0, num_pages),
+ * are not written.  No counterpart in the reference (its caches are
+ * contiguous); the paged form of the decode-step append. */
+int tkv_paged_quantize_pack(const void *x, int32_t x_is_fp32, int32_t B, int32_t HKV, int32_t N,
+                            int32_t D, int32_t nbits, int32_t group_size,
+                            const int32_t *positions, const int32_t *block_table,
+                            int32_t block_table_stride, int32_t page_size, int32_t num_pages,
+                            uint8_t *packed, uint16_t *scale, uint16_t *zero,
+                            tkv_stream_t stream);
+
 /* Split-P pack of uint8 codes (rows, D) -> (rows, D/P), as pack_codes
  * (quantize.py:149-169). */
 int tkv_pack_codes(const uint8_t *codes, int64_t rows, int32_t D, int32_t nbits,
@@ -143,7 +165,8 @@ int tkv_device_info(tkv_device_info_t *info);
 /* Human-readable text for a status code returned by any tkv_ function. */
 const char *tkv_status_string(int status);
 
-/* ABI version of this library (bumped on any incompatible change). */
+/* ABI version of this library (bumped on any incompatible change; 3 added the
+ * paged-cache fields of tkv_decode_args and tkv_paged_quantize_pack). */
 int tkv_abi_version(void);
 
 #ifdef __cplusplus

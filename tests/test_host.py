@@ -45,7 +45,7 @@ def test_library_exports_every_declared_symbol():
     for name in _declared_symbols():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.tkv_abi_version() == 2
+    assert lib.tkv_abi_version() == 3
 
 
 def test_library_is_gfx950_only():
@@ -69,11 +69,13 @@ def test_decode_args_layout_matches_c():
     #include <stddef.h>
     #include "tkv.h"
     int main(void) {
-      printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu\n", sizeof(tkv_decode_args),
+      printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\n", sizeof(tkv_decode_args),
              offsetof(tkv_decode_args, q_is_fp32), offsetof(tkv_decode_args, seq_lens),
              offsetof(tkv_decode_args, B), offsetof(tkv_decode_args, sm_scale),
              offsetof(tkv_decode_args, num_splits), offsetof(tkv_decode_args, counters),
-             offsetof(tkv_decode_args, waves), sizeof(tkv_device_info_t));
+             offsetof(tkv_decode_args, waves), offsetof(tkv_decode_args, block_table),
+             offsetof(tkv_decode_args, page_size), offsetof(tkv_decode_args, num_pages),
+             sizeof(tkv_device_info_t));
       return 0;
     }"""
     with tempfile.TemporaryDirectory() as d:
@@ -86,6 +88,7 @@ def test_decode_args_layout_matches_c():
     A = _lib.DecodeArgs
     assert vals == [ctypes.sizeof(A), A.q_is_fp32.offset, A.seq_lens.offset, A.B.offset,
                     A.sm_scale.offset, A.num_splits.offset, A.counters.offset, A.waves.offset,
+                    A.block_table.offset, A.page_size.offset, A.num_pages.offset,
                     ctypes.sizeof(_lib.DeviceInfo)]
 
 
@@ -117,6 +120,22 @@ def test_c_entry_points_reject_bad_arguments_without_a_gpu():
     assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
     a.waves, a.D = 8, 96
     assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EUNSUPPORTED
+    # Paged caches: page size a multiple of 32, a block table covering S exactly.
+    a.D, a.page_size, a.num_pages, a.block_table_stride = 128, 16, 8, 4
+    assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    a.page_size, a.block_table_stride = 32, 2
+    assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL  # no table
+    a.block_table = dummy
+    a.block_table_stride = 3
+    assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL  # 3*32 != S
+    a.block_table_stride = 2
+    assert lib.tkv_fp16_decode_attention(ctypes.byref(a), None) == _lib.TKV_EUNSUPPORTED
+    a.page_size = -32
+    assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    assert lib.tkv_paged_quantize_pack(None, 0, 1, 1, 1, 128, 4, 32, None, None, 1, 32, 1, None,
+                                       None, None, None) == _lib.TKV_EINVAL
+    assert lib.tkv_paged_quantize_pack(dummy, 0, 1, 1, 1, 128, 4, 32, dummy, dummy, 1, 48, 1,
+                                       dummy, dummy, dummy, None) == _lib.TKV_EINVAL
     assert _lib.status_string(_lib.TKV_EINVAL) == "invalid argument"
 
 

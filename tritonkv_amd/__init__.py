@@ -8,7 +8,9 @@ surface:
 * ``tritonkv_amd.kernels``: ``fused_decode_attention``, ``fp16_decode_attention``,
   ``pick_num_splits``, ``triton_available`` (reference ``kernels/__init__.py``);
 * ``tritonkv_amd.quantize``: ``QuantizedTensor`` and the split-P
-  pack/scale/zero layout (reference ``quantize.py``), plus ``append_kv``.
+  pack/scale/zero layout (reference ``quantize.py``), plus ``append_kv``;
+* ``tritonkv_amd.paged``: the same cache format in page pools addressed
+  through a block table (``paged_append``, ``paged_decode_attention``).
 
 The kernels live in ``libtkv_hip.so`` (C ABI in ``include/tkv.h``), built by
 ``python -m tritonkv_amd.build``.  There is no CPU or Triton fallback.

@@ -55,6 +55,10 @@ class DecodeArgs(ctypes.Structure):
         ("num_splits", ctypes.c_int32),
         ("counters", ctypes.c_void_p),
         ("waves", ctypes.c_int32),
+        ("block_table", ctypes.c_void_p),
+        ("block_table_stride", ctypes.c_int32),
+        ("page_size", ctypes.c_int32),
+        ("num_pages", ctypes.c_int32),
     ]
 
 
@@ -84,6 +88,8 @@ SIGNATURES = {
     "tkv_combine_splits": ([_P, _P, _P, _P, _I32, _I32, _I32, _I32, _P], ctypes.c_int),
     "tkv_quantize_pack": ([_P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _P, _I32, _P, _P, _P, _P],
                           ctypes.c_int),
+    "tkv_paged_quantize_pack": ([_P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P, _I32, _I32,
+                                 _I32, _P, _P, _P, _P], ctypes.c_int),
     "tkv_pack_codes": ([_P, _I64, _I32, _I32, _P, _P], ctypes.c_int),
     "tkv_unpack_dequant": ([_P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P], ctypes.c_int),
     "tkv_device_info": ([ctypes.POINTER(DeviceInfo)], ctypes.c_int),

@@ -48,6 +48,11 @@ struct SplitParams {
   float* sums;
   float* out;
   int* counters;  // fused-combine tickets, or null
+  // Paged caches (page_size > 0): the K/V tensors are pools of pages laid out
+  // (num_pages, HKV, page_size, ...); logical page p of batch row b is pool
+  // page block_table[b * bt_stride + p].  S = bt_stride * page_size.
+  const int32_t* block_table;
+  int bt_stride, page_size, num_pages;
   int HQ, HKV, S, G, num_splits, split_size, q_fp32;
   float qk_scale;  // sm_scale * log2(e)
 };
@@ -424,6 +429,7 @@ __device__ __forceinline__ void wait_lgkmcnt0() {
 template <int D, int KNB, int VNB, int GS>
 __device__ __forceinline__ void issue_chunk(uint8_t* stage, const rsrc_t& rk, const rsrc_t& rv,
                                             const rsrc_t (&rm)[4], int cb, bool valid, int lane) {
+  // cb: index, within the resources, of the chunk's first row
   using SG = StageGeom<D, KNB, VNB, GS>;
   using KL = typename SG::KL;
   using VL = typename SG::VL;
@@ -474,7 +480,7 @@ struct LdsKernelSmem {
   static constexpr int WAVE = ((RING > OUT ? RING : OUT) + 15) / 16 * 16;
 };
 
-template <int D, int KNB, int VNB, int GS, int NW, int NSTAGE>
+template <int D, int KNB, int VNB, int GS, int NW, int NSTAGE, bool PAGED>
 __global__ void __launch_bounds__(NW * 64)
 quant_split_lds_kernel(SplitParams prm) {
   using SG = StageGeom<D, KNB, VNB, GS>;
@@ -504,23 +510,49 @@ quant_split_lds_kernel(SplitParams prm) {
   const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int r = lane & 15, j = lane >> 4;
   const int n = r;
-  const int64_t row0 = (int64_t)unit * prm.S;
-  const rsrc_t rk = make_rsrc(prm.k + row0 * KL::DP, (uint32_t)prm.S * KL::DP);
-  const rsrc_t rv = make_rsrc(prm.v + row0 * VL::DP, (uint32_t)prm.S * VL::DP);
-  const rsrc_t rm[4] = {make_rsrc(prm.ks + row0 * NG, (uint32_t)prm.S * NG * 2),
-                        make_rsrc(prm.kz + row0 * NG, (uint32_t)prm.S * NG * 2),
-                        make_rsrc(prm.vs + row0 * NG, (uint32_t)prm.S * NG * 2),
-                        make_rsrc(prm.vz + row0 * NG, (uint32_t)prm.S * NG * 2)};
+  // Where a chunk's rows live.  Contiguous caches: one buffer resource per
+  // tensor over this (b, kv head) block, chunk rows at token index cb.  Paged
+  // caches: resources over the (pool page, kv head) slab holding the chunk
+  // (chunks never straddle a page: page_size % 32 == 0), rows at cb % page.
+  // Either way the hardware range check returns zeros past the resource.
+  struct ChunkSrc {
+    rsrc_t k, v, m[4];
+    int row;
+  };
+  auto slab_src = [&](int64_t slab, int rows, int row) -> ChunkSrc {
+    return ChunkSrc{make_rsrc(prm.k + slab * rows * KL::DP, (uint32_t)rows * KL::DP),
+                    make_rsrc(prm.v + slab * rows * VL::DP, (uint32_t)rows * VL::DP),
+                    {make_rsrc(prm.ks + slab * rows * NG, (uint32_t)rows * NG * 2),
+                     make_rsrc(prm.kz + slab * rows * NG, (uint32_t)rows * NG * 2),
+                     make_rsrc(prm.vs + slab * rows * NG, (uint32_t)rows * NG * 2),
+                     make_rsrc(prm.vz + slab * rows * NG, (uint32_t)rows * NG * 2)},
+                    row};
+  };
+  const ChunkSrc unit_src = slab_src(PAGED ? 0 : (int64_t)unit, PAGED ? prm.page_size : prm.S, 0);
+  // Pool page of logical token cb (the entry is clamped into the pool, so a
+  // bad table entry can only select another page, never leave the pool).
+  auto page_of = [&](int cb) -> int {
+    const int e = prm.block_table[(int64_t)b * prm.bt_stride + cb / prm.page_size];
+    return min(max(e, 0), prm.num_pages - 1);
+  };
+  auto chunk_src = [&](int cb, int page) -> ChunkSrc {
+    if constexpr (PAGED)
+      return slab_src((int64_t)page * prm.HKV + hk, prm.page_size, cb % prm.page_size);
+    else
+      return ChunkSrc{unit_src.k, unit_src.v, {unit_src.m[0], unit_src.m[1], unit_src.m[2], unit_src.m[3]}, cb};
+  };
   uint8_t* ring = smem + w * SM::WAVE;
 
   // Chunk k of this wave starts at token lo + 32 * (w + NW * k).
   const int cb0 = lo + kChunk * w;
   const int cstride = kChunk * NW;
-#pragma unroll
-  for (int k = 0; k < NSTAGE - 1; ++k) {
-    const int cb = cb0 + k * cstride;
-    issue_chunk<D, KNB, VNB, GS>(ring + k * SG::BYTES, rk, rv, rm, cb, cb < hi, lane);
+  static_assert(NSTAGE == 2, "the chunk loop is unrolled for a two-stage ring");
+  {
+    const ChunkSrc src = chunk_src(cb0, PAGED && cb0 < hi ? page_of(cb0) : 0);
+    issue_chunk<D, KNB, VNB, GS>(ring, src.k, src.v, src.m, src.row, cb0 < hi, lane);
   }
+  // Paged: the pool page of the chunk issued next, looked up one step early.
+  int page_next = PAGED && cb0 + cstride < hi ? page_of(cb0 + cstride) : 0;
 
 
   QOperands<D, KNB, GS> qo;
@@ -594,8 +626,11 @@ quant_split_lds_kernel(SplitParams prm) {
       const int cn = cb + (NSTAGE - 1) * cstride;
       wait_lgkmcnt0();  // the previous chunk's LDS reads of that stage are done
       asm volatile("" ::: "memory");
-      issue_chunk<D, KNB, VNB, GS>(ring + ((SK + NSTAGE - 1) % NSTAGE) * SG::BYTES, rk, rv, rm, cn,
-                                   !TAIL && cn < hi, lane);
+      const bool valid = !TAIL && cn < hi;
+      const ChunkSrc src = chunk_src(cn, page_next);
+      issue_chunk<D, KNB, VNB, GS>(ring + ((SK + NSTAGE - 1) % NSTAGE) * SG::BYTES, src.k, src.v,
+                                   src.m, src.row, valid, lane);
+      if constexpr (PAGED) page_next = valid && cn + cstride < hi ? page_of(cn + cstride) : 0;
     }
     wait_vmcnt<(NSTAGE - 1) * NI>();
     asm volatile("" ::: "memory");  // no LDS read of this stage above the wait
@@ -737,7 +772,6 @@ quant_split_lds_kernel(SplitParams prm) {
   // Pairs of full chunks (stages 0 and 1), then what is left: at most one
   // full chunk and the split's partial last chunk.  A single loop exit keeps
   // the accumulators in place across the unrolled copies.
-  static_assert(NSTAGE == 2, "the chunk loop is unrolled for a two-stage ring");
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
   int cb = cb0;
@@ -1035,6 +1069,12 @@ static int validate_common(const tkv_decode_args* a) {
   if (((uintptr_t)a->acc | (uintptr_t)a->out) & 15) return TKV_EINVAL;  // float4 rows
   if (a->waves != 0 && a->waves != 4 && a->waves != 8) return TKV_EINVAL;
   if ((uintptr_t)a->counters & 3) return TKV_EINVAL;
+  if (a->page_size < 0) return TKV_EINVAL;
+  if (a->page_size > 0) {
+    if (a->page_size % 32 || !a->block_table || a->block_table_stride <= 0 || a->num_pages <= 0)
+      return TKV_EINVAL;
+    if ((int64_t)a->block_table_stride * a->page_size != a->S) return TKV_EINVAL;
+  }
   if (a->D != 64 && a->D != 128) return TKV_EUNSUPPORTED;
   return TKV_OK;
 }
@@ -1054,6 +1094,10 @@ static SplitParams make_params(const tkv_decode_args* a) {
   p.sums = a->sums;
   p.out = a->out;
   p.counters = a->counters;
+  p.block_table = a->page_size > 0 ? a->block_table : nullptr;
+  p.bt_stride = a->page_size > 0 ? a->block_table_stride : 0;
+  p.page_size = a->page_size > 0 ? a->page_size : 0;
+  p.num_pages = a->page_size > 0 ? a->num_pages : 0;
   p.HQ = a->HQ;
   p.HKV = a->HKV;
   p.S = a->S;
@@ -1074,10 +1118,14 @@ constexpr int kStages = 2;  // ring depth per wave of the quantized split kernel
 
 template <int D, int KNB, int VNB, int GS>
 static void launch_quant(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
-  if (waves == 8)
-    quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages><<<grid, dim3(8 * 64), 0, st>>>(p);
-  else
-    quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages><<<grid, dim3(4 * 64), 0, st>>>(p);
+  const bool paged = p.page_size > 0;
+  if (waves == 8) {
+    if (paged) quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages, true><<<grid, dim3(8 * 64), 0, st>>>(p);
+    else quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages, false><<<grid, dim3(8 * 64), 0, st>>>(p);
+  } else {
+    if (paged) quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages, true><<<grid, dim3(4 * 64), 0, st>>>(p);
+    else quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages, false><<<grid, dim3(4 * 64), 0, st>>>(p);
+  }
 }
 
 template <int D, int KNB, int VNB>
@@ -1147,6 +1195,7 @@ static int launch_fused_split(const tkv_decode_args* a, hipStream_t st) {
 static int launch_fp16_split(const tkv_decode_args* a, hipStream_t st) {
   const int rc = validate_common(a);
   if (rc) return rc;
+  if (a->page_size > 0) return TKV_EUNSUPPORTED;  // the fp16 control reads contiguous caches
   const SplitParams p = make_params(a);
   const dim3 grid = split_grid(a);
   (void)hipGetLastError();

@@ -14,6 +14,7 @@
 // The arithmetic relies on IEEE binary32 division (hipcc's default correctly
 // rounded fp32 divide -- this file must not be built with fast-math) and on
 // rintf rounding half to even like torch.round.
+#include <stdint.h>
 #include <type_traits>
 
 #include "tkv_codec.h"
@@ -21,11 +22,19 @@
 
 namespace tkv {
 
+// Destination of appended rows in a paged cache (page_size > 0): logical token
+// t of batch row b goes to pool page block_table[b * stride + t / page_size],
+// slot t % page_size; pools are laid out (num_pages, HKV, page_size, ...).
+struct PageMap {
+  const int32_t* block_table;
+  int stride, page_size, num_pages;
+};
+
 // One wave per cache row (token x kv head); lane l holds dims [l*EPL, l*EPL+EPL).
 template <int D, int NB, int GS, bool F32>
 __global__ void __launch_bounds__(256)
 quantize_pack_kernel(const void* __restrict__ x, int64_t rows, int HKV, int N,
-                     const int32_t* __restrict__ positions, int S_cap,
+                     const int32_t* __restrict__ positions, int S_cap, PageMap pm,
                      uint8_t* __restrict__ packed, uint16_t* __restrict__ scale,
                      uint16_t* __restrict__ zero) {
   constexpr int EPL = D / 64;
@@ -40,8 +49,13 @@ quantize_pack_kernel(const void* __restrict__ x, int64_t rows, int HKV, int N,
   const int t = (int)(rr % N);
   const int b = (int)(bh / HKV);
   const int64_t dst_t = (int64_t)(positions ? positions[b] : 0) + t;
-  const bool in_range = dst_t >= 0 && dst_t < S_cap;
-  const int64_t dst_row = bh * S_cap + dst_t;
+  bool in_range = dst_t >= 0 && dst_t < S_cap;
+  int64_t dst_row = bh * S_cap + dst_t;
+  if (pm.page_size > 0 && in_range) {  // S_cap == stride * page_size
+    const int e = pm.block_table[(int64_t)b * pm.stride + dst_t / pm.page_size];
+    in_range = e >= 0 && e < pm.num_pages;  // rows mapped outside the pool are not written
+    dst_row = ((int64_t)e * HKV + bh % HKV) * pm.page_size + dst_t % pm.page_size;
+  }
 
   float xv[EPL];
 #pragma unroll
@@ -213,13 +227,13 @@ unpack_v_kernel(const uint8_t* __restrict__ packed, const uint16_t* __restrict__
 
 template <int D, int NB, int GS>
 static void launch_quantize(const void* x, bool f32, int64_t rows, int HKV, int N,
-                            const int32_t* pos, int S_cap, uint8_t* pk, uint16_t* sc,
+                            const int32_t* pos, int S_cap, PageMap pm, uint8_t* pk, uint16_t* sc,
                             uint16_t* zr, hipStream_t st) {
   const dim3 grid((unsigned)((rows + 3) / 4));
   if (f32)
-    quantize_pack_kernel<D, NB, GS, true><<<grid, 256, 0, st>>>(x, rows, HKV, N, pos, S_cap, pk, sc, zr);
+    quantize_pack_kernel<D, NB, GS, true><<<grid, 256, 0, st>>>(x, rows, HKV, N, pos, S_cap, pm, pk, sc, zr);
   else
-    quantize_pack_kernel<D, NB, GS, false><<<grid, 256, 0, st>>>(x, rows, HKV, N, pos, S_cap, pk, sc, zr);
+    quantize_pack_kernel<D, NB, GS, false><<<grid, 256, 0, st>>>(x, rows, HKV, N, pos, S_cap, pm, pk, sc, zr);
 }
 
 template <int D, int NB, int GS>
@@ -281,9 +295,39 @@ extern "C" int tkv_quantize_pack(const void* x, int32_t x_is_fp32, int32_t B, in
   if ((uintptr_t)x & (x_is_fp32 ? 3 : 1)) return TKV_EINVAL;
   const int64_t rows = (int64_t)B * HKV * N;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const PageMap pm{nullptr, 0, 0, 0};
   (void)hipGetLastError();
 #define TKV_Q(Dv, NBv, GSv) \
-  launch_quantize<Dv, NBv, GSv>(x, x_is_fp32 != 0, rows, HKV, N, positions, S_cap, packed, scale, zero, st)
+  launch_quantize<Dv, NBv, GSv>(x, x_is_fp32 != 0, rows, HKV, N, positions, S_cap, pm, packed, scale, zero, st)
+  TKV_DISPATCH_DNG(D, nbits, group_size, TKV_Q);
+#undef TKV_Q
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? TKV_OK : (int)e;
+}
+
+extern "C" int tkv_paged_quantize_pack(const void* x, int32_t x_is_fp32, int32_t B, int32_t HKV,
+                                       int32_t N, int32_t D, int32_t nbits, int32_t group_size,
+                                       const int32_t* positions, const int32_t* block_table,
+                                       int32_t block_table_stride, int32_t page_size,
+                                       int32_t num_pages, uint8_t* packed, uint16_t* scale,
+                                       uint16_t* zero, tkv_stream_t stream) {
+  using namespace tkv;
+  if (!x || !packed || !scale || !zero || !positions || !block_table) return TKV_EINVAL;
+  if (B <= 0 || HKV <= 0 || N <= 0 || D <= 0) return TKV_EINVAL;
+  if (block_table_stride <= 0 || page_size <= 0 || page_size % 32 || num_pages <= 0)
+    return TKV_EINVAL;
+  if ((int64_t)block_table_stride * page_size > INT32_MAX) return TKV_EINVAL;
+  if (nbits != 2 && nbits != 4) return TKV_EINVAL;
+  if (group_size <= 0 || D % group_size) return TKV_EINVAL;
+  if (((uintptr_t)packed & 3) || ((uintptr_t)scale & 1) || ((uintptr_t)zero & 1)) return TKV_EINVAL;
+  if ((uintptr_t)x & (x_is_fp32 ? 3 : 1)) return TKV_EINVAL;
+  const int64_t rows = (int64_t)B * HKV * N;
+  const int S_cap = block_table_stride * page_size;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const PageMap pm{block_table, block_table_stride, page_size, num_pages};
+  (void)hipGetLastError();
+#define TKV_Q(Dv, NBv, GSv) \
+  launch_quantize<Dv, NBv, GSv>(x, x_is_fp32 != 0, rows, HKV, N, positions, S_cap, pm, packed, scale, zero, st)
   TKV_DISPATCH_DNG(D, nbits, group_size, TKV_Q);
 #undef TKV_Q
   const hipError_t e = hipGetLastError();
