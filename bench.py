@@ -20,7 +20,8 @@ to its own average duration (a graph of split-kernel launches only) and
 MI355X's 8 TB/s HBM peak.  ``cpu_baseline`` times the oracle's scalar C
 restatement of the reference's CPU path on a bounded sample of the same step.
 Unless ``--quick``, the line also carries the 2-bit and fp16-control numbers of
-the same shape and the Qwen2.5-1.5B table of BASELINE.json configs 2-3
+the same shape, the same 4-bit step over shuffled page pools (page sizes 32
+and 256), and the Qwen2.5-1.5B table of BASELINE.json configs 2-3
 (cache-resident and DRAM-resident, ctx 512..16384).
 """
 
@@ -202,6 +203,52 @@ def fused_call(q, kq, vq, num_splits=None, split_only=False, waves=None, fused_c
     call.keep = (out, acc, mx, sm, cnt, q, kq, vq)
     call.num_splits = ns
     call.kernel = (f"quant_split_lds_kernel<{D}, {kq.nbits}, {vq.nbits}, {kq.group_size}, {wv}, 2>")
+    return call
+
+
+def to_pool(qt, page_size, seed):
+    """``qt`` scattered page by page into a pool in random page order, with
+    the block table that maps it back: ``(pool, table)``."""
+    import torch
+
+    from tritonkv_amd.paged import empty_paged_pool
+
+    B, H, S, _ = qt.packed.shape
+    mp = S // page_size
+    g = torch.Generator().manual_seed(seed)
+    table = torch.randperm(B * mp, generator=g).reshape(B, mp).to(torch.int32).to(qt.device)
+    pool = empty_paged_pool(B * mp, H, page_size, qt.head_dim, qt.nbits, qt.group_size, qt.device)
+    for src, dst in ((qt.packed, pool.packed), (qt.scale, pool.scale), (qt.zero, pool.zero)):
+        dst[table.long()] = src.reshape(B, H, mp, page_size, -1).permute(0, 2, 1, 3, 4)
+    return pool, table
+
+
+def paged_call(q, kp, vp, table, split_only=False):
+    import torch
+
+    from tritonkv_amd import _lib
+    from tritonkv_amd.kernels.fused_decode_attn import _workspace_for, choose_waves, plan_splits
+
+    B, HQ, D = q.shape
+    num_pages, HKV, page, _ = kp.packed.shape
+    S = table.shape[1] * page
+    _, ns, size = plan_splits(S, 64, None, B, HKV, HQ // HKV)
+    out = torch.empty(B, HQ, D, device=q.device)
+    acc, mx, sm, _ = _workspace_for({}, B, HQ, ns, D, q.device, HKV)
+    args = _lib.DecodeArgs(
+        q=q.data_ptr(), k=kp.packed.data_ptr(), k_scale=kp.scale.data_ptr(),
+        k_zero=kp.zero.data_ptr(), v=vp.packed.data_ptr(), v_scale=vp.scale.data_ptr(),
+        v_zero=vp.zero.data_ptr(), acc=_lib.ptr(acc), maxs=_lib.ptr(mx), sums=_lib.ptr(sm),
+        out=out.data_ptr(), B=B, HQ=HQ, HKV=HKV, S=S, D=D, k_nbits=kp.nbits, v_nbits=vp.nbits,
+        group_size=kp.group_size, sm_scale=D ** -0.5, split_size=size, num_splits=ns,
+        waves=choose_waves(B, HKV, HQ // HKV, size, ns), block_table=table.data_ptr(),
+        block_table_stride=table.shape[1], page_size=page, num_pages=num_pages)
+    lib = _lib.load()
+    fn = lib.tkv_fused_decode_split if split_only else lib.tkv_fused_decode_attention
+
+    def call():
+        _lib.check(fn(args, torch.cuda.current_stream().cuda_stream), "paged")
+    call.keep = (out, acc, mx, sm, q, kp, vp, table)
     return call
 
 
@@ -697,7 +744,29 @@ def main() -> int:
         q0, kq0, vq0 = copies4[0]
         cpu = cpu_baseline(q0, kq0, vq0, a.cpu_seconds)
         cpu["config1_reference_cpu_step"] = cpu_config1()
-    del steps4, split4, copies4
+    del steps4, split4
+    torch.cuda.empty_cache()
+    if not a.quick:
+        # the same step over page pools in shuffled page order (serving layout)
+        detail["paged4"] = {}
+        for page in (32, 256):
+            pools = []
+            for i, (q, kq, vq) in enumerate(copies4):
+                kp, table = to_pool(kq, page, seed=100 + i)
+                vp, _ = to_pool(vq, page, seed=100 + i)
+                pools.append((q, kp, vp, table))
+            us, _, _ = timed_steps([paged_call(*p) for p in pools], a.steps, a.warmup)
+            sp, _, _ = timed_steps([paged_call(*p, split_only=True) for p in pools], a.steps,
+                                   a.warmup)
+            detail["paged4"][f"page{page}"] = {
+                "us_per_step": round(us, 2), "split_kernel_us": round(sp, 2),
+                "frac_of_hbm_peak": round(bytes4 / sp / 1e3 / HBM_PEAK_GBS, 4),
+                "vs_contiguous_step": round(us / us4, 4)}
+            print(f"# llama 4-bit paged (page {page}, shuffled): step {us:.2f} us, split "
+                  f"{sp:.2f} us", file=sys.stderr, flush=True)
+            del pools
+            torch.cuda.empty_cache()
+    del copies4
     torch.cuda.empty_cache()
 
     if not a.quick:

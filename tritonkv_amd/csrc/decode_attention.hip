@@ -529,17 +529,27 @@ quant_split_lds_kernel(SplitParams prm) {
                     row};
   };
   const ChunkSrc unit_src = slab_src(PAGED ? 0 : (int64_t)unit, PAGED ? prm.page_size : prm.S, 0);
-  // Pool page of logical token cb (the entry is clamped into the pool, so a
-  // bad table entry can only select another page, never leave the pool).
-  auto page_of = [&](int cb) -> int {
-    const int e = prm.block_table[(int64_t)b * prm.bt_stride + cb / prm.page_size];
-    return min(max(e, 0), prm.num_pages - 1);
-  };
   auto chunk_src = [&](int cb, int page) -> ChunkSrc {
     if constexpr (PAGED)
-      return slab_src((int64_t)page * prm.HKV + hk, prm.page_size, cb % prm.page_size);
+      return slab_src((int64_t)page * prm.HKV + hk, prm.page_size,
+                      (int)((uint32_t)cb % (uint32_t)prm.page_size));
     else
       return ChunkSrc{unit_src.k, unit_src.v, {unit_src.m[0], unit_src.m[1], unit_src.m[2], unit_src.m[3]}, cb};
+  };
+  // Paged: block-table entries are read with vector loads, each issued right
+  // behind a chunk's DMA for the chunk two steps ahead, so it retires with
+  // the next step's wait and no lookup ever stalls the stream.  Entries of
+  // chunks at or past the end of the split are never read (their offset is
+  // out of range and reads 0), and every entry is clamped into the pool, so a
+  // bad entry can only select another page, never leave the pool.
+  const rsrc_t rtab = make_rsrc(prm.block_table + (PAGED ? (int64_t)b * prm.bt_stride : 0),
+                                PAGED ? (uint32_t)prm.bt_stride * 4u : 0u);
+  auto tab_entry = [&](int c) -> uint32_t {
+    return buf_u32<kPolicyDefault>(
+        rtab, c < hi ? (uint32_t)c / (uint32_t)prm.page_size * 4u : 0x80000000u);
+  };
+  auto to_page = [&](uint32_t e) -> int {
+    return min(max((int)__builtin_amdgcn_readfirstlane(e), 0), prm.num_pages - 1);
   };
   uint8_t* ring = smem + w * SM::WAVE;
 
@@ -547,12 +557,21 @@ quant_split_lds_kernel(SplitParams prm) {
   const int cb0 = lo + kChunk * w;
   const int cstride = kChunk * NW;
   static_assert(NSTAGE == 2, "the chunk loop is unrolled for a two-stage ring");
+  // Paged: page_next is the pool page of the chunk whose DMA is issued next;
+  // tab_pending the (in-flight) table entry of the chunk after that.
+  int page_next = 0;
+  uint32_t tab_pending = 0;
   {
-    const ChunkSrc src = chunk_src(cb0, PAGED && cb0 < hi ? page_of(cb0) : 0);
+    int page0 = 0;
+    if constexpr (PAGED) {
+      const uint32_t e0 = tab_entry(cb0), e1 = tab_entry(cb0 + cstride);
+      page0 = to_page(e0);
+      page_next = to_page(e1);
+    }
+    const ChunkSrc src = chunk_src(cb0, page0);
     issue_chunk<D, KNB, VNB, GS>(ring, src.k, src.v, src.m, src.row, cb0 < hi, lane);
+    if constexpr (PAGED) tab_pending = tab_entry(cb0 + 2 * cstride);
   }
-  // Paged: the pool page of the chunk issued next, looked up one step early.
-  int page_next = PAGED && cb0 + cstride < hi ? page_of(cb0 + cstride) : 0;
 
 
   QOperands<D, KNB, GS> qo;
@@ -630,10 +649,16 @@ quant_split_lds_kernel(SplitParams prm) {
       const ChunkSrc src = chunk_src(cn, page_next);
       issue_chunk<D, KNB, VNB, GS>(ring + ((SK + NSTAGE - 1) % NSTAGE) * SG::BYTES, src.k, src.v,
                                    src.m, src.row, valid, lane);
-      if constexpr (PAGED) page_next = valid && cn + cstride < hi ? page_of(cn + cstride) : 0;
     }
-    wait_vmcnt<(NSTAGE - 1) * NI>();
+    // Paged: one more vector load in flight, behind the DMA just issued.
+    uint32_t tab_new = 0;
+    if constexpr (PAGED) tab_new = tab_entry(cb + 3 * cstride);
+    wait_vmcnt<(NSTAGE - 1) * NI + (PAGED ? 1 : 0)>();
     asm volatile("" ::: "memory");  // no LDS read of this stage above the wait
+    if constexpr (PAGED) {  // retired with the wait above: issued a step ago
+      page_next = to_page(tab_pending);
+      tab_pending = tab_new;
+    }
     const uint8_t* st = ring + SK * SG::BYTES;
     const uint8_t* mks = st + SG::M_OFF;
     const uint8_t* mkz = mks + SG::MB;
