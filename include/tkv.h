@@ -79,6 +79,17 @@ typedef struct tkv_decode_args {
    * contiguous (B, HKV, S, ...) caches and the block table is unused. */
   const int32_t *block_table;
   int32_t block_table_stride, page_size, num_pages;
+  /* Fused append (quantized path only): if k_new != NULL, the step first puts
+   * one new token per (b, kv head) into the cache -- k_new/v_new laid out
+   * (B, HKV, D), fp16 (new_is_fp32 == 0) or fp32 -- at position L_b - 1, where
+   * L_b = seq_lens[b] (or S), quantized exactly as tkv_quantize_pack /
+   * tkv_paged_quantize_pack would, and then attends over [0, L_b) including
+   * it.  The same result and the same cache bits as that append followed by
+   * the decode, in one launch.  A paged token whose table entry lies outside
+   * [0, num_pages) is not stored.  No counterpart in the reference (it has no
+   * GPU append). */
+  const void *k_new, *v_new;
+  int32_t new_is_fp32;
 } tkv_decode_args;
 
 /* Fused 2/4-bit split-P decode attention: the split kernel, then (if
@@ -166,7 +177,8 @@ int tkv_device_info(tkv_device_info_t *info);
 const char *tkv_status_string(int status);
 
 /* ABI version of this library (bumped on any incompatible change; 3 added the
- * paged-cache fields of tkv_decode_args and tkv_paged_quantize_pack). */
+ * paged-cache fields of tkv_decode_args and tkv_paged_quantize_pack, 4 the
+ * fused-append fields). */
 int tkv_abi_version(void);
 
 #ifdef __cplusplus

@@ -45,7 +45,7 @@ def test_library_exports_every_declared_symbol():
     for name in _declared_symbols():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.tkv_abi_version() == 3
+    assert lib.tkv_abi_version() == 4
 
 
 def test_library_is_gfx950_only():
@@ -69,12 +69,13 @@ def test_decode_args_layout_matches_c():
     #include <stddef.h>
     #include "tkv.h"
     int main(void) {
-      printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\n", sizeof(tkv_decode_args),
+      printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\n", sizeof(tkv_decode_args),
              offsetof(tkv_decode_args, q_is_fp32), offsetof(tkv_decode_args, seq_lens),
              offsetof(tkv_decode_args, B), offsetof(tkv_decode_args, sm_scale),
              offsetof(tkv_decode_args, num_splits), offsetof(tkv_decode_args, counters),
              offsetof(tkv_decode_args, waves), offsetof(tkv_decode_args, block_table),
              offsetof(tkv_decode_args, page_size), offsetof(tkv_decode_args, num_pages),
+             offsetof(tkv_decode_args, k_new), offsetof(tkv_decode_args, new_is_fp32),
              sizeof(tkv_device_info_t));
       return 0;
     }"""
@@ -89,7 +90,7 @@ def test_decode_args_layout_matches_c():
     assert vals == [ctypes.sizeof(A), A.q_is_fp32.offset, A.seq_lens.offset, A.B.offset,
                     A.sm_scale.offset, A.num_splits.offset, A.counters.offset, A.waves.offset,
                     A.block_table.offset, A.page_size.offset, A.num_pages.offset,
-                    ctypes.sizeof(_lib.DeviceInfo)]
+                    A.k_new.offset, A.new_is_fp32.offset, ctypes.sizeof(_lib.DeviceInfo)]
 
 
 def test_c_entry_points_reject_bad_arguments_without_a_gpu():
@@ -132,6 +133,14 @@ def test_c_entry_points_reject_bad_arguments_without_a_gpu():
     assert lib.tkv_fp16_decode_attention(ctypes.byref(a), None) == _lib.TKV_EUNSUPPORTED
     a.page_size = -32
     assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    # Fused append: k_new needs v_new; the fp16 control has no fused append.
+    a.page_size, a.block_table, a.block_table_stride = 0, None, 0
+    a.k_new = dummy
+    assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    a.v_new = dummy + 1  # misaligned fp16
+    assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    a.v_new = dummy
+    assert lib.tkv_fp16_decode_attention(ctypes.byref(a), None) == _lib.TKV_EUNSUPPORTED
     assert lib.tkv_paged_quantize_pack(None, 0, 1, 1, 1, 128, 4, 32, None, None, 1, 32, 1, None,
                                        None, None, None) == _lib.TKV_EINVAL
     assert lib.tkv_paged_quantize_pack(dummy, 0, 1, 1, 1, 128, 4, 32, dummy, dummy, 1, 48, 1,

@@ -59,6 +59,9 @@ class DecodeArgs(ctypes.Structure):
         ("block_table_stride", ctypes.c_int32),
         ("page_size", ctypes.c_int32),
         ("num_pages", ctypes.c_int32),
+        ("k_new", ctypes.c_void_p),
+        ("v_new", ctypes.c_void_p),
+        ("new_is_fp32", ctypes.c_int32),
     ]
 
 

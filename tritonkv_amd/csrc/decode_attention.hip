@@ -30,6 +30,7 @@
 #include <type_traits>
 
 #include "tkv_codec.h"
+#include "tkv_quant.h"
 #include "../../include/tkv.h"
 
 namespace tkv {
@@ -53,6 +54,12 @@ struct SplitParams {
   // page block_table[b * bt_stride + p].  S = bt_stride * page_size.
   const int32_t* block_table;
   int bt_stride, page_size, num_pages;
+  // Fused append (quantized path): if k_new is set, the token at L_b - 1 of
+  // every (b, kv head) is k_new/v_new[b][kv] (fp16, or fp32 if new_fp32),
+  // quantized into the cache by the step itself.
+  const void* k_new;
+  const void* v_new;
+  int new_fp32;
   int HQ, HKV, S, G, num_splits, split_size, q_fp32;
   float qk_scale;  // sm_scale * log2(e)
 };
@@ -478,6 +485,10 @@ struct LdsKernelSmem {
   // workgroup's combine ticket flag right behind it).
   static constexpr int OUT = (int)sizeof(WavePartial<D>) + 16;
   static constexpr int WAVE = ((RING > OUT ? RING : OUT) + 15) / 16 * 16;
+  // Fused append: the new token's row in staged form (K bytes, V bytes, then
+  // the fp16 scale/zero of K and V, NG each), behind the waves' rings.
+  static constexpr int PATCH_META = SG::KL::DP + SG::VL::DP;
+  static constexpr int PATCH = (PATCH_META + 4 * SG::NG * 2 + 15) / 16 * 16;
 };
 
 template <int D, int KNB, int VNB, int GS, int NW, int NSTAGE, bool PAGED>
@@ -494,7 +505,7 @@ quant_split_lds_kernel(SplitParams prm) {
   static_assert(2 * NG <= 16, "zero-point MFMA holds hi/lo of at most 8 groups");
   static_assert((NSTAGE - 1) * NI < 64, "vmcnt range");
 
-  __shared__ __attribute__((aligned(16))) uint8_t smem[NW * SM::WAVE];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[NW * SM::WAVE + SM::PATCH];
 
   const int split = blockIdx.x;
   const int unit = blockIdx.y;
@@ -579,6 +590,56 @@ quant_split_lds_kernel(SplitParams prm) {
   const u4* qf = qo.qf;
   const u2 qzb = qo.qzb;
 
+  // ---- fused append ----------------------------------------------------------
+  // The token at L - 1 comes from k_new / v_new.  The wave whose chunk holds it
+  // quantizes the row here (quantize_row, the append kernel's own code), keeps
+  // the row in the workgroup's patch area and, in the first block of query
+  // heads, stores it into the cache.  Once that chunk's DMA has landed the wave
+  // overwrites the chunk's row with the patch, so the step never depends on
+  // when the store becomes visible to its own loads.
+  uint8_t* const patch = smem + NW * SM::WAVE;
+  int cb_new = -1;  // first token of the chunk this wave patches, or -1
+  int t_new = 0;    // the new token's row within that chunk
+  if (prm.k_new && L - 1 >= lo && L - 1 < hi && ((L - 1 - lo) / kChunk) % NW == w) {
+    const int tn = L - 1;
+    int64_t row = (int64_t)unit * prm.S + tn;
+    bool use = true;
+    if constexpr (PAGED) {
+      const int e = prm.block_table[(int64_t)b * prm.bt_stride + tn / prm.page_size];
+      use = e >= 0 && e < prm.num_pages;  // as the append kernel: such a token is not stored
+      row = ((int64_t)e * prm.HKV + hk) * prm.page_size + tn % prm.page_size;
+    }
+    if (use) {
+      cb_new = lo + kChunk * ((tn - lo) / kChunk);
+      t_new = tn - cb_new;
+      const int64_t xoff = (int64_t)unit * D * (prm.new_fp32 ? 4 : 2);
+      float xk[KL::P], xv[VL::P];
+      load_row_for_quant<D, KNB>(static_cast<const uint8_t*>(prm.k_new) + xoff, prm.new_fp32, lane, xk);
+      load_row_for_quant<D, VNB>(static_cast<const uint8_t*>(prm.v_new) + xoff, prm.new_fp32, lane, xv);
+      const RowQuant<D, KNB, GS> rk = quantize_row<D, KNB, GS>(xk, lane);
+      const RowQuant<D, VNB, GS> rv = quantize_row<D, VNB, GS>(xv, lane);
+      uint16_t* pmeta = reinterpret_cast<uint16_t*>(patch + SM::PATCH_META);
+      if (lane < KL::DP) patch[lane] = (uint8_t)rk.byte;
+      if (lane < VL::DP) patch[KL::DP + lane] = (uint8_t)rv.byte;
+      if (lane < NG) {
+        pmeta[lane] = (uint16_t)(rk.meta & 0xFFFFu);
+        pmeta[NG + lane] = (uint16_t)(rk.meta >> 16);
+        pmeta[2 * NG + lane] = (uint16_t)(rv.meta & 0xFFFFu);
+        pmeta[3 * NG + lane] = (uint16_t)(rv.meta >> 16);
+      }
+      if (blockIdx.z == 0) {
+        if (lane < KL::DP) const_cast<uint8_t*>(prm.k)[row * KL::DP + lane] = (uint8_t)rk.byte;
+        if (lane < VL::DP) const_cast<uint8_t*>(prm.v)[row * VL::DP + lane] = (uint8_t)rv.byte;
+        if (lane < NG) {
+          const_cast<uint16_t*>(prm.ks)[row * NG + lane] = (uint16_t)(rk.meta & 0xFFFFu);
+          const_cast<uint16_t*>(prm.kz)[row * NG + lane] = (uint16_t)(rk.meta >> 16);
+          const_cast<uint16_t*>(prm.vs)[row * NG + lane] = (uint16_t)(rv.meta & 0xFFFFu);
+          const_cast<uint16_t*>(prm.vz)[row * NG + lane] = (uint16_t)(rv.meta >> 16);
+        }
+      }
+    }
+  }
+
   uint32_t vsel[VL::NE];
 #pragma unroll
   for (int e = 0; e < VL::NE; ++e) vsel[e] = VL::perm_sel(VL::byte_in_dword(e, r));
@@ -658,6 +719,18 @@ quant_split_lds_kernel(SplitParams prm) {
     if constexpr (PAGED) {  // retired with the wait above: issued a step ago
       page_next = to_page(tab_pending);
       tab_pending = tab_new;
+    }
+    if (cb == cb_new) {  // fused append: the new token's row replaces what the DMA read
+      uint8_t* sw = ring + SK * SG::BYTES;
+      const uint16_t* pmeta = reinterpret_cast<const uint16_t*>(patch + SM::PATCH_META);
+      if (lane < KL::DP)
+        sw[SG::K_OFF + SG::template pos_of<KL::DP>(t_new, lane >> 4) * 16 + (lane & 15)] = patch[lane];
+      if (lane < VL::DP)
+        sw[SG::V_OFF + SG::template pos_of<VL::DP>(t_new, lane >> 4) * 16 + (lane & 15)] =
+            patch[KL::DP + lane];
+      if (lane < 4 * NG)
+        *reinterpret_cast<uint16_t*>(sw + SG::M_OFF + (lane / NG) * SG::MB +
+                                     2 * (t_new * SG::MROW + lane % NG)) = pmeta[lane];
     }
     const uint8_t* st = ring + SK * SG::BYTES;
     const uint8_t* mks = st + SG::M_OFF;
@@ -1100,6 +1173,10 @@ static int validate_common(const tkv_decode_args* a) {
       return TKV_EINVAL;
     if ((int64_t)a->block_table_stride * a->page_size != a->S) return TKV_EINVAL;
   }
+  if (a->k_new) {
+    if (!a->v_new) return TKV_EINVAL;
+    if (((uintptr_t)a->k_new | (uintptr_t)a->v_new) & (a->new_is_fp32 ? 3 : 1)) return TKV_EINVAL;
+  }
   if (a->D != 64 && a->D != 128) return TKV_EUNSUPPORTED;
   return TKV_OK;
 }
@@ -1123,6 +1200,9 @@ static SplitParams make_params(const tkv_decode_args* a) {
   p.bt_stride = a->page_size > 0 ? a->block_table_stride : 0;
   p.page_size = a->page_size > 0 ? a->page_size : 0;
   p.num_pages = a->page_size > 0 ? a->num_pages : 0;
+  p.k_new = a->k_new;
+  p.v_new = a->k_new ? a->v_new : nullptr;
+  p.new_fp32 = a->new_is_fp32 ? 1 : 0;
   p.HQ = a->HQ;
   p.HKV = a->HKV;
   p.S = a->S;
@@ -1220,7 +1300,8 @@ static int launch_fused_split(const tkv_decode_args* a, hipStream_t st) {
 static int launch_fp16_split(const tkv_decode_args* a, hipStream_t st) {
   const int rc = validate_common(a);
   if (rc) return rc;
-  if (a->page_size > 0) return TKV_EUNSUPPORTED;  // the fp16 control reads contiguous caches
+  // the fp16 control reads contiguous caches and has no fused append
+  if (a->page_size > 0 || a->k_new) return TKV_EUNSUPPORTED;
   const SplitParams p = make_params(a);
   const dim3 grid = split_grid(a);
   (void)hipGetLastError();

@@ -18,6 +18,7 @@
 #include <type_traits>
 
 #include "tkv_codec.h"
+#include "tkv_quant.h"
 #include "../../include/tkv.h"
 
 namespace tkv {
@@ -30,21 +31,20 @@ struct PageMap {
   int stride, page_size, num_pages;
 };
 
-// One wave per cache row (token x kv head); lane l holds dims [l*EPL, l*EPL+EPL).
+// One wave per cache row (token x kv head), quantized by quantize_row: lane j
+// owns packed byte j of the row.
 template <int D, int NB, int GS, bool F32>
 __global__ void __launch_bounds__(256)
 quantize_pack_kernel(const void* __restrict__ x, int64_t rows, int HKV, int N,
                      const int32_t* __restrict__ positions, int S_cap, PageMap pm,
                      uint8_t* __restrict__ packed, uint16_t* __restrict__ scale,
                      uint16_t* __restrict__ zero) {
-  constexpr int EPL = D / 64;
-  constexpr int LPG = GS / EPL;  // lanes per group
-  constexpr int P = 8 / NB, DP = D / P, NG = D / GS, QMAX = (1 << NB) - 1;
-  __shared__ uint8_t codes_lds[4][D];
+  using R = RowQuant<D, NB, GS>;
+  constexpr int P = R::P, DP = R::DP, NG = R::NG;
 
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t rr = (int64_t)blockIdx.x * 4 + w;
-  if (rr >= rows) return;  // whole wave; no workgroup barrier below
+  if (rr >= rows) return;  // whole wave
   const int64_t bh = rr / N;
   const int t = (int)(rr % N);
   const int b = (int)(bh / HKV);
@@ -57,54 +57,14 @@ quantize_pack_kernel(const void* __restrict__ x, int64_t rows, int HKV, int N,
     dst_row = ((int64_t)e * HKV + bh % HKV) * pm.page_size + dst_t % pm.page_size;
   }
 
-  float xv[EPL];
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    const int64_t idx = rr * D + lane * EPL + e;
-    xv[e] = F32 ? static_cast<const float*>(x)[idx] : (float)static_cast<const _Float16*>(x)[idx];
-  }
-  float mn = xv[0], mx = xv[0];
-#pragma unroll
-  for (int e = 1; e < EPL; ++e) {
-    mn = fminf(mn, xv[e]);
-    mx = fmaxf(mx, xv[e]);
-  }
-#pragma unroll
-  for (int k = 1; k < LPG; k <<= 1) {
-    mn = fminf(mn, __shfl_xor(mn, k, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, k, 64));
-  }
-  float sc = (mx - mn) / (float)QMAX;
-  if (!(sc > 0.0f)) sc = 1.0f;
-  const _Float16 s16 = (_Float16)sc;
-  const _Float16 z16 = (_Float16)mn;
-  const float sf = (float)s16, zf = (float)z16;
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    float c = rintf((xv[e] - zf) / sf);
-    if (c != c) c = 0.0f;  // 0/0 when the fp16 scale underflows: torch yields code 0
-    c = fminf(fmaxf(c, 0.0f), (float)QMAX);
-    codes_lds[w][lane * EPL + e] = (uint8_t)c;
-  }
-  if (in_range && (lane % LPG) == 0) {
-    const int g = lane / LPG;
-    scale[dst_row * NG + g] = __builtin_bit_cast(uint16_t, s16);
-    zero[dst_row * NG + g] = __builtin_bit_cast(uint16_t, z16);
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if (in_range && lane < DP / 4) {
-    uint32_t word = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int jb = 4 * lane + k;
-      uint32_t byte = 0;
-#pragma unroll
-      for (int p = 0; p < P; ++p) byte |= (uint32_t)codes_lds[w][jb + p * DP] << (p * NB);
-      word |= byte << (8 * k);
-    }
-    reinterpret_cast<uint32_t*>(packed + dst_row * DP)[lane] = word;
+  float xv[P];
+  load_row_for_quant<D, NB>(static_cast<const uint8_t*>(x) + rr * D * (F32 ? 4 : 2), F32, lane, xv);
+  const R q = quantize_row<D, NB, GS>(xv, lane);
+  if (!in_range) return;
+  if (lane < DP) packed[dst_row * DP + lane] = (uint8_t)q.byte;
+  if (lane < NG) {
+    scale[dst_row * NG + lane] = (uint16_t)(q.meta & 0xFFFFu);
+    zero[dst_row * NG + lane] = (uint16_t)(q.meta >> 16);
   }
 }
 

@@ -32,6 +32,8 @@ Differences a caller can observe, all deliberate:
   (last workgroup per unit) instead of a second launch; it is correct but
   measured slower on MI355X (every workgroup's agent-scope release writes back
   its L2), so it is off by default.
+* ``k_new`` / ``v_new`` (new, keyword-only): the decode-step append fused into
+  the same launch -- see :func:`new_token_args`.
 """
 
 from __future__ import annotations
@@ -191,6 +193,36 @@ def _seq_lens_arg(seq_lens, B, S, device):
     return seq_lens.contiguous()
 
 
+def new_token_args(k_new, v_new, B: int, HKV: int, D: int, device):
+    """Validated ``(k_new, v_new, is_fp32)`` for the fused append, or Nones.
+
+    ``k_new`` / ``v_new``: ``(B, HKV, D)`` or ``(B, HKV, 1, D)``, both fp16 or
+    both fp32.  The token goes to position ``L_b - 1`` of row b, where ``L_b``
+    is ``seq_lens[b]`` (or the cache capacity), and is quantized into the
+    caches in place exactly as :func:`~tritonkv_amd.quantize.append_kv` at
+    ``positions = L - 1`` would; attention then covers ``[0, L_b)``.
+    """
+    if k_new is None and v_new is None:
+        return None, None, 0
+    if k_new is None or v_new is None:
+        raise ValueError("k_new and v_new must be given together")
+    out = []
+    for name, x in (("k_new", k_new), ("v_new", v_new)):
+        if x.dim() == 4 and x.shape[2] == 1:
+            x = x[:, :, 0]
+        if tuple(x.shape) != (B, HKV, D):
+            raise ValueError(f"{name} must have shape ({B}, {HKV}, {D}) or ({B}, {HKV}, 1, {D}), "
+                             f"got {tuple(x.shape)}")
+        if x.dtype not in (torch.float16, torch.float32):
+            raise TypeError(f"{name} must be float16 or float32, got {x.dtype}")
+        if x.device != torch.device(device):
+            raise ValueError(f"{name} must be on the cache's device")
+        out.append(x.contiguous())
+    if out[0].dtype != out[1].dtype:
+        raise TypeError("k_new and v_new must have the same dtype")
+    return out[0], out[1], int(out[0].dtype == torch.float32)
+
+
 def fused_decode_attention(
     q: torch.Tensor,
     kq: QuantizedTensor,
@@ -209,6 +241,8 @@ def fused_decode_attention(
     seq_lens: torch.Tensor | None = None,
     allow_mixed_bits: bool = False,
     fused_combine: bool = False,
+    k_new: torch.Tensor | None = None,
+    v_new: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Single decode step of attention, computed directly on packed low-bit K/V.
 
@@ -251,6 +285,7 @@ def fused_decode_attention(
     out = _check_out(out, B, HQ, D, q.device)
     acc, maxs, sums, counters = _workspace_for(_workspace, B, HQ, num_splits, D, q.device, HKV)
     lens = _seq_lens_arg(seq_lens, B, S, q.device)
+    kn, vn, new_f32 = new_token_args(k_new, v_new, B, HKV, D, q.device)
 
     args = _lib.DecodeArgs(
         q=q.data_ptr(), q_is_fp32=int(q.dtype == torch.float32),
@@ -261,7 +296,8 @@ def fused_decode_attention(
         k_nbits=kq.nbits, v_nbits=vq.nbits, group_size=kq.group_size,
         sm_scale=float(sm_scale), split_size=split_size, num_splits=num_splits,
         counters=_lib.ptr(counters) if fused_combine else None,
-        waves=choose_waves(B, HKV, group, split_size, num_splits))
+        waves=choose_waves(B, HKV, group, split_size, num_splits),
+        k_new=_lib.ptr(kn), v_new=_lib.ptr(vn), new_is_fp32=new_f32)
     with torch.cuda.device(q.device):
         rc = _lib.load().tkv_fused_decode_attention(args, _lib.stream_handle(q.device))
     _lib.check(rc, "fused_decode_attention")

@@ -30,7 +30,7 @@ import torch
 
 from . import _lib
 from .kernels.fused_decode_attn import (_aligned16, _check_out, _workspace_for, choose_waves,
-                                        plan_splits)
+                                        new_token_args, plan_splits)
 from .quantize import QuantizedTensor, _check_bits, _require_gpu, empty_cache
 
 PAGE_MULTIPLE = 32
@@ -116,6 +116,8 @@ def paged_decode_attention(
     _workspace: dict | None = None,
     *,
     allow_mixed_bits: bool = False,
+    k_new: torch.Tensor | None = None,
+    v_new: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """One decode step of attention over paged 2/4-bit K/V pools.
 
@@ -125,7 +127,10 @@ def paged_decode_attention(
     and ``out`` contract as
     :func:`~tritonkv_amd.kernels.fused_decode_attention`; returns
     ``(B, HQ, D)`` float32, bit-identical to that function on a contiguous
-    cache holding the same tokens with the same ``num_splits``.
+    cache holding the same tokens with the same ``num_splits``.  ``k_new`` /
+    ``v_new`` fuse the step's append into the same launch (the token lands at
+    ``seq_lens[b] - 1``), bit-identical to :func:`paged_append` followed by
+    this call.
     """
     if k_pool.group_size != v_pool.group_size or (k_pool.nbits != v_pool.nbits
                                                   and not allow_mixed_bits):
@@ -160,6 +165,7 @@ def paged_decode_attention(
     out = _check_out(out, B, HQ, D, q.device)
     acc, maxs, sums, _ = _workspace_for(_workspace, B, HQ, num_splits, D, q.device, HKV)
     lens = seq_lens.contiguous() if seq_lens is not None else None
+    kn, vn, new_f32 = new_token_args(k_new, v_new, B, HKV, D, q.device)
     args = _lib.DecodeArgs(
         q=q.data_ptr(), q_is_fp32=int(q.dtype == torch.float32),
         k=k_pool.packed.data_ptr(), k_scale=k_pool.scale.data_ptr(),
@@ -171,7 +177,7 @@ def paged_decode_attention(
         sm_scale=float(sm_scale), split_size=split_size, num_splits=num_splits, counters=None,
         waves=choose_waves(B, HKV, group, split_size, num_splits),
         block_table=table.data_ptr(), block_table_stride=table.shape[1], page_size=page_size,
-        num_pages=num_pages)
+        num_pages=num_pages, k_new=_lib.ptr(kn), v_new=_lib.ptr(vn), new_is_fp32=new_f32)
     with torch.cuda.device(q.device):
         rc = _lib.load().tkv_fused_decode_attention(args, _lib.stream_handle(q.device))
     _lib.check(rc, "paged_decode_attention")
