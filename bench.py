@@ -559,6 +559,10 @@ def ragged_70b(steps, warmup, seed=2024):
         append_kv(vc, v_new, pos)
         decode()
 
+    def fused_step():  # the append inside the split kernel: one launch
+        fused_decode_attention(q, kc, vc, seq_lens=lens1, allow_mixed_bits=True, out=out,
+                               _workspace=ws, k_new=k_new, v_new=v_new)
+
     torch.cuda.synchronize()
     row = cache_row_bytes(D, 4, gs) + cache_row_bytes(D, 2, gs)
     tokens = int(lens1.sum())
@@ -566,16 +570,18 @@ def ragged_70b(steps, warmup, seed=2024):
     append_bytes = B * HKV * (2 * D * 2 + row)
     us, _, _ = timed_steps([step], steps, warmup)
     dus, _, _ = timed_steps([decode], steps, warmup)
+    fus, _, _ = timed_steps([fused_step], steps, warmup)
     total = decode_bytes + append_bytes
     res = {"us_per_step": round(us, 2), "decode_us": round(dus, 2),
-           "append_us": round(us - dus, 2), "sum_tokens": tokens,
+           "append_us": round(us - dus, 2), "fused_append_step_us": round(fus, 2),
+           "sum_tokens": tokens,
            "algorithmic_bytes": total,
            "gbps_step": round(total / us / 1e3, 1),
            "frac_of_hbm_peak_step": round(total / us / 1e3 / HBM_PEAK_GBS, 4),
            "frac_of_hbm_peak_decode": round(decode_bytes / dus / 1e3 / HBM_PEAK_GBS, 4),
            "lengths": "S_b ~ U[1024, 131072], torch.Generator().manual_seed(%d)" % seed}
-    print(f"# ragged 70b K4/V2: step {us:.1f} us (decode {dus:.1f} us), "
-          f"{total / us / 1e3:.0f} GB/s", file=sys.stderr, flush=True)
+    print(f"# ragged 70b K4/V2: step {us:.1f} us (decode {dus:.1f} us, fused append+decode "
+          f"{fus:.1f} us), {total / us / 1e3:.0f} GB/s", file=sys.stderr, flush=True)
     del kc, vc, ws
     torch.cuda.empty_cache()
     return res
@@ -645,6 +651,52 @@ def qwen_table(ctxs=(512, 2048, 8192, 16384)):
                         "flash_decode_effect_hot_vs_torch": ratio(S, "torch_fp16", "fp16", "hot_us")}
                for S in ctxs}
     return {"rows": rows, "effects": effects}
+
+
+def qwen_serving_steps(ctxs=(2048, 16384)):
+    """A whole decode step at the Qwen2.5-1.5B shape (B=1, 4-bit gs32, one
+    cache): append the new token's K and V, then attend over it -- as three
+    launches (two appends + decode) and as one (the append fused into the split
+    kernel).  Per-step µs of a graph of 50 steps."""
+    import torch
+
+    from tritonkv_amd.kernels import fused_decode_attention
+    from tritonkv_amd.quantize import append_kv, quantize_groupwise
+
+    B, HQ, HKV, D, gs = 1, 12, 2, 128, 32
+    res = {}
+    for S in ctxs:
+        g = torch.Generator(device="cuda").manual_seed(2000 + S)
+        q = torch.randn(B, HQ, D, device="cuda", generator=g, dtype=torch.float16)
+        kq = quantize_groupwise(torch.randn(B, HKV, S, D, device="cuda", generator=g,
+                                            dtype=torch.float16), 4, gs)
+        vq = quantize_groupwise(torch.randn(B, HKV, S, D, device="cuda", generator=g,
+                                            dtype=torch.float16), 4, gs)
+        k_new = torch.randn(B, HKV, 1, D, device="cuda", generator=g, dtype=torch.float16)
+        v_new = torch.randn(B, HKV, 1, D, device="cuda", generator=g, dtype=torch.float16)
+        lens = torch.full((B,), S, dtype=torch.int32, device="cuda")
+        pos = lens - 1
+        out = torch.empty(B, HQ, D, device="cuda")
+        ws = {}
+
+        def three():
+            append_kv(kq, k_new, pos)
+            append_kv(vq, v_new, pos)
+            fused_decode_attention(q, kq, vq, seq_lens=lens, out=out, _workspace=ws)
+
+        def one():
+            fused_decode_attention(q, kq, vq, seq_lens=lens, out=out, _workspace=ws,
+                                   k_new=k_new, v_new=v_new)
+
+        t3 = per_call_us([three] * 50)
+        t1 = per_call_us([one] * 50)
+        res[str(S)] = {"three_launches_us": round(t3, 3), "fused_us": round(t1, 3),
+                       "speedup": round(t3 / t1, 3)}
+        print(f"# qwen serving step ctx={S}: append+append+decode {t3:.2f} us, fused {t1:.2f} us",
+              file=sys.stderr, flush=True)
+        del kq, vq
+        torch.cuda.empty_cache()
+    return res
 
 
 # ---------------------------------------------------------------------------
@@ -788,6 +840,7 @@ def main() -> int:
         detail["quant_effect_2b"] = round(detail["fp16"]["us_per_step"] / detail["fused2"]["us_per_step"], 3)
         detail["empty_graph_node_us"] = round(empty_kernel_floor() * 1e3, 2)
         detail["qwen2.5-1.5b"] = qwen_table()
+        detail["qwen2.5-1.5b_serving_step"] = qwen_serving_steps()
         detail["ragged_70b_k4v2"] = ragged_70b(a.steps, a.warmup)
 
     line = {

@@ -720,7 +720,9 @@ quant_split_lds_kernel(SplitParams prm) {
       page_next = to_page(tab_pending);
       tab_pending = tab_new;
     }
-    if (cb == cb_new) {  // fused append: the new token's row replaces what the DMA read
+    // Fused append: the new token is the split's last (L - 1 = hi - 1), so its
+    // chunk is always a TAIL step; its row replaces what the DMA read.
+    if (TAIL && cb == cb_new) {
       uint8_t* sw = ring + SK * SG::BYTES;
       const uint16_t* pmeta = reinterpret_cast<const uint16_t*>(patch + SM::PATCH_META);
       if (lane < KL::DP)
@@ -867,17 +869,19 @@ quant_split_lds_kernel(SplitParams prm) {
     }
   };
 
-  // Pairs of full chunks (stages 0 and 1), then what is left: at most one
-  // full chunk and the split's partial last chunk.  A single loop exit keeps
-  // the accumulators in place across the unrolled copies.
+  // Pairs of chunks that end before the split's last token (stages 0 and 1),
+  // then what is left: at most one such chunk and the chunk holding the last
+  // token, which always runs as the TAIL step (even when it is full).  A
+  // single loop exit keeps the accumulators in place across the unrolled
+  // copies.
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
   int cb = cb0;
-  for (; cb + cstride + kChunk <= hi; cb += 2 * cstride) {
+  for (; cb + cstride + kChunk < hi; cb += 2 * cstride) {
     step(cb, std::false_type{}, S0{});
     step(cb + cstride, std::false_type{}, S1{});
   }
-  if (cb + kChunk <= hi) {
+  if (cb + kChunk < hi) {
     step(cb, std::false_type{}, S0{});
     if (cb + cstride < hi) step(cb + cstride, std::true_type{}, S1{});
   } else if (cb < hi) {
