@@ -28,6 +28,7 @@
 //     (quantized kernel) or registers (fp16 control); the partial (m, l, acc)
 //     of the NW waves is merged in LDS and written once per workgroup.
 #include <type_traits>
+#include <utility>
 
 #include "tkv_codec.h"
 #include "tkv_quant.h"
@@ -420,6 +421,16 @@ __device__ __forceinline__ void dma2(rsrc_t r, lds_ptr_t lds, uint32_t off) {
   else dma2_default(r, lds, off);
 }
 
+// f(std::integral_constant<int, I>) for I = 0 .. N-1, unrolled at compile time.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 // vmcnt-only wait (gfx9 encoding: vmcnt[3:0] | expcnt 7 | lgkmcnt 15 | vmcnt[5:4]).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -567,21 +578,26 @@ quant_split_lds_kernel(SplitParams prm) {
   // Chunk k of this wave starts at token lo + 32 * (w + NW * k).
   const int cb0 = lo + kChunk * w;
   const int cstride = kChunk * NW;
-  static_assert(NSTAGE == 2, "the chunk loop is unrolled for a two-stage ring");
+  static_assert(NSTAGE >= 2 && (!PAGED || NSTAGE == 2), "ring depth");
   // Paged: page_next is the pool page of the chunk whose DMA is issued next;
   // tab_pending the (in-flight) table entry of the chunk after that.
   int page_next = 0;
   uint32_t tab_pending = 0;
-  {
-    int page0 = 0;
-    if constexpr (PAGED) {
-      const uint32_t e0 = tab_entry(cb0), e1 = tab_entry(cb0 + cstride);
-      page0 = to_page(e0);
-      page_next = to_page(e1);
-    }
+  if constexpr (PAGED) {
+    const uint32_t e0 = tab_entry(cb0), e1 = tab_entry(cb0 + cstride);
+    const int page0 = to_page(e0);
+    page_next = to_page(e1);
     const ChunkSrc src = chunk_src(cb0, page0);
     issue_chunk<D, KNB, VNB, GS>(ring, src.k, src.v, src.m, src.row, cb0 < hi, lane);
-    if constexpr (PAGED) tab_pending = tab_entry(cb0 + 2 * cstride);
+    tab_pending = tab_entry(cb0 + 2 * cstride);
+  } else {
+    // the first NSTAGE - 1 chunks into stages 0 .. NSTAGE - 2
+    static_for<NSTAGE - 1>([&](auto s) __attribute__((always_inline)) {
+      constexpr int SS = decltype(s)::value;
+      const int c = cb0 + SS * cstride;
+      const ChunkSrc src = chunk_src(c, 0);
+      issue_chunk<D, KNB, VNB, GS>(ring + SS * SG::BYTES, src.k, src.v, src.m, src.row, c < hi, lane);
+    });
   }
 
 
@@ -698,7 +714,7 @@ quant_split_lds_kernel(SplitParams prm) {
 
   // Chunk k of the wave uses stage k % NSTAGE; the loop below is unrolled by
   // NSTAGE so every stage offset is a compile-time constant.
-  auto step = [&](int cb, auto tail, auto stage) {
+  auto step = [&](int cb, auto tail, auto stage) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail)::value;
     constexpr int SK = decltype(stage)::value;
     // refill the stage consumed by the previous chunk, NSTAGE-1 chunks ahead
@@ -869,24 +885,29 @@ quant_split_lds_kernel(SplitParams prm) {
     }
   };
 
-  // Pairs of chunks that end before the split's last token (stages 0 and 1),
-  // then what is left: at most one such chunk and the chunk holding the last
-  // token, which always runs as the TAIL step (even when it is full).  A
-  // single loop exit keeps the accumulators in place across the unrolled
-  // copies.
-  using S0 = std::integral_constant<int, 0>;
-  using S1 = std::integral_constant<int, 1>;
+  // Runs of NSTAGE chunks that end before the split's last token (stages
+  // 0 .. NSTAGE-1), then what is left: at most NSTAGE - 1 such chunks and the
+  // chunk holding the last token, which always runs as the TAIL step (even
+  // when it is full).  A single loop exit keeps the accumulators in place
+  // across the unrolled copies.
   int cb = cb0;
-  for (; cb + cstride + kChunk < hi; cb += 2 * cstride) {
-    step(cb, std::false_type{}, S0{});
-    step(cb + cstride, std::false_type{}, S1{});
+  for (; cb + (NSTAGE - 1) * cstride + kChunk < hi; cb += NSTAGE * cstride) {
+    static_for<NSTAGE>([&](auto s) __attribute__((always_inline)) {
+      step(cb + decltype(s)::value * cstride, std::false_type{}, s);
+    });
   }
-  if (cb + kChunk < hi) {
-    step(cb, std::false_type{}, S0{});
-    if (cb + cstride < hi) step(cb + cstride, std::true_type{}, S1{});
-  } else if (cb < hi) {
-    step(cb, std::true_type{}, S0{});
-  }
+  bool more = true;
+  static_for<NSTAGE>([&](auto s) __attribute__((always_inline)) {
+    if (more) {
+      if (cb + kChunk < hi) {
+        step(cb, std::false_type{}, s);
+        cb += cstride;
+      } else {
+        if (cb < hi) step(cb, std::true_type{}, s);
+        more = false;
+      }
+    }
+  });
   wait_vmcnt<0>();  // retire the trailing (out-of-range) prefetches
   wave_lds_fence();
 
@@ -1223,17 +1244,23 @@ static dim3 split_grid(const tkv_decode_args* a) {
   return dim3((unsigned)a->num_splits, (unsigned)(a->B * a->HKV), (unsigned)((G + 15) / 16));
 }
 
-constexpr int kStages = 2;  // ring depth per wave of the quantized split kernel
+// Ring depth per wave of the quantized split kernel.  8-wave workgroups run
+// one per CU (VGPRs), so their LDS could hold three stages, but a third stage
+// measured slightly slower at the Llama-3-8B shape (208 vs 206 us): one chunk
+// in flight per wave already saturates what this access pattern streams.
+// Paged caches use two stages.
+constexpr int kStages8 = 2;
+constexpr int kStages4 = 2;
 
 template <int D, int KNB, int VNB, int GS>
 static void launch_quant(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
   const bool paged = p.page_size > 0;
   if (waves == 8) {
-    if (paged) quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages, true><<<grid, dim3(8 * 64), 0, st>>>(p);
-    else quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages, false><<<grid, dim3(8 * 64), 0, st>>>(p);
+    if (paged) quant_split_lds_kernel<D, KNB, VNB, GS, 8, 2, true><<<grid, dim3(8 * 64), 0, st>>>(p);
+    else quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false><<<grid, dim3(8 * 64), 0, st>>>(p);
   } else {
-    if (paged) quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages, true><<<grid, dim3(4 * 64), 0, st>>>(p);
-    else quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages, false><<<grid, dim3(4 * 64), 0, st>>>(p);
+    if (paged) quant_split_lds_kernel<D, KNB, VNB, GS, 4, 2, true><<<grid, dim3(4 * 64), 0, st>>>(p);
+    else quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false><<<grid, dim3(4 * 64), 0, st>>>(p);
   }
 }
 
