@@ -256,11 +256,12 @@ def fp16_call(q, k, v, num_splits=None, split_only=False, waves=None, fused_comb
     import torch
 
     from tritonkv_amd import _lib
-    from tritonkv_amd.kernels.fused_decode_attn import _workspace_for, choose_waves, plan_splits
+    from tritonkv_amd.kernels.fused_decode_attn import (TOKENS_PER_WORKGROUP_FP16, _workspace_for,
+                                                        choose_waves, plan_splits)
 
     B, HQ, D = q.shape
     _, HKV, S, _ = k.shape
-    _, ns, size = plan_splits(S, 64, num_splits, B, HKV, HQ // HKV)
+    _, ns, size = plan_splits(S, 64, num_splits, B, HKV, HQ // HKV, TOKENS_PER_WORKGROUP_FP16)
     out = torch.empty(B, HQ, D, device=q.device)
     acc, mx, sm, cnt = _workspace_for({}, B, HQ, ns, D, q.device, HKV)
     wv = choose_waves(B, HKV, HQ // HKV, size, ns) if waves is None else waves
@@ -699,6 +700,92 @@ def qwen_serving_steps(ctxs=(2048, 16384)):
     return res
 
 
+def qwen_e2e(ctxs=(8192, 32768), B=16, steps=8, seed=11):
+    """End-to-end decode tokens/s of a random-initialised Qwen2.5-1.5B-architecture
+    model (transformers, fp16 weights, 28 layers, HQ=12, HKV=2, D=128) at batch B
+    with the cache pre-filled to ctx tokens of synthetic K/V: stock transformers
+    (SDPA + DynamicCache, eager), the fp16 control kernel and the fused 4-bit
+    kernel (``tritonkv_amd.hf``, eager and as one captured HIP graph per step)."""
+    import torch
+    from transformers import DynamicCache, Qwen2Config, Qwen2ForCausalLM
+
+    from tritonkv_amd import hf
+
+    hf.register()
+    cfg = Qwen2Config(vocab_size=151936, hidden_size=1536, intermediate_size=8960,
+                      num_hidden_layers=28, num_attention_heads=12, num_key_value_heads=2,
+                      max_position_embeddings=65536, rope_theta=1e6, tie_word_embeddings=True)
+    torch.manual_seed(seed)
+    model = Qwen2ForCausalLM(cfg).half().cuda().eval()
+    HKV, D = 2, 128
+    res = {}
+
+    def fill(cache, L):
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        for i in range(cfg.num_hidden_layers):
+            k = torch.randn(B, HKV, L, D, device="cuda", generator=g, dtype=torch.float16)
+            v = torch.randn(B, HKV, L, D, device="cuda", generator=g, dtype=torch.float16)
+            cache.update(k, v, i)
+            del k, v
+
+    def timed(fn, n):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        s.record()
+        for _ in range(n):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) * 1e3 / n
+
+    with torch.no_grad():
+        for L in ctxs:
+            row = {}
+            for name in ("stock_sdpa", "tkv_fp16", "tkv_4bit"):
+                if name == "stock_sdpa":
+                    model.set_attn_implementation("sdpa")
+                    cache = DynamicCache(config=model.config)
+                else:
+                    model.set_attn_implementation(hf.ATTN_NAME)
+                    cache = hf.TkvCache(model.config, capacity=L + 4 * steps + 8,
+                                        nbits=16 if name == "tkv_fp16" else 4)
+                fill(cache, L)
+                ids = torch.zeros(B, 1, dtype=torch.long, device="cuda")
+                pos = torch.full((B, 1), L, dtype=torch.long, device="cuda")
+
+                def step():
+                    model(input_ids=ids, position_ids=pos, past_key_values=cache, use_cache=True,
+                          logits_to_keep=1)
+                    pos.add_(1)
+
+                step()  # warm-up
+                entry = {"eager_us": round(timed(step, steps), 1)}
+                if name != "stock_sdpa":
+                    try:
+                        g = capture([step])
+                        entry["graph_us"] = round(timed(g.replay, steps), 1)
+                        del g
+                    except Exception as exc:  # report, do not fail the bench
+                        entry["graph_error"] = f"{type(exc).__name__}: {exc}"[:200]
+                best = min(v for k, v in entry.items() if k.endswith("_us"))
+                entry["tokens_per_s"] = round(B / best * 1e6, 1)
+                if name != "stock_sdpa":
+                    entry["cache_bytes"] = cache.nbytes
+                row[name] = entry
+                print(f"# e2e qwen2.5-1.5b B={B} ctx={L} {name}: {entry}", file=sys.stderr,
+                      flush=True)
+                del cache
+                torch.cuda.empty_cache()
+            row["speedup_4bit_vs_fp16_control"] = round(
+                row["tkv_4bit"]["tokens_per_s"] / row["tkv_fp16"]["tokens_per_s"], 3)
+            row["speedup_4bit_vs_stock"] = round(
+                row["tkv_4bit"]["tokens_per_s"] / row["stock_sdpa"]["tokens_per_s"], 3)
+            res[str(L)] = row
+    del model
+    torch.cuda.empty_cache()
+    return {"batch": B, "model": "Qwen2.5-1.5B architecture, random init, fp16", "ctx": res}
+
+
 # ---------------------------------------------------------------------------
 
 
@@ -841,6 +928,7 @@ def main() -> int:
         detail["empty_graph_node_us"] = round(empty_kernel_floor() * 1e3, 2)
         detail["qwen2.5-1.5b"] = qwen_table()
         detail["qwen2.5-1.5b_serving_step"] = qwen_serving_steps()
+        detail["qwen2.5-1.5b_e2e_decode"] = qwen_e2e()
         detail["ragged_70b_k4v2"] = ragged_70b(a.steps, a.warmup)
 
     line = {

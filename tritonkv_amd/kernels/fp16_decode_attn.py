@@ -17,6 +17,7 @@ import torch
 
 from .. import _lib
 from .fused_decode_attn import (
+    TOKENS_PER_WORKGROUP_FP16,
     _aligned16,
     _check_out,
     _seq_lens_arg,
@@ -58,7 +59,8 @@ def fp16_decode_attention(
 
     group = HQ // HKV
     sm_scale = 1.0 / math.sqrt(D) if sm_scale is None else sm_scale
-    _, num_splits, split_size = plan_splits(S, block_n, num_splits, B, HKV, group)
+    _, num_splits, split_size = plan_splits(S, block_n, num_splits, B, HKV, group,
+                                            TOKENS_PER_WORKGROUP_FP16)
 
     if q.dtype not in (torch.float16, torch.float32):
         q = q.float()

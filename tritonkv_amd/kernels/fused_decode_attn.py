@@ -98,17 +98,29 @@ def pick_num_splits(B: int, HKV: int, n_blocks: int, target_programs: int | None
     return max(1, min(n_blocks, want))
 
 
-def default_num_splits(B: int, HKV: int, G: int, S: int, block_n: int) -> int:
+# Tokens one workgroup of a split history should stream (see default_num_splits).
+TOKENS_PER_WORKGROUP = 512      # fused 2/4-bit kernel
+TOKENS_PER_WORKGROUP_FP16 = 256  # fp16 control: 3-6x the bytes per token
+
+
+def default_num_splits(B: int, HKV: int, G: int, S: int, block_n: int,
+                       tokens_per_workgroup: int = TOKENS_PER_WORKGROUP) -> int:
     """Split count used when the caller passes ``num_splits=None``.
 
-    Chosen from a sweep on MI355X (split count x workgroup size x combine mode,
-    Qwen2.5-1.5B shape at ctx 512..16384 and Llama-3-8B at B=32, ctx 32768):
+    Chosen from sweeps on MI355X (split count x workgroup size, DRAM-resident
+    caches, batch 1..64, 2..8 KV heads, ctx 2048..32768):
 
     * a batch that already offers one (b, kv head, 16-head block) unit per
-      compute unit or more runs unsplit -- no partials, no combine launch;
-    * otherwise about 64 workgroups in total, each streaming at least 128
-      tokens, and no split at all up to 1024 tokens, where one 8-wave
-      workgroup per unit beats any split-plus-combine on latency.
+      compute unit or more runs unsplit -- no partials, no combine launch --
+      and so does a history of at most 1024 tokens, where one workgroup per
+      unit beats any split-plus-combine on latency;
+    * otherwise the history is cut so that each workgroup streams about
+      ``tokens_per_workgroup`` tokens (512 for the fused kernel, 256 for the
+      fp16 control, whose tokens are 3-6x larger), with at least 32 and at
+      most one workgroup per compute unit in total.  Fewer, longer workgroups
+      win at small caches (the Qwen2.5-1.5B shape, fused: 64 workgroups at
+      ctx 16384); one per CU wins as soon as the cache is tens of MB (e.g. 3x
+      over a fixed 64 at B=16, ctx 32768).
 
     Returned in units of ``block_n`` blocks so the reference's tightening
     applies unchanged.
@@ -117,23 +129,26 @@ def default_num_splits(B: int, HKV: int, G: int, S: int, block_n: int) -> int:
     units = B * HKV * _cdiv(G, 16)
     if units >= cu or S <= 1024:
         return 1
-    want = max(1, _cdiv(64, units))
+    workgroups = min(cu, max(32, units * S // tokens_per_workgroup))
+    want = max(1, workgroups // units)
     max_splits = max(1, S // max(_MIN_SPLIT_TOKENS, block_n))
     return max(1, min(want, max_splits, _cdiv(S, block_n)))
 
 
 def choose_waves(B: int, HKV: int, G: int, split_size: int, num_splits: int = 0) -> int:
-    """Waves per workgroup: 8 for unsplit runs (one workgroup per unit must
-    carry the whole history), 4 when the history is split."""
-    return 8 if num_splits == 1 else 4
+    """Waves per workgroup: 8 when a workgroup streams the whole history or at
+    least 512 tokens (two 32-token chunks per wave, so each wave overlaps a
+    load with compute), else 4."""
+    return 8 if num_splits == 1 or split_size >= 512 else 4
 
 
-def plan_splits(S: int, block_n: int, num_splits: int | None, B: int, HKV: int, G: int):
+def plan_splits(S: int, block_n: int, num_splits: int | None, B: int, HKV: int, G: int,
+                tokens_per_workgroup: int = TOKENS_PER_WORKGROUP):
     """Reference split arithmetic (:486-499) -> (block_n, num_splits, split_size)."""
     block_n = min(block_n, max(16, _next_pow2(S)))
     n_blocks = _cdiv(S, block_n)
     if num_splits is None:
-        num_splits = default_num_splits(B, HKV, G, S, block_n)
+        num_splits = default_num_splits(B, HKV, G, S, block_n, tokens_per_workgroup)
     num_splits = max(1, min(num_splits, n_blocks))
     blocks_per_split = _cdiv(n_blocks, num_splits)
     num_splits = _cdiv(n_blocks, blocks_per_split)  # tighten: no empty splits
