@@ -2,8 +2,9 @@
 
     python -m tritonkv_amd.build          # or: __graft_entry__.build()
 
-Each ``.hip`` source is compiled to an object in parallel, then linked into
-``tritonkv_amd/libtkv_hip.so``.  Flags:
+Each ``.hip`` source is compiled to an object in parallel (the quantized split
+kernel's instantiations are spread over one file per K/V bit-width pair), then
+linked into ``tritonkv_amd/libtkv_hip.so``.  Flags:
 
 * ``--offload-arch=gfx950`` only -- no other targets, no host fallback;
 * ``-O3`` without fast-math: the quantizer needs IEEE binary32 division and
@@ -29,7 +30,8 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 OBJ = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libtkv_hip.so")
-SOURCES = ["decode_attention.hip", "quant_pack.hip", "runtime.hip"]
+SOURCES = ["decode_attention.hip", "quant_split_k4v4.hip", "quant_split_k2v2.hip",
+           "quant_split_k4v2.hip", "quant_split_k2v4.hip", "quant_pack.hip", "runtime.hip"]
 ARCH = "gfx950"
 
 

@@ -1,0 +1,298 @@
+// Shared pieces of the flash-decoding split kernels (gfx950): arguments, the
+// online-softmax step, the workgroup merge of the waves' partials and the
+// q operands of the quantized kernel.
+#pragma once
+
+#include <type_traits>
+#include <utility>
+
+#include "tkv_codec.h"
+#include "tkv_quant.h"
+#include "../../include/tkv.h"
+
+namespace tkv {
+
+struct SplitParams {
+  const void* q;
+  const uint8_t* k;
+  const uint16_t* ks;
+  const uint16_t* kz;
+  const uint8_t* v;
+  const uint16_t* vs;
+  const uint16_t* vz;
+  const int32_t* seq_lens;
+  float* acc;
+  float* maxs;
+  float* sums;
+  float* out;
+  int* counters;  // fused-combine tickets, or null
+  // Paged caches (page_size > 0): the K/V tensors are pools of pages laid out
+  // (num_pages, HKV, page_size, ...); logical page p of batch row b is pool
+  // page block_table[b * bt_stride + p].  S = bt_stride * page_size.
+  const int32_t* block_table;
+  int bt_stride, page_size, num_pages;
+  // Fused append (quantized path): if k_new is set, the token at L_b - 1 of
+  // every (b, kv head) is k_new/v_new[b][kv] (fp16, or fp32 if new_fp32),
+  // quantized into the cache by the step itself.
+  const void* k_new;
+  const void* v_new;
+  int new_fp32;
+  int HQ, HKV, S, G, num_splits, split_size, q_fp32;
+  float qk_scale;  // sm_scale * log2(e)
+};
+
+constexpr int kChunk = 32;  // tokens per wave iteration (two 16-row MFMA tiles)
+
+// Cache policies of the streamed loads.
+constexpr int kPolF16 = kPolicyNT;       // fp16 control K and V rows
+constexpr int kPolDma = kPolicyNT;       // LDS-staged kernel: K/V code and metadata ranges
+
+// Token of k-slot i (0..7) of lane-group j within a chunk: the rows 4j..4j+3
+// of tile 0 followed by those of tile 1 -- the order in which the S^T
+// accumulators of the two tiles hand P^T to the V MFMA without any shuffle.
+__device__ __forceinline__ int slot_token(int j, int i) { return (i < 4 ? 0 : 12) + 4 * j + i; }
+
+
+// ---------------------------------------------------------------------------
+// Online softmax over one chunk.  x[8]: scores of this lane's 8 tokens for
+// its head, already -inf where masked; logit = x * lscale.  Updates m (shared
+// by the four lanes of a head) and the lane's partial l; returns alpha, the
+// factor the accumulators must be multiplied by (1 if no head moved), and the
+// probabilities as 4 fp16 pairs in slot order plus fp32 values.
+// ---------------------------------------------------------------------------
+struct ChunkProbs {
+  uint32_t ph[4];
+  float p[8];
+};
+
+template <bool TRACK_L = true>
+__device__ __forceinline__ bool softmax_chunk(const float (&x)[8], float lscale, float& m,
+                                              float& l, float& alpha, ChunkProbs& out) {
+  float mx = x[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) mx = fmaxf(mx, x[i]);
+  mx = xor_max16_32(mx) * lscale;
+  const bool moved = mx > m;
+  const bool any_moved = __builtin_amdgcn_ballot_w64(moved) != 0;
+  alpha = 1.0f;
+  if (any_moved) {
+    const float mn = fmaxf(m, mx);
+    alpha = safe_exp2_diff(m, mn);
+    m = mn;
+    if constexpr (TRACK_L) l *= alpha;
+  }
+  float sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    out.p[i] = __builtin_amdgcn_exp2f(fmaf(x[i], lscale, -m));
+    if constexpr (TRACK_L) sum += out.p[i];
+  }
+  if constexpr (TRACK_L) l += sum;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) out.ph[i] = pack_h2(out.p[2 * i], out.p[2 * i + 1]);
+  return any_moved;
+}
+
+// ---------------------------------------------------------------------------
+// Workgroup merge of the NW waves' (m, l, O) and the final store.
+// o_lds[w][n][d] holds each wave's unnormalised output for head n.
+// ---------------------------------------------------------------------------
+// Where a kernel keeps each wave's partial in LDS: output row n of wave w at
+// o + w * stride + n * (D + 1), its running max and sum at m / l + w * stride + n.
+struct MergeView {
+  float* o;
+  float* m;
+  float* l;
+  int stride;  // floats between consecutive waves
+  int* last;   // this workgroup holds the final ticket of its unit
+};
+
+template <int D>
+struct WavePartial {
+  float o[16][D + 1];
+  float m[16];
+  float l[16];
+};
+
+template <int D, int NW>
+struct MergeLds {
+  WavePartial<D> wp[NW];
+  int last;
+  __device__ MergeView view() {
+    constexpr int stride = sizeof(WavePartial<D>) / 4;
+    return MergeView{&wp[0].o[0][0], &wp[0].m[0], &wp[0].l[0], stride, &last};
+  }
+};
+
+template <int D, int NW>
+__device__ void merge_and_store(const SplitParams& prm, const MergeView& mv, int b, int h0,
+                                int nh, int split) {
+  __syncthreads();
+  const int tid = threadIdx.x;
+  for (int idx = tid; idx < nh * D; idx += NW * 64) {
+    const int n = idx / D, d = idx % D;
+    float mstar = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) mstar = fmaxf(mstar, mv.m[w * mv.stride + n]);
+    float o = 0.0f, l = 0.0f;
+    if (mstar != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const float f = safe_exp2_diff(mv.m[w * mv.stride + n], mstar);
+        o = fmaf(f, mv.o[w * mv.stride + n * (D + 1) + d], o);
+        l = fmaf(f, mv.l[w * mv.stride + n], l);
+      }
+    }
+    const int64_t row = (int64_t)b * prm.HQ + h0 + n;
+    if (prm.num_splits == 1) {
+      prm.out[row * D + d] = o / l;
+    } else {
+      const int64_t pr = row * prm.num_splits + split;
+      prm.acc[pr * D + d] = o;
+      if (d == 0) {
+        prm.maxs[pr] = mstar;
+        prm.sums[pr] = l;
+      }
+    }
+  }
+  if (prm.num_splits == 1 || prm.counters == nullptr) return;
+
+  // Fused combine.  Each workgroup releases its partials (agent scope: the
+  // reader may sit on another XCD with its own L2) and takes a ticket; the
+  // one that draws the last ticket acquires everyone's partials and merges
+  // the splits of its rows, then resets the counter for the next call.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __syncthreads();
+  const int cidx = (b * prm.HKV + h0 / prm.G) * ((prm.G + 15) / 16) + (h0 % prm.G) / 16;
+  if (tid == 0) {
+    const int t = __hip_atomic_fetch_add(prm.counters + cidx, 1, __ATOMIC_ACQ_REL,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    *mv.last = (t == prm.num_splits - 1);
+  }
+  __syncthreads();
+  if (!*mv.last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  constexpr int DQ = D / 4;
+  const int ns = prm.num_splits;
+  for (int idx = tid; idx < nh * DQ; idx += NW * 64) {
+    const int n = idx / DQ, dq = idx % DQ;
+    const int64_t row = (int64_t)b * prm.HQ + h0 + n;
+    float m = -INFINITY, l = 0.0f;
+    f4 a = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+    for (int s = 0; s < ns; ++s) {
+      const int64_t ps = row * ns + s;
+      const float ms = prm.maxs[ps];
+      const float ls = prm.sums[ps];
+      const f4 as = reinterpret_cast<const f4*>(prm.acc + ps * D)[dq];
+      if (ms == -INFINITY) continue;
+      const float mn = fmaxf(m, ms);
+      const float al = safe_exp2_diff(m, mn);
+      const float be = __builtin_amdgcn_exp2f(ms - mn);
+      a = a * al + as * be;
+      l = l * al + ls * be;
+      m = mn;
+    }
+    reinterpret_cast<f4*>(prm.out + row * D)[dq] = a / l;
+  }
+  if (tid == 0) __hip_atomic_store(prm.counters + cidx, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+
+// ---------------------------------------------------------------------------
+// Q^T as the B operand of the score MFMAs, in K slot order and pre-scaled by
+// 2^-(slice*KNB), plus the B operand of the K zero-point MFMA.  Lane-group j's
+// dims of step m are the contiguous run [m*KSTEP + CB*j, +CB): one vector load
+// per step, then slot order.  Lanes of heads >= nh hold zeros.
+// ---------------------------------------------------------------------------
+template <int D, int KNB, int GS>
+struct QOperands {
+  u4 qf[KLayout<D, KNB, GS>::NKM];
+  u2 qzb;
+};
+
+template <int D, int KNB, int GS>
+__device__ __forceinline__ void load_q_operands(const SplitParams& prm, int b, int h0, int n, int nh,
+                                                int j, QOperands<D, KNB, GS>& qo) {
+  using KL = KLayout<D, KNB, GS>;
+  constexpr int NG = D / GS;
+  constexpr int NKM = KL::NKM;
+  u4* qf = qo.qf;
+  u2& qzb = qo.qzb;
+  float qz[NG];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) qz[g] = 0.0f;
+  {
+    const bool hv = n < nh;
+    const int64_t qrow = ((int64_t)b * prm.HQ + h0 + (hv ? n : 0)) * D;
+    float qv[NKM][KL::CB];
+    if (prm.q_fp32) {
+      const float* qp = static_cast<const float*>(prm.q) + qrow;
+#pragma unroll
+      for (int m = 0; m < NKM; ++m)
+#pragma unroll
+        for (int c = 0; c < KL::CB; c += 4) {
+          const f4 v = *reinterpret_cast<const f4*>(qp + m * KL::KSTEP + KL::CB * j + c);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) qv[m][c + e] = (float)(_Float16)v[e];
+        }
+    } else {
+      const _Float16* qp = static_cast<const _Float16*>(prm.q) + qrow;
+#pragma unroll
+      for (int m = 0; m < NKM; ++m) {
+        if constexpr (KL::CB == 8) {
+          const h8 v = *reinterpret_cast<const h8*>(qp + m * KL::KSTEP + KL::CB * j);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) qv[m][e] = (float)v[e];
+        } else {
+          const h4 v = *reinterpret_cast<const h4*>(qp + m * KL::KSTEP + KL::CB * j);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) qv[m][e] = (float)v[e];
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < NKM; ++m) {
+      const int p = KL::slice_of(m, j);
+      const float pre = __builtin_ldexpf(1.0f, -p * KNB);
+      uint32_t wv[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int s2 = 0; s2 < KL::CB; s2 += 2) {
+        const float q0 = hv ? qv[m][slot_byte(s2)] : 0.0f;
+        const float q1 = hv ? qv[m][slot_byte(s2 + 1)] : 0.0f;
+        qz[KL::group_of_step(m)] += q0 + q1;
+        wv[s2 / 2] = pack_h2(q0 * pre, q1 * pre);
+      }
+      qf[m] = u4{wv[0], wv[1], wv[2], wv[3]};
+    }
+#pragma unroll
+    for (int g = 0; g < NG; ++g) qz[g] = xor_sum16_32(qz[g]);
+  }
+  // B operand of the K zero-point MFMA: k-slot k < NG holds fp16(Qz_k),
+  // NG <= k < 2NG the fp16 remainder Qz - fp16(Qz), so the product with the
+  // exact fp16 zero points keeps fp32 precision.
+  {
+    float hl[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = 4 * j + i;
+      float v = 0.0f;
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        const float hi16 = (float)(_Float16)qz[g];
+        if (k == g) v = hi16;
+        if (k == NG + g) v = qz[g] - hi16;
+      }
+      hl[i] = v;
+    }
+    qzb = u2{pack_h2(hl[0], hl[1]), pack_h2(hl[2], hl[3])};
+  }
+}
+
+}  // namespace tkv

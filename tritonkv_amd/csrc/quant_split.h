@@ -1,0 +1,650 @@
+// The fused 2/4-bit quantized split kernel (gfx950) and its launcher.
+// Included by quant_split_k*v*.hip, which instantiate the launcher for one
+// K/V bit-width pair each.
+#pragma once
+
+#include "decode_common.h"
+
+namespace tkv {
+
+// ===========================================================================
+// Fused quantized split kernel.
+//
+// Every chunk (32 tokens) of K codes, V codes and the four metadata tensors is
+// copied by direct-to-LDS buffer loads (buffer_load_dword{,x4} ... lds) into a
+// per-wave ring of NSTAGE stages, NSTAGE-1 chunks ahead of the compute.  Each
+// load instruction moves whole 16-byte lanes of a contiguous range, so every
+// line of the cache is fetched once with the non-temporal policy, and the
+// prefetch depth costs LDS instead of VGPRs.  The MFMA operands are then
+// gathered from LDS:
+//   K, V codes  blocks of 16 tokens, each block [16-byte unit][token]: every
+//               DMA instruction still copies one contiguous kilobyte, and the
+//               16 rows of an MFMA tile read from one unit are 16 consecutive
+//               entries, so the operand reads spread over the banks;
+//   metadata    the global layout [t][g] of each tensor, one dword DMA per
+//               lane; pairs of tokens are gathered with v_perm_b32.
+// Scores, softmax and PV follow the design notes at the top of this file.
+// ===========================================================================
+template <int D, int KNB, int VNB, int GS>
+struct StageGeom {
+  using KL = KLayout<D, KNB, GS>;
+  using VL = VLayout<D, VNB, GS>;
+  static constexpr int NG = D / GS;
+  // fp16 slots per token row of a staged metadata tensor: the global row of NG
+  // values, except NG == 1, whose rows are copied one fp16 per dword (a dword
+  // copy of 2-byte rows could straddle the end of the buffer range).
+  static constexpr int MROW = NG >= 2 ? NG : 2;
+  static constexpr int KB = kChunk * KL::DP;    // K code bytes per chunk
+  static constexpr int VB = kChunk * VL::DP;    // V code bytes per chunk
+  static constexpr int MB = kChunk * MROW * 2;  // bytes of one staged metadata tensor
+  static constexpr int K_OFF = 0;
+  static constexpr int V_OFF = K_OFF + KB;
+  static constexpr int M_OFF = V_OFF + VB;    // ks, kz, vs, vz at M_OFF + t * MB
+  static constexpr int BYTES = M_OFF + 4 * MB;
+  static constexpr int NKI = (KB + 1023) / 1024;  // 16-byte-lane DMA instructions for K
+  static constexpr int NVI = (VB + 1023) / 1024;
+  static constexpr int NMI = (MB + 255) / 256;    // dword-lane DMA instructions per tensor
+  static constexpr int NINSTR = NKI + NVI + 4 * NMI;
+  static_assert(KB % 512 == 0 && VB % 512 == 0 && MB % 64 == 0, "chunk sizes");
+
+  // Staged K/V code layout: blocks of 16 tokens, each block [unit][token]:
+  // 16-byte unit u of token t sits at position
+  //   (t / 16) * 16 * NU + 16 * u + t % 16          (NU = DP / 16 units per row)
+  // so a block is one contiguous 16 * DP bytes of the cache, and the 16 rows an
+  // MFMA tile reads from one unit are 16 consecutive 16-byte entries.
+  template <int DP>
+  __device__ static constexpr int pos_of(int t, int u) {
+    return (t >> 4) * 16 * (DP / 16) + 16 * u + (t & 15);
+  }
+  template <int DP>
+  __device__ static constexpr int token_of(int pos) {
+    return 16 * (pos / (16 * (DP / 16))) + (pos & 15);
+  }
+  template <int DP>
+  __device__ static constexpr int unit_of(int pos) {
+    return (pos % (16 * (DP / 16))) >> 4;
+  }
+};
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+__device__ __forceinline__ lds_ptr_t to_lds(void* p) {
+  return (lds_ptr_t)(uintptr_t)(uint32_t)(uintptr_t)p;
+}
+
+// Direct-to-LDS buffer loads of 16 / 4 bytes per lane (lane L writes
+// lds + L * size).  Plain functions per cache policy: the builtin is device-only.
+__device__ __forceinline__ void dma16_default(rsrc_t r, lds_ptr_t lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, off, 0, 0, kPolicyDefault);
+}
+__device__ __forceinline__ void dma16_nt(rsrc_t r, lds_ptr_t lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, off, 0, 0, kPolicyNT);
+}
+__device__ __forceinline__ void dma4_default(rsrc_t r, lds_ptr_t lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 4, off, 0, 0, kPolicyDefault);
+}
+__device__ __forceinline__ void dma4_nt(rsrc_t r, lds_ptr_t lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 4, off, 0, 0, kPolicyNT);
+}
+// 2 bytes per lane, zero-extended into a dword at lds + 4 * L.
+__device__ __forceinline__ void dma2_default(rsrc_t r, lds_ptr_t lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 2, off, 0, 0, kPolicyDefault);
+}
+__device__ __forceinline__ void dma2_nt(rsrc_t r, lds_ptr_t lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 2, off, 0, 0, kPolicyNT);
+}
+template <int POL>
+__device__ __forceinline__ void dma16(rsrc_t r, lds_ptr_t lds, uint32_t off) {
+  if constexpr (POL == kPolicyNT) dma16_nt(r, lds, off);
+  else dma16_default(r, lds, off);
+}
+template <int POL>
+__device__ __forceinline__ void dma4(rsrc_t r, lds_ptr_t lds, uint32_t off) {
+  if constexpr (POL == kPolicyNT) dma4_nt(r, lds, off);
+  else dma4_default(r, lds, off);
+}
+template <int POL>
+__device__ __forceinline__ void dma2(rsrc_t r, lds_ptr_t lds, uint32_t off) {
+  if constexpr (POL == kPolicyNT) dma2_nt(r, lds, off);
+  else dma2_default(r, lds, off);
+}
+
+// f(std::integral_constant<int, I>) for I = 0 .. N-1, unrolled at compile time.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// vmcnt-only wait (gfx9 encoding: vmcnt[3:0] | expcnt 7 | lgkmcnt 15 | vmcnt[5:4]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+__device__ __forceinline__ void wait_lgkmcnt0() {
+  __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));
+}
+
+// Issue the DMA of one chunk into a stage.  `valid` false turns every lane's
+// offset out of the buffer range, so the instructions still retire (keeping
+// the vmcnt arithmetic static) but read nothing and write zeros.
+template <int D, int KNB, int VNB, int GS>
+__device__ __forceinline__ void issue_chunk(uint8_t* stage, const rsrc_t& rk, const rsrc_t& rv,
+                                            const rsrc_t (&rm)[4], int cb, bool valid, int lane) {
+  // cb: index, within the resources, of the chunk's first row
+  using SG = StageGeom<D, KNB, VNB, GS>;
+  using KL = typename SG::KL;
+  using VL = typename SG::VL;
+  constexpr uint32_t kOut = 0x80000000u;
+  // K / V: instruction q copies the contiguous kilobyte [1024q, 1024q + 1024)
+  // of the chunk (whole lines).  Lane L takes the 16-byte unit that belongs at
+  // stage position 64q + L of the layout described at the top of this kernel.
+#pragma unroll
+  for (int q = 0; q < SG::NKI; ++q) {
+    const int t = SG::template token_of<KL::DP>(64 * q + lane);
+    const int u = SG::template unit_of<KL::DP>(64 * q + lane);
+    const uint32_t off = valid ? (uint32_t)(cb + t) * KL::DP + 16 * u : kOut;
+    if (SG::KB >= 1024 || lane < SG::KB / 16)
+      dma16<kPolDma>(rk, to_lds(stage + SG::K_OFF + 1024 * q), off);
+  }
+#pragma unroll
+  for (int q = 0; q < SG::NVI; ++q) {
+    const int t = SG::template token_of<VL::DP>(64 * q + lane);
+    const int u = SG::template unit_of<VL::DP>(64 * q + lane);
+    const uint32_t off = valid ? (uint32_t)(cb + t) * VL::DP + 16 * u : kOut;
+    if (SG::VB >= 1024 || lane < SG::VB / 16)
+      dma16<kPolDma>(rv, to_lds(stage + SG::V_OFF + 1024 * q), off);
+  }
+  // metadata: the chunk's [t][g] rows are contiguous; lane L copies dword L
+  // (NG == 1: the fp16 of token L, into dword L).
+#pragma unroll
+  for (int tsr = 0; tsr < 4; ++tsr)
+#pragma unroll
+    for (int q = 0; q < SG::NMI; ++q) {
+      uint8_t* dst = stage + SG::M_OFF + tsr * SG::MB + 256 * q;
+      if constexpr (SG::NG == 1) {
+        const uint32_t off = valid ? (uint32_t)(cb + lane) * 2 : kOut;
+        if (lane < kChunk) dma2<kPolDma>(rm[tsr], to_lds(dst), off);
+      } else {
+        const uint32_t off = valid ? (uint32_t)cb * SG::NG * 2 + 4 * (64 * q + lane) : kOut;
+        if (SG::MB >= 256 || lane < SG::MB / 4) dma4<kPolDma>(rm[tsr], to_lds(dst), off);
+      }
+    }
+}
+
+template <int D, int KNB, int VNB, int GS, int NW, int NSTAGE>
+struct LdsKernelSmem {
+  using SG = StageGeom<D, KNB, VNB, GS>;
+  static constexpr int RING = NSTAGE * SG::BYTES;
+  // After the loop the ring holds the wave's partial (and, in wave 0, the
+  // workgroup's combine ticket flag right behind it).
+  static constexpr int OUT = (int)sizeof(WavePartial<D>) + 16;
+  static constexpr int WAVE = ((RING > OUT ? RING : OUT) + 15) / 16 * 16;
+  // Fused append: the new token's row in staged form (K bytes, V bytes, then
+  // the fp16 scale/zero of K and V, NG each), behind the waves' rings.
+  static constexpr int PATCH_META = SG::KL::DP + SG::VL::DP;
+  static constexpr int PATCH = (PATCH_META + 4 * SG::NG * 2 + 15) / 16 * 16;
+};
+
+template <int D, int KNB, int VNB, int GS, int NW, int NSTAGE, bool PAGED>
+__global__ void __launch_bounds__(NW * 64)
+quant_split_lds_kernel(SplitParams prm) {
+  using SG = StageGeom<D, KNB, VNB, GS>;
+  using KL = typename SG::KL;
+  using VL = typename SG::VL;
+  using SM = LdsKernelSmem<D, KNB, VNB, GS, NW, NSTAGE>;
+  constexpr int NG = SG::NG;
+  constexpr int NKM = KL::NKM;
+  constexpr int NVM = VL::NVM;
+  constexpr int NI = SG::NINSTR;
+  static_assert(2 * NG <= 16, "zero-point MFMA holds hi/lo of at most 8 groups");
+  static_assert((NSTAGE - 1) * NI < 64, "vmcnt range");
+
+  __shared__ __attribute__((aligned(16))) uint8_t smem[NW * SM::WAVE + SM::PATCH];
+
+  const int split = blockIdx.x;
+  const int unit = blockIdx.y;
+  const int b = unit / prm.HKV, hk = unit % prm.HKV;
+  const int hb0 = blockIdx.z * 16;
+  const int nh = min(16, prm.G - hb0);
+  const int h0 = hk * prm.G + hb0;
+  const int L = prm.seq_lens ? min(prm.seq_lens[b], prm.S) : prm.S;
+  const int lo = split * prm.split_size;
+  const int hi = min(lo + prm.split_size, L);
+  const int last = hi - 1;
+
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int r = lane & 15, j = lane >> 4;
+  const int n = r;
+  // Where a chunk's rows live.  Contiguous caches: one buffer resource per
+  // tensor over this (b, kv head) block, chunk rows at token index cb.  Paged
+  // caches: resources over the (pool page, kv head) slab holding the chunk
+  // (chunks never straddle a page: page_size % 32 == 0), rows at cb % page.
+  // Either way the hardware range check returns zeros past the resource.
+  struct ChunkSrc {
+    rsrc_t k, v, m[4];
+    int row;
+  };
+  auto slab_src = [&](int64_t slab, int rows, int row) -> ChunkSrc {
+    return ChunkSrc{make_rsrc(prm.k + slab * rows * KL::DP, (uint32_t)rows * KL::DP),
+                    make_rsrc(prm.v + slab * rows * VL::DP, (uint32_t)rows * VL::DP),
+                    {make_rsrc(prm.ks + slab * rows * NG, (uint32_t)rows * NG * 2),
+                     make_rsrc(prm.kz + slab * rows * NG, (uint32_t)rows * NG * 2),
+                     make_rsrc(prm.vs + slab * rows * NG, (uint32_t)rows * NG * 2),
+                     make_rsrc(prm.vz + slab * rows * NG, (uint32_t)rows * NG * 2)},
+                    row};
+  };
+  const ChunkSrc unit_src = slab_src(PAGED ? 0 : (int64_t)unit, PAGED ? prm.page_size : prm.S, 0);
+  auto chunk_src = [&](int cb, int page) -> ChunkSrc {
+    if constexpr (PAGED)
+      return slab_src((int64_t)page * prm.HKV + hk, prm.page_size,
+                      (int)((uint32_t)cb % (uint32_t)prm.page_size));
+    else
+      return ChunkSrc{unit_src.k, unit_src.v, {unit_src.m[0], unit_src.m[1], unit_src.m[2], unit_src.m[3]}, cb};
+  };
+  // Paged: block-table entries are read with vector loads, each issued right
+  // behind a chunk's DMA for the chunk two steps ahead, so it retires with
+  // the next step's wait and no lookup ever stalls the stream.  Entries of
+  // chunks at or past the end of the split are never read (their offset is
+  // out of range and reads 0), and every entry is clamped into the pool, so a
+  // bad entry can only select another page, never leave the pool.
+  const rsrc_t rtab = make_rsrc(prm.block_table + (PAGED ? (int64_t)b * prm.bt_stride : 0),
+                                PAGED ? (uint32_t)prm.bt_stride * 4u : 0u);
+  auto tab_entry = [&](int c) -> uint32_t {
+    return buf_u32<kPolicyDefault>(
+        rtab, c < hi ? (uint32_t)c / (uint32_t)prm.page_size * 4u : 0x80000000u);
+  };
+  auto to_page = [&](uint32_t e) -> int {
+    return min(max((int)__builtin_amdgcn_readfirstlane(e), 0), prm.num_pages - 1);
+  };
+  uint8_t* ring = smem + w * SM::WAVE;
+
+  // Chunk k of this wave starts at token lo + 32 * (w + NW * k).
+  const int cb0 = lo + kChunk * w;
+  const int cstride = kChunk * NW;
+  static_assert(NSTAGE >= 2 && (!PAGED || NSTAGE == 2), "ring depth");
+  // Paged: page_next is the pool page of the chunk whose DMA is issued next;
+  // tab_pending the (in-flight) table entry of the chunk after that.
+  int page_next = 0;
+  uint32_t tab_pending = 0;
+  if constexpr (PAGED) {
+    const uint32_t e0 = tab_entry(cb0), e1 = tab_entry(cb0 + cstride);
+    const int page0 = to_page(e0);
+    page_next = to_page(e1);
+    const ChunkSrc src = chunk_src(cb0, page0);
+    issue_chunk<D, KNB, VNB, GS>(ring, src.k, src.v, src.m, src.row, cb0 < hi, lane);
+    tab_pending = tab_entry(cb0 + 2 * cstride);
+  } else {
+    // the first NSTAGE - 1 chunks into stages 0 .. NSTAGE - 2
+    static_for<NSTAGE - 1>([&](auto s) __attribute__((always_inline)) {
+      constexpr int SS = decltype(s)::value;
+      const int c = cb0 + SS * cstride;
+      const ChunkSrc src = chunk_src(c, 0);
+      issue_chunk<D, KNB, VNB, GS>(ring + SS * SG::BYTES, src.k, src.v, src.m, src.row, c < hi, lane);
+    });
+  }
+
+
+  QOperands<D, KNB, GS> qo;
+  load_q_operands<D, KNB, GS>(prm, b, h0, n, nh, j, qo);
+  const u4* qf = qo.qf;
+  const u2 qzb = qo.qzb;
+
+  // ---- fused append ----------------------------------------------------------
+  // The token at L - 1 comes from k_new / v_new.  The wave whose chunk holds it
+  // quantizes the row here (quantize_row, the append kernel's own code), keeps
+  // the row in the workgroup's patch area and, in the first block of query
+  // heads, stores it into the cache.  Once that chunk's DMA has landed the wave
+  // overwrites the chunk's row with the patch, so the step never depends on
+  // when the store becomes visible to its own loads.
+  uint8_t* const patch = smem + NW * SM::WAVE;
+  int cb_new = -1;  // first token of the chunk this wave patches, or -1
+  int t_new = 0;    // the new token's row within that chunk
+  if (prm.k_new && L - 1 >= lo && L - 1 < hi && ((L - 1 - lo) / kChunk) % NW == w) {
+    const int tn = L - 1;
+    int64_t row = (int64_t)unit * prm.S + tn;
+    bool use = true;
+    if constexpr (PAGED) {
+      const int e = prm.block_table[(int64_t)b * prm.bt_stride + tn / prm.page_size];
+      use = e >= 0 && e < prm.num_pages;  // as the append kernel: such a token is not stored
+      row = ((int64_t)e * prm.HKV + hk) * prm.page_size + tn % prm.page_size;
+    }
+    if (use) {
+      cb_new = lo + kChunk * ((tn - lo) / kChunk);
+      t_new = tn - cb_new;
+      const int64_t xoff = (int64_t)unit * D * (prm.new_fp32 ? 4 : 2);
+      float xk[KL::P], xv[VL::P];
+      load_row_for_quant<D, KNB>(static_cast<const uint8_t*>(prm.k_new) + xoff, prm.new_fp32, lane, xk);
+      load_row_for_quant<D, VNB>(static_cast<const uint8_t*>(prm.v_new) + xoff, prm.new_fp32, lane, xv);
+      const RowQuant<D, KNB, GS> rk = quantize_row<D, KNB, GS>(xk, lane);
+      const RowQuant<D, VNB, GS> rv = quantize_row<D, VNB, GS>(xv, lane);
+      uint16_t* pmeta = reinterpret_cast<uint16_t*>(patch + SM::PATCH_META);
+      if (lane < KL::DP) patch[lane] = (uint8_t)rk.byte;
+      if (lane < VL::DP) patch[KL::DP + lane] = (uint8_t)rv.byte;
+      if (lane < NG) {
+        pmeta[lane] = (uint16_t)(rk.meta & 0xFFFFu);
+        pmeta[NG + lane] = (uint16_t)(rk.meta >> 16);
+        pmeta[2 * NG + lane] = (uint16_t)(rv.meta & 0xFFFFu);
+        pmeta[3 * NG + lane] = (uint16_t)(rv.meta >> 16);
+      }
+      if (blockIdx.z == 0) {
+        if (lane < KL::DP) const_cast<uint8_t*>(prm.k)[row * KL::DP + lane] = (uint8_t)rk.byte;
+        if (lane < VL::DP) const_cast<uint8_t*>(prm.v)[row * VL::DP + lane] = (uint8_t)rv.byte;
+        if (lane < NG) {
+          const_cast<uint16_t*>(prm.ks)[row * NG + lane] = (uint16_t)(rk.meta & 0xFFFFu);
+          const_cast<uint16_t*>(prm.kz)[row * NG + lane] = (uint16_t)(rk.meta >> 16);
+          const_cast<uint16_t*>(prm.vs)[row * NG + lane] = (uint16_t)(rv.meta & 0xFFFFu);
+          const_cast<uint16_t*>(prm.vz)[row * NG + lane] = (uint16_t)(rv.meta >> 16);
+        }
+      }
+    }
+  }
+
+  uint32_t vsel[VL::NE];
+#pragma unroll
+  for (int e = 0; e < VL::NE; ++e) vsel[e] = VL::perm_sel(VL::byte_in_dword(e, r));
+  uint32_t kmask[NKM];
+#pragma unroll
+  for (int m = 0; m < NKM; ++m) kmask[m] = slice_mask<KNB>(KL::slice_of(m, j));
+
+  constexpr bool kVChain = NG == 1;  // all slices of a V byte in one group
+
+  // Per-lane LDS byte offsets inside a stage.
+  // K operand of tile a, load Lh: row 16a + r, byte load_offset(Lh, j).
+  uint32_t koff[KL::NLOAD];
+#pragma unroll
+  for (int Lh = 0; Lh < KL::NLOAD; ++Lh) {
+    const int ob = KL::load_offset(Lh, j);
+    koff[Lh] = SG::K_OFF + SG::template pos_of<KL::DP>(r, ob >> 4) * 16 + (ob & 15);
+  }
+  // V operand of slot i, window wi: token slot_token(j, i), dword dword_offset(wi, r).
+  uint32_t voff[VL::NWIN];
+#pragma unroll
+  for (int wi = 0; wi < VL::NWIN; ++wi) {
+    const int ob = VL::dword_offset(wi, r);
+    voff[wi] = SG::V_OFF + SG::template pos_of<VL::DP>(4 * j, ob >> 4) * 16 + (ob & 15);
+  }
+  // V zero point rows r < NG of the zero MFMA's A operand, zeros for r >= NG.
+  // Lane r < NG gathers group r's zero points of two tokens into one fp16
+  // pair with a single v_perm (low or high half of each token's dword); the
+  // selector of lanes r >= NG yields constant zero bytes.
+  // Row NG of that operand is all ones (fp16 1.0 pairs), so the same MFMA also
+  // accumulates sum_t p_t, the softmax denominator, from the very fp16
+  // probabilities the PV products use.
+  const int zr = r < NG ? r : 0;
+  const uint32_t zsel = r < NG ? ((r & 1) ? 0x07060302u : 0x05040100u) : 0x0C0C0C0Cu;
+  const uint32_t zones = r == NG ? 0x3C003C00u : 0u;
+
+  f4 accv[NVM];
+#pragma unroll
+  for (int mv = 0; mv < NVM; ++mv) accv[mv] = f4{0.f, 0.f, 0.f, 0.f};
+  f4 oz = f4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.0f;
+  const float lscale = prm.qk_scale * kTwo24;
+
+  // In the tail chunk, rows past the sequence hold whatever the cache holds
+  // there (possibly NaN/Inf bit patterns in scale/zero): their V scale and
+  // zero-point pairs are cleared, since p = 0 alone would not cancel them.
+  auto tail_pair_mask = [&](int tok0, int tok1) -> uint32_t {
+    return (tok0 <= last ? 0x0000FFFFu : 0u) | (tok1 <= last ? 0xFFFF0000u : 0u);
+  };
+  auto half_at = [&](const uint8_t* base, int idx) -> uint32_t {  // fp16 bits of element idx
+    return *reinterpret_cast<const uint16_t*>(base + 2 * idx);
+  };
+  // The dword holding element (t, g) of a staged [t][MROW] metadata tensor.
+  auto dword_at = [&](const uint8_t* base, int t, int g) -> uint32_t {
+    return *reinterpret_cast<const uint32_t*>(base + 2 * (t * SG::MROW + (g & ~1)));
+  };
+
+  // Chunk k of the wave uses stage k % NSTAGE; the loop below is unrolled by
+  // NSTAGE so every stage offset is a compile-time constant.
+  auto step = [&](int cb, auto tail, auto stage) __attribute__((always_inline)) {
+    constexpr bool TAIL = decltype(tail)::value;
+    constexpr int SK = decltype(stage)::value;
+    // refill the stage consumed by the previous chunk, NSTAGE-1 chunks ahead
+    {
+      const int cn = cb + (NSTAGE - 1) * cstride;
+      wait_lgkmcnt0();  // the previous chunk's LDS reads of that stage are done
+      asm volatile("" ::: "memory");
+      const bool valid = !TAIL && cn < hi;
+      const ChunkSrc src = chunk_src(cn, page_next);
+      issue_chunk<D, KNB, VNB, GS>(ring + ((SK + NSTAGE - 1) % NSTAGE) * SG::BYTES, src.k, src.v,
+                                   src.m, src.row, valid, lane);
+    }
+    // Paged: one more vector load in flight, behind the DMA just issued.
+    uint32_t tab_new = 0;
+    if constexpr (PAGED) tab_new = tab_entry(cb + 3 * cstride);
+    wait_vmcnt<(NSTAGE - 1) * NI + (PAGED ? 1 : 0)>();
+    asm volatile("" ::: "memory");  // no LDS read of this stage above the wait
+    if constexpr (PAGED) {  // retired with the wait above: issued a step ago
+      page_next = to_page(tab_pending);
+      tab_pending = tab_new;
+    }
+    // Fused append: the new token is the split's last (L - 1 = hi - 1), so its
+    // chunk is always a TAIL step; its row replaces what the DMA read.
+    if (TAIL && cb == cb_new) {
+      uint8_t* sw = ring + SK * SG::BYTES;
+      const uint16_t* pmeta = reinterpret_cast<const uint16_t*>(patch + SM::PATCH_META);
+      if (lane < KL::DP)
+        sw[SG::K_OFF + SG::template pos_of<KL::DP>(t_new, lane >> 4) * 16 + (lane & 15)] = patch[lane];
+      if (lane < VL::DP)
+        sw[SG::V_OFF + SG::template pos_of<VL::DP>(t_new, lane >> 4) * 16 + (lane & 15)] =
+            patch[KL::DP + lane];
+      if (lane < 4 * NG)
+        *reinterpret_cast<uint16_t*>(sw + SG::M_OFF + (lane / NG) * SG::MB +
+                                     2 * (t_new * SG::MROW + lane % NG)) = pmeta[lane];
+    }
+    const uint8_t* st = ring + SK * SG::BYTES;
+    const uint8_t* mks = st + SG::M_OFF;
+    const uint8_t* mkz = mks + SG::MB;
+    const uint8_t* mvs = mkz + SG::MB;
+    const uint8_t* mvz = mvs + SG::MB;
+
+    // ---- scores S^T for the two 16-token tiles ---------------------------
+    float x[8];
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      f4 c[NG];
+#pragma unroll
+      for (int g = 0; g < NG; ++g) c[g] = f4{0.f, 0.f, 0.f, 0.f};
+      typename std::conditional<KL::CB == 8, u2, uint32_t>::type kx[KL::NLOAD];
+#pragma unroll
+      for (int Lh = 0; Lh < KL::NLOAD; ++Lh) {
+        // tile a = rows 16a.. = block a: 16 * NU entries further
+        constexpr int kTile = 16 * (KL::DP / 16) * 16;
+        if constexpr (KL::CB == 8) kx[Lh] = *reinterpret_cast<const u2*>(st + koff[Lh] + kTile * a);
+        else kx[Lh] = *reinterpret_cast<const uint32_t*>(st + koff[Lh] + kTile * a);
+      }
+#pragma unroll
+      for (int m = 0; m < NKM; ++m) {
+        const int g = KL::group_of_step(m);
+        if constexpr (KL::CB == 8)
+          c[g] = mfma_k32(k_extract8(kx[KL::load_of_step(m)], kmask[m]), qf[m], c[g]);
+        else
+          c[g] = mfma_k16(k_extract4(kx[KL::load_of_step(m)], kmask[m]), u2{qf[m][0], qf[m][1]}, c[g]);
+      }
+      // zero-point part: A row = token 16a + r, k-slots = its NG zero points
+      u2 za;
+      {
+        const uint8_t* zr = mkz + (16 * a + r) * SG::MROW * 2;
+        if constexpr (NG == 8) {
+          const u4 z8 = *reinterpret_cast<const u4*>(zr);
+          za = (j & 1) ? u2{z8[2], z8[3]} : u2{z8[0], z8[1]};
+        } else if constexpr (NG == 4) {
+          za = *reinterpret_cast<const u2*>(zr);
+        } else if constexpr (NG == 2) {
+          const uint32_t z2 = *reinterpret_cast<const uint32_t*>(zr);
+          za = u2{z2, z2};
+        } else {
+          const uint32_t z1 = *reinterpret_cast<const uint16_t*>(zr);
+          za = u2{z1 | (z1 << 16), 0u};
+        }
+      }
+      const f4 yz = mfma_k16(za, qzb, f4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * a + 4 * j + i;
+        float sc = yz[i] * kTwoM24;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          const float sv = (float)__builtin_bit_cast(_Float16, (uint16_t)half_at(mks, t * SG::MROW + g));
+          sc = fmaf(sv, c[g][i], sc);
+        }
+        x[4 * a + i] = sc;
+      }
+    }
+    if constexpr (TAIL) {
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (cb + 16 * a + 4 * j + i > last) x[4 * a + i] = -INFINITY;
+    }
+
+    // ---- online softmax ---------------------------------------------------
+    float alpha;
+    ChunkProbs pr;
+    if (softmax_chunk<false>(x, lscale, m_run, l_run, alpha, pr)) {
+#pragma unroll
+      for (int mv = 0; mv < NVM; ++mv) accv[mv] *= alpha;
+      oz *= alpha;
+    }
+    const u4 pb = u4{pr.ph[0], pr.ph[1], pr.ph[2], pr.ph[3]};
+
+    // ---- V zero point: oz += Z^T P (A rows = groups, k = the lane's 8 tokens)
+    {
+      uint32_t zp[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int t0 = slot_token(j, 2 * q), t1 = slot_token(j, 2 * q + 1);
+        zp[q] = perm(dword_at(mvz, t1, zr), dword_at(mvz, t0, zr), zsel);
+        if constexpr (TAIL) zp[q] &= tail_pair_mask(cb + t0, cb + t1);
+        zp[q] |= zones;
+      }
+      oz = mfma_k32(u4{zp[0], zp[1], zp[2], zp[3]}, pb, oz);
+    }
+    // ---- P'_g = P * s_g ------------------------------------------------------
+    u4 pg[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      uint32_t sp[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int t0 = slot_token(j, 2 * q), t1 = slot_token(j, 2 * q + 1);
+        sp[q] = perm(dword_at(mvs, t1, g), dword_at(mvs, t0, g), (g & 1) ? 0x07060302u : 0x05040100u);
+        if constexpr (TAIL) sp[q] &= tail_pair_mask(cb + t0, cb + t1);
+      }
+      pg[g] = u4{pk_mul(pb[0], sp[0]), pk_mul(pb[1], sp[1]), pk_mul(pb[2], sp[2]), pk_mul(pb[3], sp[3])};
+    }
+
+    // ---- O^T += V^T P'^T ---------------------------------------------------
+#pragma unroll
+    for (int wi = 0; wi < VL::NWIN; ++wi) {
+      uint32_t vx[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        // slot i: token 4j + i (block 0) or 16 + 4j + i - 4 (block 1)
+        vx[i] = *reinterpret_cast<const uint32_t*>(
+            st + voff[wi] + (i < 4 ? 0 : 16 * (VL::DP / 16) * 16) + 16 * (i & 3));
+#pragma unroll
+      for (int e = 0; e < VL::NE; ++e) {
+        uint32_t pm[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pm[i] = perm(vx[2 * i + 1], vx[2 * i], vsel[e]);
+        // With one group per row (NG == 1) every slice of a byte shares the
+        // same P', so slice p's MFMA may take the byte with only the slices
+        // below p cleared (p = 0: the raw byte): its accumulator holds the
+        // codes of slices >= p at their bit positions, and slice p alone is
+        // recovered after the loop as acc[p] - acc[p + 1] -- one AND fewer
+        // per byte pair.  Otherwise each slice is isolated by its own mask.
+#pragma unroll
+        for (int p = 0; p < VL::P; ++p) {
+          const int mv = VL::mfma_index(p, wi, e);
+          const uint32_t msk = kVChain ? hi_slices_mask<VNB>(p) : slice_mask<VNB>(p);
+          const u4 av = (kVChain && p == 0) ? u4{pm[0], pm[1], pm[2], pm[3]}
+                                            : u4{pm[0] & msk, pm[1] & msk, pm[2] & msk, pm[3] & msk};
+          accv[mv] = mfma_k32(av, pg[VL::group_of(mv)], accv[mv]);
+        }
+      }
+    }
+  };
+
+  // Runs of NSTAGE chunks that end before the split's last token (stages
+  // 0 .. NSTAGE-1), then what is left: at most NSTAGE - 1 such chunks and the
+  // chunk holding the last token, which always runs as the TAIL step (even
+  // when it is full).  A single loop exit keeps the accumulators in place
+  // across the unrolled copies.
+  int cb = cb0;
+  for (; cb + (NSTAGE - 1) * cstride + kChunk < hi; cb += NSTAGE * cstride) {
+    static_for<NSTAGE>([&](auto s) __attribute__((always_inline)) {
+      step(cb + decltype(s)::value * cstride, std::false_type{}, s);
+    });
+  }
+  bool more = true;
+  static_for<NSTAGE>([&](auto s) __attribute__((always_inline)) {
+    if (more) {
+      if (cb + kChunk < hi) {
+        step(cb, std::false_type{}, s);
+        cb += cstride;
+      } else {
+        if (cb < hi) step(cb, std::true_type{}, s);
+        more = false;
+      }
+    }
+  });
+  wait_vmcnt<0>();  // retire the trailing (out-of-range) prefetches
+  wave_lds_fence();
+
+  // ---- this wave's partial into its own ring region -------------------------
+  WavePartial<D>& wp = *reinterpret_cast<WavePartial<D>*>(ring);
+  {
+    const float lt = __shfl(oz[NG % 4], 16 * (NG / 4) + n, 64);  // the ones row
+    float ozg[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) ozg[g] = __shfl(oz[g % 4], 16 * (g / 4) + n, 64);
+#pragma unroll
+    for (int mv = 0; mv < NVM; ++mv) {
+      const int p = VL::slice_of(mv);
+      const float fac = kTwo24 * __builtin_ldexpf(1.0f, -p * VNB);
+      const float zv = ozg[VL::group_of(mv)];
+      f4 a = accv[mv];
+      if (kVChain && p + 1 < VL::P) a -= accv[VL::mfma_index(p + 1, VL::window_of(mv), VL::e_of(mv))];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wp.o[n][VL::dim_of(mv, 4 * j + i)] = fmaf(a[i], fac, zv);
+    }
+    if (j == 0) {
+      wp.m[n] = m_run;
+      wp.l[n] = lt;
+    }
+  }
+  WavePartial<D>& wp0 = *reinterpret_cast<WavePartial<D>*>(smem);
+  const MergeView view{&wp0.o[0][0], &wp0.m[0], &wp0.l[0], SM::WAVE / 4,
+                       reinterpret_cast<int*>(smem + sizeof(WavePartial<D>))};
+  merge_and_store<D, NW>(prm, view, b, h0, nh, split);
+}
+
+// Ring depth per wave of the quantized split kernel.  8-wave workgroups run
+// one per CU (VGPRs), so their LDS could hold three stages, but a third stage
+// measured slightly slower at the Llama-3-8B shape (208 vs 206 us): one chunk
+// in flight per wave already saturates what this access pattern streams.
+// Paged caches use two stages.
+constexpr int kStages8 = 2;
+constexpr int kStages4 = 2;
+
+template <int D, int KNB, int VNB, int GS>
+void launch_quant(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
+  const bool paged = p.page_size > 0;
+  if (waves == 8) {
+    if (paged) quant_split_lds_kernel<D, KNB, VNB, GS, 8, 2, true><<<grid, dim3(8 * 64), 0, st>>>(p);
+    else quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false><<<grid, dim3(8 * 64), 0, st>>>(p);
+  } else {
+    if (paged) quant_split_lds_kernel<D, KNB, VNB, GS, 4, 2, true><<<grid, dim3(4 * 64), 0, st>>>(p);
+    else quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false><<<grid, dim3(4 * 64), 0, st>>>(p);
+  }
+}
+
+}  // namespace tkv

@@ -1,0 +1,14 @@
+// quant_split_lds_kernel instantiations for 4-bit K and 4-bit V codes.
+#include "quant_split.h"
+
+namespace tkv {
+
+template void launch_quant<128, 4, 4, 16>(const SplitParams&, dim3, int, hipStream_t);
+template void launch_quant<128, 4, 4, 32>(const SplitParams&, dim3, int, hipStream_t);
+template void launch_quant<128, 4, 4, 64>(const SplitParams&, dim3, int, hipStream_t);
+template void launch_quant<128, 4, 4, 128>(const SplitParams&, dim3, int, hipStream_t);
+template void launch_quant<64, 4, 4, 16>(const SplitParams&, dim3, int, hipStream_t);
+template void launch_quant<64, 4, 4, 32>(const SplitParams&, dim3, int, hipStream_t);
+template void launch_quant<64, 4, 4, 64>(const SplitParams&, dim3, int, hipStream_t);
+
+}  // namespace tkv
