@@ -176,6 +176,116 @@ __device__ __forceinline__ void issue_chunk(uint8_t* stage, const rsrc_t& rk, co
     }
 }
 
+// ---------------------------------------------------------------------------
+// Paired tiles, for GQA groups of at most 8 query heads.
+//
+// A 16x16 MFMA has 16 columns.  With G <= 8 heads per group, half or more of
+// them would carry padding heads, and every per-score instruction after the
+// score MFMAs (scale fold, softmax, exponentials) would spend that share of its
+// lanes on them.  Instead the two 16-token tiles of a chunk share one set of
+// MFMAs: column c = 8 * tile + head, and the K dimension is split between the
+// tiles (a block-diagonal B operand): lane groups j = 0, 1 carry tile 0's
+// codes, j = 2, 3 tile 1's, and their B entries hold q for columns of their
+// own tile and zero for the other.  Each MFMA covers 16 dims of both tiles
+// (D / 16 MFMAs, as many as two tiles x D / 32), and each lane ends up with
+// the 4 scores of one tile for one head: half the fold and softmax work.
+// The PV product keeps its layout: lane (j, c < 8) needs the probabilities of
+// head c for both tiles, which are its own and those of lane c + 8.
+// ---------------------------------------------------------------------------
+template <int D, int KNB, int GS>
+struct QOperandsPT {
+  static constexpr int P = 8 / KNB;
+  static constexpr int DP = D / P;
+  static constexpr int NU = DP / 16;  // 16-byte units per packed row
+  static constexpr int NB = D / 16;   // 16-dim blocks: block p * NU + u = unit u of slice p
+  u4 qb[NB];
+  u4 qzb;  // zero-point MFMA (K = 32): slots 8j + g hold hi (j even) or lo (j odd) of sum q_g
+};
+
+template <int D, int KNB, int GS>
+__device__ __forceinline__ void load_q_operands_pt(const SplitParams& prm, int b, int h0, int col,
+                                                   int nh, int j, QOperandsPT<D, KNB, GS>& qo) {
+  using QO = QOperandsPT<D, KNB, GS>;
+  constexpr int NG = D / GS;
+  const int h = col & 7;
+  const bool hv = h < nh;
+  const bool own = (col >> 3) == (j >> 1);  // these k-slots belong to this column's tile
+  const int64_t qrow = ((int64_t)b * prm.HQ + h0 + (hv ? h : 0)) * D;
+  float qz[NG];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) qz[g] = 0.0f;
+#pragma unroll
+  for (int p = 0; p < QO::P; ++p)
+#pragma unroll
+    for (int u = 0; u < QO::NU; ++u) {
+      const int d0 = p * QO::DP + 16 * u + 8 * (j & 1);
+      float qv[8];
+      if (prm.q_fp32) {
+        const float* qp = static_cast<const float*>(prm.q) + qrow + d0;
+        const f4 a = *reinterpret_cast<const f4*>(qp), c = *reinterpret_cast<const f4*>(qp + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          qv[e] = (float)(_Float16)a[e];
+          qv[4 + e] = (float)(_Float16)c[e];
+        }
+      } else {
+        const h8 v = *reinterpret_cast<const h8*>(static_cast<const _Float16*>(prm.q) + qrow + d0);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qv[e] = (float)v[e];
+      }
+      const int g = (p * QO::DP + 16 * u) / GS;
+      const float pre = __builtin_ldexpf(1.0f, -p * KNB);
+      uint32_t wv[4];
+#pragma unroll
+      for (int s2 = 0; s2 < 8; s2 += 2) {
+        const float q0 = hv ? qv[slot_byte(s2)] : 0.0f;
+        const float q1 = hv ? qv[slot_byte(s2 + 1)] : 0.0f;
+        qz[g] += q0 + q1;
+        wv[s2 / 2] = own ? pack_h2(q0 * pre, q1 * pre) : 0u;
+      }
+      qo.qb[p * QO::NU + u] = u4{wv[0], wv[1], wv[2], wv[3]};
+    }
+  // lanes j and j ^ 1 hold the two halves of every 16-dim block (j ^ 2 repeats them)
+#pragma unroll
+  for (int g = 0; g < NG; ++g) qz[g] += __shfl_xor(qz[g], 16, 64);
+  float hl[8];
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    float v = 0.0f;
+    if (g < NG && own) {
+      const float hi16 = (float)(_Float16)qz[g < NG ? g : 0];
+      v = (j & 1) ? qz[g < NG ? g : 0] - hi16 : hi16;
+    }
+    hl[g] = v;
+  }
+  qo.qzb = u4{pack_h2(hl[0], hl[1]), pack_h2(hl[2], hl[3]), pack_h2(hl[4], hl[5]),
+              pack_h2(hl[6], hl[7])};
+}
+
+// Online-softmax step of a paired-tile chunk: 4 scores per lane (one tile, one
+// head); the head's 32 tokens span lanes c and c ^ 8 of all four lane groups.
+// Returns whether any running max moved; ph holds the lane's fp16 pairs.
+__device__ __forceinline__ bool softmax_chunk_pt(const float (&x)[4], float lscale, float& m,
+                                                 float& alpha, uint32_t (&ph)[2]) {
+  float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+  mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
+  mx = xor_max16_32(mx) * lscale;
+  const bool moved = mx > m;
+  const bool any_moved = __builtin_amdgcn_ballot_w64(moved) != 0;
+  alpha = 1.0f;
+  if (any_moved) {
+    const float mn = fmaxf(m, mx);
+    alpha = safe_exp2_diff(m, mn);
+    m = mn;
+  }
+  float p[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(fmaf(x[i], lscale, -m));
+  ph[0] = pack_h2(p[0], p[1]);
+  ph[1] = pack_h2(p[2], p[3]);
+  return any_moved;
+}
+
 template <int D, int KNB, int VNB, int GS, int NW, int NSTAGE>
 struct LdsKernelSmem {
   using SG = StageGeom<D, KNB, VNB, GS>;
@@ -190,7 +300,7 @@ struct LdsKernelSmem {
   static constexpr int PATCH = (PATCH_META + 4 * SG::NG * 2 + 15) / 16 * 16;
 };
 
-template <int D, int KNB, int VNB, int GS, int NW, int NSTAGE, bool PAGED>
+template <int D, int KNB, int VNB, int GS, int NW, int NSTAGE, bool PAGED, bool PT>
 __global__ void __launch_bounds__(NW * 64)
 quant_split_lds_kernel(SplitParams prm) {
   using SG = StageGeom<D, KNB, VNB, GS>;
@@ -289,8 +399,13 @@ quant_split_lds_kernel(SplitParams prm) {
   }
 
 
+  // q operands: one per MFMA step of a tile, or (paired tiles, G <= 8) one
+  // block-diagonal operand per 16-dim block of both tiles.
+  using QP = QOperandsPT<D, KNB, GS>;
   QOperands<D, KNB, GS> qo;
-  load_q_operands<D, KNB, GS>(prm, b, h0, n, nh, j, qo);
+  QP qpt;
+  if constexpr (PT) load_q_operands_pt<D, KNB, GS>(prm, b, h0, r, nh, j, qpt);
+  else load_q_operands<D, KNB, GS>(prm, b, h0, n, nh, j, qo);
   const u4* qf = qo.qf;
   const u2 qzb = qo.qzb;
 
@@ -361,6 +476,12 @@ quant_split_lds_kernel(SplitParams prm) {
     const int ob = KL::load_offset(Lh, j);
     koff[Lh] = SG::K_OFF + SG::template pos_of<KL::DP>(r, ob >> 4) * 16 + (ob & 15);
   }
+  // Paired tiles: unit u of token 16 * (j >> 1) + r, bytes 8 * (j & 1) .. + 7.
+  uint32_t koffp[QP::NU];
+#pragma unroll
+  for (int u = 0; u < QP::NU; ++u)
+    koffp[u] = SG::K_OFF + SG::template pos_of<KL::DP>(16 * (j >> 1) + r, u) * 16 + 8 * (j & 1);
+  const int tile_pt = 16 * (r >> 3);  // paired tiles: the tile of this lane's scores
   // V operand of slot i, window wi: token slot_token(j, i), dword dword_offset(wi, r).
   uint32_t voff[VL::NWIN];
 #pragma unroll
@@ -444,76 +565,146 @@ quant_split_lds_kernel(SplitParams prm) {
     const uint8_t* mvs = mkz + SG::MB;
     const uint8_t* mvz = mvs + SG::MB;
 
-    // ---- scores S^T for the two 16-token tiles ---------------------------
-    float x[8];
-#pragma unroll
-    for (int a = 0; a < 2; ++a) {
-      f4 c[NG];
-#pragma unroll
-      for (int g = 0; g < NG; ++g) c[g] = f4{0.f, 0.f, 0.f, 0.f};
-      typename std::conditional<KL::CB == 8, u2, uint32_t>::type kx[KL::NLOAD];
-#pragma unroll
-      for (int Lh = 0; Lh < KL::NLOAD; ++Lh) {
-        // tile a = rows 16a.. = block a: 16 * NU entries further
-        constexpr int kTile = 16 * (KL::DP / 16) * 16;
-        if constexpr (KL::CB == 8) kx[Lh] = *reinterpret_cast<const u2*>(st + koff[Lh] + kTile * a);
-        else kx[Lh] = *reinterpret_cast<const uint32_t*>(st + koff[Lh] + kTile * a);
-      }
-#pragma unroll
-      for (int m = 0; m < NKM; ++m) {
-        const int g = KL::group_of_step(m);
-        if constexpr (KL::CB == 8)
-          c[g] = mfma_k32(k_extract8(kx[KL::load_of_step(m)], kmask[m]), qf[m], c[g]);
-        else
-          c[g] = mfma_k16(k_extract4(kx[KL::load_of_step(m)], kmask[m]), u2{qf[m][0], qf[m][1]}, c[g]);
-      }
-      // zero-point part: A row = token 16a + r, k-slots = its NG zero points
-      u2 za;
+    u4 pb;  // P^T in the PV MFMA's B layout: lane (j, c) holds tokens slot_token(j, .) of head c
+    if constexpr (PT) {
+      // ---- scores: both tiles in one set of MFMAs (paired tiles) ----------
+      float x[4];  // tokens 16 * tile + 4j + i of head c & 7, tile = c >> 3
       {
-        const uint8_t* zr = mkz + (16 * a + r) * SG::MROW * 2;
-        if constexpr (NG == 8) {
-          const u4 z8 = *reinterpret_cast<const u4*>(zr);
-          za = (j & 1) ? u2{z8[2], z8[3]} : u2{z8[0], z8[1]};
-        } else if constexpr (NG == 4) {
-          za = *reinterpret_cast<const u2*>(zr);
-        } else if constexpr (NG == 2) {
-          const uint32_t z2 = *reinterpret_cast<const uint32_t*>(zr);
-          za = u2{z2, z2};
-        } else {
-          const uint32_t z1 = *reinterpret_cast<const uint16_t*>(zr);
-          za = u2{z1 | (z1 << 16), 0u};
+        f4 c[NG];
+#pragma unroll
+        for (int g = 0; g < NG; ++g) c[g] = f4{0.f, 0.f, 0.f, 0.f};
+        u2 kx[QP::NU];
+#pragma unroll
+        for (int u = 0; u < QP::NU; ++u) kx[u] = *reinterpret_cast<const u2*>(st + koffp[u]);
+#pragma unroll
+        for (int p = 0; p < QP::P; ++p)
+#pragma unroll
+          for (int u = 0; u < QP::NU; ++u) {
+            const int g = (p * QP::DP + 16 * u) / GS;
+            c[g] = mfma_k32(k_extract8(kx[u], slice_mask<KNB>(p)), qpt.qb[p * QP::NU + u], c[g]);
+          }
+        // zero-point part: A row = token 16 * (j >> 1) + r, k-slots 8j + g = its zero points
+        u4 za;
+        {
+          const uint8_t* zrow = mkz + (16 * (j >> 1) + r) * SG::MROW * 2;
+          if constexpr (NG == 8) {
+            za = *reinterpret_cast<const u4*>(zrow);
+          } else if constexpr (NG == 4) {
+            const u2 z4 = *reinterpret_cast<const u2*>(zrow);
+            za = u4{z4[0], z4[1], 0u, 0u};
+          } else if constexpr (NG == 2) {
+            za = u4{*reinterpret_cast<const uint32_t*>(zrow), 0u, 0u, 0u};
+          } else {
+            za = u4{(uint32_t)*reinterpret_cast<const uint16_t*>(zrow), 0u, 0u, 0u};
+          }
+          // A row r mixes both tiles' token r, and 0 * NaN is NaN: zero points of
+          // rows past the sequence (whatever the cache holds there) are cleared
+          // so they cannot reach the other tile's columns.
+          if constexpr (TAIL)
+            if (cb + 16 * (j >> 1) + r > last) za = u4{0u, 0u, 0u, 0u};
+        }
+        const f4 yz = mfma_k32(za, qpt.qzb, f4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int t = tile_pt + 4 * j + i;
+          float sc = yz[i] * kTwoM24;
+#pragma unroll
+          for (int g = 0; g < NG; ++g) {
+            const float sv =
+                (float)__builtin_bit_cast(_Float16, (uint16_t)half_at(mks, t * SG::MROW + g));
+            sc = fmaf(sv, c[g][i], sc);
+          }
+          x[i] = sc;
         }
       }
-      const f4 yz = mfma_k16(za, qzb, f4{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = 16 * a + 4 * j + i;
-        float sc = yz[i] * kTwoM24;
-#pragma unroll
-        for (int g = 0; g < NG; ++g) {
-          const float sv = (float)__builtin_bit_cast(_Float16, (uint16_t)half_at(mks, t * SG::MROW + g));
-          sc = fmaf(sv, c[g][i], sc);
-        }
-        x[4 * a + i] = sc;
-      }
-    }
-    if constexpr (TAIL) {
-#pragma unroll
-      for (int a = 0; a < 2; ++a)
+      if constexpr (TAIL) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (cb + 16 * a + 4 * j + i > last) x[4 * a + i] = -INFINITY;
-    }
-
-    // ---- online softmax ---------------------------------------------------
-    float alpha;
-    ChunkProbs pr;
-    if (softmax_chunk<false>(x, lscale, m_run, l_run, alpha, pr)) {
+          if (cb + tile_pt + 4 * j + i > last) x[i] = -INFINITY;
+      }
+      // ---- online softmax ---------------------------------------------------
+      float alpha;
+      uint32_t ph[2];
+      if (softmax_chunk_pt(x, lscale, m_run, alpha, ph)) {
 #pragma unroll
-      for (int mv = 0; mv < NVM; ++mv) accv[mv] *= alpha;
-      oz *= alpha;
+        for (int mv = 0; mv < NVM; ++mv) accv[mv] *= alpha;
+        oz *= alpha;
+      }
+      // tile 0 of head c is this lane's (c < 8), tile 1 is lane c + 8's
+      pb = u4{ph[0], ph[1], (uint32_t)__shfl_xor((int)ph[0], 8, 64),
+              (uint32_t)__shfl_xor((int)ph[1], 8, 64)};
+    } else {
+      // ---- scores S^T for the two 16-token tiles ---------------------------
+      float x[8];
+  #pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        f4 c[NG];
+  #pragma unroll
+        for (int g = 0; g < NG; ++g) c[g] = f4{0.f, 0.f, 0.f, 0.f};
+        typename std::conditional<KL::CB == 8, u2, uint32_t>::type kx[KL::NLOAD];
+  #pragma unroll
+        for (int Lh = 0; Lh < KL::NLOAD; ++Lh) {
+          // tile a = rows 16a.. = block a: 16 * NU entries further
+          constexpr int kTile = 16 * (KL::DP / 16) * 16;
+          if constexpr (KL::CB == 8) kx[Lh] = *reinterpret_cast<const u2*>(st + koff[Lh] + kTile * a);
+          else kx[Lh] = *reinterpret_cast<const uint32_t*>(st + koff[Lh] + kTile * a);
+        }
+  #pragma unroll
+        for (int m = 0; m < NKM; ++m) {
+          const int g = KL::group_of_step(m);
+          if constexpr (KL::CB == 8)
+            c[g] = mfma_k32(k_extract8(kx[KL::load_of_step(m)], kmask[m]), qf[m], c[g]);
+          else
+            c[g] = mfma_k16(k_extract4(kx[KL::load_of_step(m)], kmask[m]), u2{qf[m][0], qf[m][1]}, c[g]);
+        }
+        // zero-point part: A row = token 16a + r, k-slots = its NG zero points
+        u2 za;
+        {
+          const uint8_t* zr = mkz + (16 * a + r) * SG::MROW * 2;
+          if constexpr (NG == 8) {
+            const u4 z8 = *reinterpret_cast<const u4*>(zr);
+            za = (j & 1) ? u2{z8[2], z8[3]} : u2{z8[0], z8[1]};
+          } else if constexpr (NG == 4) {
+            za = *reinterpret_cast<const u2*>(zr);
+          } else if constexpr (NG == 2) {
+            const uint32_t z2 = *reinterpret_cast<const uint32_t*>(zr);
+            za = u2{z2, z2};
+          } else {
+            const uint32_t z1 = *reinterpret_cast<const uint16_t*>(zr);
+            za = u2{z1 | (z1 << 16), 0u};
+          }
+        }
+        const f4 yz = mfma_k16(za, qzb, f4{0.f, 0.f, 0.f, 0.f});
+  #pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int t = 16 * a + 4 * j + i;
+          float sc = yz[i] * kTwoM24;
+  #pragma unroll
+          for (int g = 0; g < NG; ++g) {
+            const float sv = (float)__builtin_bit_cast(_Float16, (uint16_t)half_at(mks, t * SG::MROW + g));
+            sc = fmaf(sv, c[g][i], sc);
+          }
+          x[4 * a + i] = sc;
+        }
+      }
+      if constexpr (TAIL) {
+  #pragma unroll
+        for (int a = 0; a < 2; ++a)
+  #pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (cb + 16 * a + 4 * j + i > last) x[4 * a + i] = -INFINITY;
+      }
+
+      // ---- online softmax ---------------------------------------------------
+      float alpha;
+      ChunkProbs pr;
+      if (softmax_chunk<false>(x, lscale, m_run, l_run, alpha, pr)) {
+  #pragma unroll
+        for (int mv = 0; mv < NVM; ++mv) accv[mv] *= alpha;
+        oz *= alpha;
+      }
+      pb = u4{pr.ph[0], pr.ph[1], pr.ph[2], pr.ph[3]};
     }
-    const u4 pb = u4{pr.ph[0], pr.ph[1], pr.ph[2], pr.ph[3]};
 
     // ---- V zero point: oz += Z^T P (A rows = groups, k = the lane's 8 tokens)
     {
@@ -635,16 +826,23 @@ quant_split_lds_kernel(SplitParams prm) {
 constexpr int kStages8 = 2;
 constexpr int kStages4 = 2;
 
-template <int D, int KNB, int VNB, int GS>
-void launch_quant(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
+template <int D, int KNB, int VNB, int GS, bool PT>
+void launch_quant_pt(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
   const bool paged = p.page_size > 0;
   if (waves == 8) {
-    if (paged) quant_split_lds_kernel<D, KNB, VNB, GS, 8, 2, true><<<grid, dim3(8 * 64), 0, st>>>(p);
-    else quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false><<<grid, dim3(8 * 64), 0, st>>>(p);
+    if (paged) quant_split_lds_kernel<D, KNB, VNB, GS, 8, 2, true, PT><<<grid, dim3(8 * 64), 0, st>>>(p);
+    else quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, PT><<<grid, dim3(8 * 64), 0, st>>>(p);
   } else {
-    if (paged) quant_split_lds_kernel<D, KNB, VNB, GS, 4, 2, true><<<grid, dim3(4 * 64), 0, st>>>(p);
-    else quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false><<<grid, dim3(4 * 64), 0, st>>>(p);
+    if (paged) quant_split_lds_kernel<D, KNB, VNB, GS, 4, 2, true, PT><<<grid, dim3(4 * 64), 0, st>>>(p);
+    else quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false, PT><<<grid, dim3(4 * 64), 0, st>>>(p);
   }
+}
+
+// Paired tiles whenever the GQA group has at most 8 query heads.
+template <int D, int KNB, int VNB, int GS>
+void launch_quant(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
+  if (p.G <= 8) launch_quant_pt<D, KNB, VNB, GS, true>(p, grid, waves, st);
+  else launch_quant_pt<D, KNB, VNB, GS, false>(p, grid, waves, st);
 }
 
 }  // namespace tkv
