@@ -202,7 +202,7 @@ def fused_call(q, kq, vq, num_splits=None, split_only=False, waves=None, fused_c
         _lib.check(fn(args, torch.cuda.current_stream().cuda_stream), "fused")
     call.keep = (out, acc, mx, sm, cnt, q, kq, vq)
     call.num_splits = ns
-    pt = "true" if HQ // HKV <= 8 else "false"
+    pt = "true" if HQ // HKV <= 8 and size >= 8192 else "false"
     call.kernel = (f"quant_split_lds_kernel<{D}, {kq.nbits}, {vq.nbits}, {kq.group_size}, {wv}, 2, false, {pt}>")
     return call
 

@@ -214,32 +214,42 @@ __device__ __forceinline__ void load_q_operands_pt(const SplitParams& prm, int b
   float qz[NG];
 #pragma unroll
   for (int g = 0; g < NG; ++g) qz[g] = 0.0f;
+  // All loads first, in one branch, so they are in flight together.
+  float qv[QO::NB][8];
+  if (prm.q_fp32) {
+    const float* qp = static_cast<const float*>(prm.q) + qrow + 8 * (j & 1);
+#pragma unroll
+    for (int bi = 0; bi < QO::NB; ++bi) {
+      const int d0 = (bi / QO::NU) * QO::DP + 16 * (bi % QO::NU);
+      const f4 a = *reinterpret_cast<const f4*>(qp + d0);
+      const f4 c = *reinterpret_cast<const f4*>(qp + d0 + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        qv[bi][e] = (float)(_Float16)a[e];
+        qv[bi][4 + e] = (float)(_Float16)c[e];
+      }
+    }
+  } else {
+    const _Float16* qp = static_cast<const _Float16*>(prm.q) + qrow + 8 * (j & 1);
+#pragma unroll
+    for (int bi = 0; bi < QO::NB; ++bi) {
+      const int d0 = (bi / QO::NU) * QO::DP + 16 * (bi % QO::NU);
+      const h8 v = *reinterpret_cast<const h8*>(qp + d0);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qv[bi][e] = (float)v[e];
+    }
+  }
 #pragma unroll
   for (int p = 0; p < QO::P; ++p)
 #pragma unroll
     for (int u = 0; u < QO::NU; ++u) {
-      const int d0 = p * QO::DP + 16 * u + 8 * (j & 1);
-      float qv[8];
-      if (prm.q_fp32) {
-        const float* qp = static_cast<const float*>(prm.q) + qrow + d0;
-        const f4 a = *reinterpret_cast<const f4*>(qp), c = *reinterpret_cast<const f4*>(qp + 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          qv[e] = (float)(_Float16)a[e];
-          qv[4 + e] = (float)(_Float16)c[e];
-        }
-      } else {
-        const h8 v = *reinterpret_cast<const h8*>(static_cast<const _Float16*>(prm.q) + qrow + d0);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qv[e] = (float)v[e];
-      }
       const int g = (p * QO::DP + 16 * u) / GS;
       const float pre = __builtin_ldexpf(1.0f, -p * KNB);
       uint32_t wv[4];
 #pragma unroll
       for (int s2 = 0; s2 < 8; s2 += 2) {
-        const float q0 = hv ? qv[slot_byte(s2)] : 0.0f;
-        const float q1 = hv ? qv[slot_byte(s2 + 1)] : 0.0f;
+        const float q0 = hv ? qv[p * QO::NU + u][slot_byte(s2)] : 0.0f;
+        const float q1 = hv ? qv[p * QO::NU + u][slot_byte(s2 + 1)] : 0.0f;
         qz[g] += q0 + q1;
         wv[s2 / 2] = own ? pack_h2(q0 * pre, q1 * pre) : 0u;
       }
@@ -838,10 +848,17 @@ void launch_quant_pt(const SplitParams& p, dim3 grid, int waves, hipStream_t st)
   }
 }
 
-// Paired tiles whenever the GQA group has at most 8 query heads.
+// Paired tiles when the GQA group has at most 8 query heads and every
+// workgroup streams a long history.  They cost about 1 us more per workgroup
+// (twice the q operands to build, three more cross-lane moves per chunk), so
+// they pay only over many chunks per wave: measured 4-6% faster at 32768 tokens
+// per workgroup (2-bit, K4/V2), equal at 4096, 5-10% slower at 512-1024.
+constexpr int kPairedTilesMinSplit = 8192;
+
 template <int D, int KNB, int VNB, int GS>
 void launch_quant(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
-  if (p.G <= 8) launch_quant_pt<D, KNB, VNB, GS, true>(p, grid, waves, st);
+  if (p.G <= 8 && p.split_size >= kPairedTilesMinSplit)
+    launch_quant_pt<D, KNB, VNB, GS, true>(p, grid, waves, st);
   else launch_quant_pt<D, KNB, VNB, GS, false>(p, grid, waves, st);
 }
 
