@@ -283,6 +283,7 @@ def fused_decode_attention(
         raise ValueError(f"head_dim {D} must be a multiple of group_size {kq.group_size}")
     if fold_zp and kq.group_size < 16:
         raise ValueError(f"fold_zp needs group_size >= 16, got {kq.group_size}")
+    kn, vn, new_f32 = new_token_args(k_new, v_new, B, HKV, D, q.device)
 
     ok, why = triton_available()
     if not ok:
@@ -300,7 +301,6 @@ def fused_decode_attention(
     out = _check_out(out, B, HQ, D, q.device)
     acc, maxs, sums, counters = _workspace_for(_workspace, B, HQ, num_splits, D, q.device, HKV)
     lens = _seq_lens_arg(seq_lens, B, S, q.device)
-    kn, vn, new_f32 = new_token_args(k_new, v_new, B, HKV, D, q.device)
 
     args = _lib.DecodeArgs(
         q=q.data_ptr(), q_is_fp32=int(q.dtype == torch.float32),

@@ -30,7 +30,7 @@ import torch
 
 from . import _lib
 from .kernels.fused_decode_attn import (_aligned16, _check_out, _workspace_for, choose_waves,
-                                        new_token_args, plan_splits)
+                                        new_token_args, plan_splits, triton_available)
 from .quantize import QuantizedTensor, _check_bits, _require_gpu, empty_cache
 
 PAGE_MULTIPLE = 32
@@ -155,6 +155,10 @@ def paged_decode_attention(
         raise ValueError("seq_lens must be an int32 tensor of B lengths on the pool's device")
     if q.device != k_pool.device:
         raise ValueError("q and the pools must be on the same device")
+    kn, vn, new_f32 = new_token_args(k_new, v_new, B, HKV, D, q.device)
+    ok, why = triton_available()
+    if not ok:
+        raise RuntimeError(f"paged_decode_attention requires the tritonkv_amd HIP backend: {why}")
 
     group = HQ // HKV
     sm_scale = 1.0 / math.sqrt(D) if sm_scale is None else sm_scale
@@ -165,7 +169,6 @@ def paged_decode_attention(
     out = _check_out(out, B, HQ, D, q.device)
     acc, maxs, sums, _ = _workspace_for(_workspace, B, HQ, num_splits, D, q.device, HKV)
     lens = seq_lens.contiguous() if seq_lens is not None else None
-    kn, vn, new_f32 = new_token_args(k_new, v_new, B, HKV, D, q.device)
     args = _lib.DecodeArgs(
         q=q.data_ptr(), q_is_fp32=int(q.dtype == torch.float32),
         k=k_pool.packed.data_ptr(), k_scale=k_pool.scale.data_ptr(),
