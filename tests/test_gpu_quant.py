@@ -66,6 +66,91 @@ def test_gpu_quantize_matches_oracle_bitwise(D, nbits, gs, dtype):
     assert np.array_equal(_bits16(qt.zero), ref.zero.view(np.uint16))
 
 
+@pytest.mark.parametrize("nbits,gs,D,dtype", [(4, 32, 128, torch.float16),
+                                              (2, 16, 64, torch.float32)])
+def test_gpu_bulk_quantize_matches_oracle_bitwise(nbits, gs, D, dtype):
+    """>= 65536 rows take the several-rows-per-wave launch; 65604 rows is not a
+    multiple of its 32 rows per workgroup, so the last wave has a partial batch."""
+    from tritonkv_amd.quantize import quantize_groupwise
+
+    print(f"bulk quantize D={D} nbits={nbits} gs={gs} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(nbits + D)
+    k = (torch.randn(2, 2, 16401, D, generator=g) * 3).to(dtype)
+    k[0, 1, 7, :gs] = 1.5  # a constant group
+    qt = quantize_groupwise(k.to(DEV), nbits, gs)
+    ref = oq.quantize_groupwise(k.numpy(), nbits, gs)
+    assert np.array_equal(qt.packed.cpu().numpy(), ref.packed)
+    assert np.array_equal(_bits16(qt.scale), ref.scale.view(np.uint16))
+    assert np.array_equal(_bits16(qt.zero), ref.zero.view(np.uint16))
+
+
+@pytest.mark.parametrize("nbits,gs,D", [(4, 32, 128), (2, 16, 128), (4, 64, 64), (2, 128, 128)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_gpu_quantize_unaligned_input_takes_the_row_kernel(nbits, gs, D, dtype):
+    """Input not 16-byte aligned: quantized one wave per row (lane j owns byte
+    j), the same code the fused decode-step append runs; bit-exact too."""
+    from tritonkv_amd.quantize import quantize_groupwise
+
+    g = torch.Generator().manual_seed(nbits * gs + D)
+    n = 3 * 2 * 77 * D
+    buf = torch.empty(n + 1, dtype=dtype, device=DEV)
+    x = buf[1:].view(3, 2, 77, D)  # one element past a 256-byte boundary
+    x.copy_((torch.randn(3, 2, 77, D, generator=g) * 2).to(dtype))
+    assert x.data_ptr() % 16
+    qt = quantize_groupwise(x, nbits, gs)
+    ref = oq.quantize_groupwise(x.cpu().numpy(), nbits, gs)
+    assert np.array_equal(qt.packed.cpu().numpy(), ref.packed)
+    assert np.array_equal(_bits16(qt.scale), ref.scale.view(np.uint16))
+    assert np.array_equal(_bits16(qt.zero), ref.zero.view(np.uint16))
+    xb = _boundary_rows(300, 128, nbits, 32, seed=5).to(torch.float32)
+    buf = torch.empty(xb.numel() + 1, dtype=torch.float32, device=DEV)
+    xu = buf[1:].view(xb.shape)
+    xu.copy_(xb)
+    qt = quantize_groupwise(xu, nbits, 32)
+    ref = oq.quantize_groupwise(xb.numpy(), nbits, 32)
+    assert np.array_equal(qt.packed.cpu().numpy(), ref.packed)
+
+
+def _boundary_rows(rows, D, nbits, gs, seed):
+    """fp32 rows whose values sit on, and one or two ulps either side of, the
+    half-integer code boundaries (x - zero) / scale = k + 1/2 of their group."""
+    rng = np.random.default_rng(seed)
+    qmax = 2 ** nbits - 1
+    x = np.empty((rows, D // gs, gs), np.float32)
+    mn = rng.standard_normal((rows, D // gs)).astype(np.float16).astype(np.float32)
+    rngw = rng.choice(np.array([1e-3, 0.37, 1.0, 3.0, 250.0], np.float32), size=mn.shape)
+    mx = (mn + rngw).astype(np.float32)
+    sf = ((mx - mn) / np.float32(qmax)).astype(np.float16).astype(np.float32)
+    k = rng.integers(0, qmax, size=x.shape).astype(np.float32)
+    v = (mn[..., None] + ((k + np.float32(0.5)) * sf[..., None]).astype(np.float32)).astype(np.float32)
+    nudge = rng.integers(-2, 3, size=x.shape)
+    for _ in range(2):
+        v = np.where(nudge > 0, np.nextafter(v, np.float32(np.inf)), v)
+        v = np.where(nudge < 0, np.nextafter(v, np.float32(-np.inf)), v)
+        nudge = nudge - np.sign(nudge)
+    x[:] = np.clip(v, mn[..., None], mx[..., None])
+    x[..., 0], x[..., 1] = mn, mx
+    return torch.from_numpy(x.reshape(1, 1, rows, D))
+
+
+@pytest.mark.parametrize("rows", [300, 65600])
+@pytest.mark.parametrize("nbits,gs", [(4, 32), (2, 16), (4, 128)])
+def test_gpu_quantize_rounding_boundaries(rows, nbits, gs):
+    """Values on and next to the codes' rounding boundaries, where a quotient
+    taken as a product with the reciprocal could round the other way; both
+    launches (a few rows, and the several-rows-per-wave bulk one)."""
+    from tritonkv_amd.quantize import quantize_groupwise
+
+    D = 128
+    print(f"boundaries rows={rows} nbits={nbits} gs={gs}", flush=True)
+    x = _boundary_rows(rows, D, nbits, gs, seed=rows + nbits + gs)
+    qt = quantize_groupwise(x.to(DEV), nbits, gs)
+    ref = oq.quantize_groupwise(x.numpy(), nbits, gs)
+    assert np.array_equal(qt.packed.cpu().numpy(), ref.packed)
+    assert np.array_equal(_bits16(qt.scale), ref.scale.view(np.uint16))
+    assert np.array_equal(_bits16(qt.zero), ref.zero.view(np.uint16))
+
+
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("nbits", [2, 4])
 @pytest.mark.parametrize("gs", [16, 32, 64, 128])

@@ -32,7 +32,8 @@ struct PageMap {
 };
 
 // One wave per cache row (token x kv head), quantized by quantize_row: lane j
-// owns packed byte j of the row.
+// owns packed byte j of the row.  Used when the input or the codes are not
+// aligned for the wide kernel below.
 template <int D, int NB, int GS, bool F32>
 __global__ void __launch_bounds__(256)
 quantize_pack_kernel(const void* __restrict__ x, int64_t rows, int HKV, int N,
@@ -42,29 +43,175 @@ quantize_pack_kernel(const void* __restrict__ x, int64_t rows, int HKV, int N,
   using R = RowQuant<D, NB, GS>;
   constexpr int P = R::P, DP = R::DP, NG = R::NG;
 
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int64_t rr = (int64_t)blockIdx.x * 4 + w;
   if (rr >= rows) return;  // whole wave
+  float xv[P];
+  load_row_for_quant<D, NB>(static_cast<const uint8_t*>(x) + rr * D * (F32 ? 4 : 2), F32, lane, xv);
   const int64_t bh = rr / N;
-  const int t = (int)(rr % N);
-  const int b = (int)(bh / HKV);
+  const int t = (int)(rr - bh * N);
+  const int b = (int)(bh / HKV), kv = (int)(bh - (int64_t)b * HKV);
   const int64_t dst_t = (int64_t)(positions ? positions[b] : 0) + t;
   bool in_range = dst_t >= 0 && dst_t < S_cap;
   int64_t dst_row = bh * S_cap + dst_t;
   if (pm.page_size > 0 && in_range) {  // S_cap == stride * page_size
     const int e = pm.block_table[(int64_t)b * pm.stride + dst_t / pm.page_size];
     in_range = e >= 0 && e < pm.num_pages;  // rows mapped outside the pool are not written
-    dst_row = ((int64_t)e * HKV + bh % HKV) * pm.page_size + dst_t % pm.page_size;
+    dst_row = ((int64_t)e * HKV + kv) * pm.page_size + dst_t % pm.page_size;
   }
-
-  float xv[P];
-  load_row_for_quant<D, NB>(static_cast<const uint8_t*>(x) + rr * D * (F32 ? 4 : 2), F32, lane, xv);
   const R q = quantize_row<D, NB, GS>(xv, lane);
   if (!in_range) return;
   if (lane < DP) packed[dst_row * DP + lane] = (uint8_t)q.byte;
   if (lane < NG) {
     scale[dst_row * NG + lane] = (uint16_t)(q.meta & 0xFFFFu);
     zero[dst_row * NG + lane] = (uint16_t)(q.meta >> 16);
+  }
+}
+
+// Bulk form of the same quantization (the same arithmetic, so the same bits):
+// lane (slot r = l / LPR, column c = l % LPR) owns the E = 8 packed bytes
+// [8c, 8c + 8) of its row, i.e. the 8P codes of dims 8c + e + p*DP.  It reads
+// P runs of 8 consecutive values (16-byte loads) and writes its 8 bytes in one
+// store.  Group min/max fold the lane's own 8 values, then run over the GS/8
+// lanes of the group (or, when a group spans GS/DP slices, over the row's LPR
+// lanes) by DPP.  A wave covers 64/LPR rows per step; with BULK it takes
+// STEPS steps of rows, all their loads issued before any arithmetic.
+// Requires x 16-byte and packed 8-byte aligned, rows < 2^31.
+template <int D, int NB, int GS, bool F32, bool BULK>
+__global__ void __launch_bounds__(256)
+quantize_pack_wide_kernel(const void* __restrict__ x, int rows, int HKV, int N,
+                          const int32_t* __restrict__ positions, int S_cap, PageMap pm,
+                          uint8_t* __restrict__ packed, uint16_t* __restrict__ scale,
+                          uint16_t* __restrict__ zero) {
+  constexpr int P = 8 / NB, DP = D / P, NG = D / GS, QMAX = (1 << NB) - 1, E = 8;
+  constexpr int LPR = DP / E, RPS = 64 / LPR;
+  constexpr int NV = F32 ? 2 : 1;  // 16-byte loads per run of E values
+  constexpr int STEPS = BULK ? (8 / (P * NV) > 0 ? 8 / (P * NV) : 1) : 1;  // ~128 B per lane
+  static_assert(DP % E == 0 && LPR >= 2 && LPR <= 16, "row shape");
+  static_assert(GS > DP ? GS % DP == 0 : GS % E == 0, "group shape");
+
+  const int lane = threadIdx.x & 63, slot = lane / LPR, c = lane % LPR;
+  const int first = ((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6)) * STEPS * RPS;
+  u4 raw[STEPS][P][NV];
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    int rr = first + s * RPS + slot;
+    if (rr >= rows) rr = rows - 1;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int64_t off = (int64_t)rr * D + p * DP + c * E;  // elements
+#pragma unroll
+      for (int k = 0; k < NV; ++k)
+        raw[s][p][k] = F32 ? reinterpret_cast<const u4*>(static_cast<const float*>(x) + off)[k]
+                           : reinterpret_cast<const u4*>(static_cast<const _Float16*>(x) + off)[k];
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const int rr = first + s * RPS + slot;
+    float v[P][E], mn[P], mx[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      if constexpr (F32) {
+        // Whole-vector casts: this compiler folds fminf/fmaxf over floats cast
+        // one by one from the elements of an integer vector to the first one.
+        const f4 lo = __builtin_bit_cast(f4, raw[s][p][0]), hi = __builtin_bit_cast(f4, raw[s][p][1]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[p][e] = lo[e], v[p][e + 4] = hi[e];
+      } else {
+        const h8 h = __builtin_bit_cast(h8, raw[s][p][0]);
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[p][e] = (float)h[e];
+      }
+      mn[p] = mx[p] = v[p][0];
+#pragma unroll
+      for (int e = 1; e < E; ++e) {
+        mn[p] = fminf(mn[p], v[p][e]);
+        mx[p] = fmaxf(mx[p], v[p][e]);
+      }
+    }
+    if constexpr (GS <= DP) {
+#pragma unroll
+      for (int p = 0; p < P; ++p) minmax_lanes<GS / E>(mn[p], mx[p]);
+    } else {
+      constexpr int SPG = GS / DP;
+#pragma unroll
+      for (int p = 0; p < P; p += SPG) {
+#pragma unroll
+        for (int e = 1; e < SPG; ++e) {
+          mn[p] = fminf(mn[p], mn[p + e]);
+          mx[p] = fmaxf(mx[p], mx[p + e]);
+        }
+        minmax_lanes<LPR>(mn[p], mx[p]);
+#pragma unroll
+        for (int e = 1; e < SPG; ++e) {
+          mn[p + e] = mn[p];
+          mx[p + e] = mx[p];
+        }
+      }
+    }
+    float sf[P], zf[P], q[P][E];
+    uint16_t s16b[P], z16b[P];
+    bool unsure = false;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      float sc = (mx[p] - mn[p]) / (float)QMAX;
+      if (!(sc > 0.0f)) sc = 1.0f;
+      const _Float16 s16 = (_Float16)sc;
+      const _Float16 z16 = (_Float16)mn[p];
+      sf[p] = (float)s16;
+      zf[p] = (float)z16;
+      s16b[p] = __builtin_bit_cast(uint16_t, s16);
+      z16b[p] = __builtin_bit_cast(uint16_t, z16);
+      const float rs = __builtin_amdgcn_rcpf(sf[p]);
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const float y = (v[p][e] - zf[p]) * rs;
+        q[p][e] = rintf(y);
+        unsure |= quotient_unsure(y, q[p][e]);
+      }
+    }
+    if (__builtin_expect(unsure, 0)) {  // rare: redo the lane's codes by division
+#pragma unroll
+      for (int p = 0; p < P; ++p)
+#pragma unroll
+        for (int e = 0; e < E; ++e) q[p][e] = rintf((v[p][e] - zf[p]) / sf[p]);
+    }
+    uint32_t w[2] = {0, 0};
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        float c = q[p][e];
+        if (c != c) c = 0.0f;
+        c = fminf(fmaxf(c, 0.0f), (float)QMAX);
+        w[e / 4] |= (uint32_t)c << (8 * (e % 4) + p * NB);
+      }
+    if (rr >= rows) continue;  // after the cross-lane steps, which need every lane
+    const int bh = rr / N, t = rr - bh * N;
+    const int b = bh / HKV, kv = bh - b * HKV;
+    const int64_t dst_t = (int64_t)(positions ? positions[b] : 0) + t;
+    bool in_range = dst_t >= 0 && dst_t < S_cap;
+    int64_t dst_row = (int64_t)bh * S_cap + dst_t;
+    if (pm.page_size > 0 && in_range) {  // S_cap == stride * page_size
+      const int e = pm.block_table[(int64_t)b * pm.stride + dst_t / pm.page_size];
+      in_range = e >= 0 && e < pm.num_pages;  // rows mapped outside the pool are not written
+      dst_row = ((int64_t)e * HKV + kv) * pm.page_size + dst_t % pm.page_size;
+    }
+    if (!in_range) continue;
+    *reinterpret_cast<u2*>(packed + dst_row * DP + c * E) = u2{w[0], w[1]};
+    // Group g's scale and zero are written by the lane holding its first byte.
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      bool first_byte;
+      if constexpr (GS <= DP) first_byte = (c * E) % GS == 0;
+      else first_byte = c == 0 && p % (GS / DP) == 0;
+      if (first_byte) {
+        const int g = (p * DP + c * E) / GS;
+        scale[dst_row * NG + g] = s16b[p];
+        zero[dst_row * NG + g] = z16b[p];
+      }
+    }
   }
 }
 
@@ -189,11 +336,32 @@ template <int D, int NB, int GS>
 static void launch_quantize(const void* x, bool f32, int64_t rows, int HKV, int N,
                             const int32_t* pos, int S_cap, PageMap pm, uint8_t* pk, uint16_t* sc,
                             uint16_t* zr, hipStream_t st) {
-  const dim3 grid((unsigned)((rows + 3) / 4));
-  if (f32)
-    quantize_pack_kernel<D, NB, GS, true><<<grid, 256, 0, st>>>(x, rows, HKV, N, pos, S_cap, pm, pk, sc, zr);
-  else
-    quantize_pack_kernel<D, NB, GS, false><<<grid, 256, 0, st>>>(x, rows, HKV, N, pos, S_cap, pm, pk, sc, zr);
+  // The wide kernel needs 16-byte aligned input and 8-byte aligned codes;
+  // otherwise one wave per row.  Bulk quantization (a whole prompt or cache)
+  // takes several steps of rows per wave.
+  constexpr int RPS = 64 / (D * NB / 64);  // rows per wave and step: 64 / (DP / 8)
+  const bool wide = !((uintptr_t)x & 15) && !((uintptr_t)pk & 7) && rows <= INT32_MAX;
+  if (wide) {
+    const bool bulk = rows >= 65536;
+    const int steps = bulk ? ((8 / ((8 / NB) * (f32 ? 2 : 1))) > 0 ? 8 / ((8 / NB) * (f32 ? 2 : 1)) : 1) : 1;
+    const int per_wg = 4 * RPS * steps;
+    const dim3 grid((unsigned)((rows + per_wg - 1) / per_wg));
+    const int r = (int)rows;
+#define TKV_WIDE(F, BK) \
+  quantize_pack_wide_kernel<D, NB, GS, F, BK><<<grid, 256, 0, st>>>(x, r, HKV, N, pos, S_cap, pm, pk, sc, zr)
+    if (f32) {
+      if (bulk) TKV_WIDE(true, true); else TKV_WIDE(true, false);
+    } else {
+      if (bulk) TKV_WIDE(false, true); else TKV_WIDE(false, false);
+    }
+#undef TKV_WIDE
+  } else {
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    if (f32)
+      quantize_pack_kernel<D, NB, GS, true><<<grid, 256, 0, st>>>(x, rows, HKV, N, pos, S_cap, pm, pk, sc, zr);
+    else
+      quantize_pack_kernel<D, NB, GS, false><<<grid, 256, 0, st>>>(x, rows, HKV, N, pos, S_cap, pm, pk, sc, zr);
+  }
 }
 
 template <int D, int NB, int GS>

@@ -14,6 +14,12 @@
 // fp16 zero) gives code 0, as torch's clamp of NaN does.  The file that uses
 // this must not be compiled with fast-math.
 //
+// The group min/max reductions run on the VALU (DPP row permutations and the
+// gfx950 permlane swaps), not through LDS.  The code's division is taken as a
+// product with the reciprocal; the IEEE quotient is computed only for the
+// rare value whose product lies too close to a rounding boundary for the two
+// to be told apart (bound below), so the codes are those of the division.
+//
 // Shared by the append kernel and the decode kernel's fused append, so the two
 // write the same bits.
 #pragma once
@@ -32,6 +38,77 @@ struct RowQuant {
   uint32_t meta;  // lanes g < NG: group g's fp16 scale (bits 0..15) and zero (16..31)
 };
 
+// One butterfly step of a min/max reduction: combine with the value DPP
+// control CTRL brings from another lane of the same row of 16 lanes.
+template <int CTRL>
+__device__ __forceinline__ void minmax_dpp(float& mn, float& mx) {
+  const float a = __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, mn), CTRL, 0xF, 0xF, false));
+  const float b = __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, mx), CTRL, 0xF, 0xF, false));
+  mn = fminf(mn, a);
+  mx = fmaxf(mx, b);
+}
+
+// The value unchanged, but opaque to the optimizer (no instruction).
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// Combine min/max across the lane pairs a permlane swap exchanges (rows 2k and
+// 2k+1 for SWAP32 = false, the two 32-lane halves for true).  Given the same
+// value v twice, the swap returns v with each odd part replaced by its even
+// partner in one output and each even part by its odd partner in the other,
+// so the min (max) of the two outputs is the pair's in every lane.  The
+// outputs go through opaque(): this compiler folds fminf/fmaxf of the two
+// outputs of the swap builtin to its first output.
+template <bool SWAP32>
+__device__ __forceinline__ void minmax_swap(float& mn, float& mx) {
+  const uint32_t n = __builtin_bit_cast(uint32_t, mn), x = __builtin_bit_cast(uint32_t, mx);
+  const auto sn = SWAP32 ? __builtin_amdgcn_permlane32_swap(n, n, false, false)
+                         : __builtin_amdgcn_permlane16_swap(n, n, false, false);
+  const auto sx = SWAP32 ? __builtin_amdgcn_permlane32_swap(x, x, false, false)
+                         : __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  mn = fminf(__builtin_bit_cast(float, opaque(sn[0])), __builtin_bit_cast(float, opaque(sn[1])));
+  mx = fmaxf(__builtin_bit_cast(float, opaque(sx[0])), __builtin_bit_cast(float, opaque(sx[1])));
+}
+
+// Min and max over aligned runs of W lanes (W a power of two, 1..64); every
+// lane of a run ends with the run's min and max.  fminf/fmaxf select one of
+// their operands, so the result does not depend on the order of the steps.
+//   lane^1, lane^2: quad_perm; the other quad of 8 lanes: row_half_mirror
+//   (lane 7-i); the other half of a 16-lane row: row_mirror (lane 15-i);
+//   rows 2k and 2k+1: v_permlane16_swap; the two 32-lane halves:
+//   v_permlane32_swap.
+template <int W>
+__device__ __forceinline__ void minmax_lanes(float& mn, float& mx) {
+  if constexpr (W >= 2) minmax_dpp<0xB1>(mn, mx);   // quad_perm [1,0,3,2]
+  if constexpr (W >= 4) minmax_dpp<0x4E>(mn, mx);   // quad_perm [2,3,0,1]
+  if constexpr (W >= 8) minmax_dpp<0x141>(mn, mx);  // row_half_mirror
+  if constexpr (W >= 16) minmax_dpp<0x140>(mn, mx); // row_mirror
+  if constexpr (W >= 32) minmax_swap<false>(mn, mx);
+  if constexpr (W >= 64) minmax_swap<true>(mn, mx);
+}
+
+// Codes as rint(a / s) in IEEE binary32 with ties to even (s > 0 or s = +0),
+// computed as y = a * rcp(s), q = rint(y).  y differs from the rounded
+// quotient d = fl(a/s) by at most 2^-22 |a/s| (v_rcp_f32 is accurate to 1 ulp,
+// the product adds half an ulp, d half an ulp), i.e. by less than 2^-17 when
+// |y| < 32.  So rint(y) == rint(d) unless y lies within 2^-16 of a
+// half-integer, or |y| >= 32 (or y is inf or NaN); only then is the quotient
+// itself needed.  s = +0 gives the same inf or NaN both ways.
+__device__ __forceinline__ bool quotient_unsure(float y, float q) {
+  return !(fabsf(y - q) <= 0.5f - 0x1p-16f) || !(fabsf(y) < 32.0f);
+}
+
+__device__ __forceinline__ float rint_quotient(float a, float s, float rs) {
+  const float y = a * rs;
+  float q = rintf(y);
+  if (__builtin_expect(quotient_unsure(y, q), 0)) q = rintf(a / s);
+  return q;
+}
+
 // x[p] = the row's value at dim (lane % DP) + p * DP, already in fp32.
 template <int D, int NB, int GS>
 __device__ __forceinline__ RowQuant<D, NB, GS> quantize_row(const float (&x)[8 / NB], int lane) {
@@ -44,12 +121,7 @@ __device__ __forceinline__ RowQuant<D, NB, GS> quantize_row(const float (&x)[8 /
   if constexpr (GS <= DP) {
     // A group is GS consecutive bytes of one slice: aligned runs of GS lanes.
 #pragma unroll
-    for (int k = 1; k < GS; k <<= 1)
-#pragma unroll
-      for (int p = 0; p < P; ++p) {
-        mn[p] = fminf(mn[p], __shfl_xor(mn[p], k, 64));
-        mx[p] = fmaxf(mx[p], __shfl_xor(mx[p], k, 64));
-      }
+    for (int p = 0; p < P; ++p) minmax_lanes<GS>(mn[p], mx[p]);
   } else {
     // A group is GS/DP whole slices: fold them in the lane, then all DP bytes.
     constexpr int SPG = GS / DP;
@@ -60,11 +132,7 @@ __device__ __forceinline__ RowQuant<D, NB, GS> quantize_row(const float (&x)[8 /
         mn[p] = fminf(mn[p], mn[p + e]);
         mx[p] = fmaxf(mx[p], mx[p + e]);
       }
-#pragma unroll
-      for (int k = 1; k < DP; k <<= 1) {
-        mn[p] = fminf(mn[p], __shfl_xor(mn[p], k, 64));
-        mx[p] = fmaxf(mx[p], __shfl_xor(mx[p], k, 64));
-      }
+      minmax_lanes<DP>(mn[p], mx[p]);
 #pragma unroll
       for (int e = 1; e < SPG; ++e) {
         mn[p + e] = mn[p];
@@ -80,7 +148,7 @@ __device__ __forceinline__ RowQuant<D, NB, GS> quantize_row(const float (&x)[8 /
     const _Float16 s16 = (_Float16)sc;
     const _Float16 z16 = (_Float16)mn[p];
     const float sf = (float)s16, zf = (float)z16;
-    float c = rintf((x[p] - zf) / sf);
+    float c = rint_quotient(x[p] - zf, sf, __builtin_amdgcn_rcpf(sf));
     if (c != c) c = 0.0f;
     c = fminf(fmaxf(c, 0.0f), (float)QMAX);
     byte |= (uint32_t)c << (p * NB);
