@@ -121,6 +121,11 @@ def test_c_entry_points_reject_bad_arguments_without_a_gpu():
     assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
     a.waves, a.D = 8, 96
     assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EUNSUPPORTED
+    # Splits are the grid's y axis: at most 65535.
+    a.D, a.S, a.split_size, a.num_splits = 128, 65536 * 32, 32, 65536
+    assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    assert lib.tkv_fp16_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    a.D, a.S, a.split_size, a.num_splits = 96, 64, 64, 1
     # Paged caches: page size a multiple of 32, a block table covering S exactly.
     a.D, a.page_size, a.num_pages, a.block_table_stride = 128, 16, 8, 4
     assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
@@ -231,6 +236,13 @@ def test_plan_splits_honours_explicit_num_splits_like_the_reference(S, block_n, 
     assert plan_splits(S, block_n, ns, 1, 2, 6) == osp.split_plan(S, block_n, ns)
 
 
+def test_plan_splits_caps_the_split_count_at_the_grid_limit():
+    from tritonkv_amd.kernels import plan_splits
+
+    _, ns, split = plan_splits(1 << 21, 16, 100000, 1, 8, 4)
+    assert ns <= 65535 and ns * split >= 1 << 21 and (ns - 1) * split < 1 << 21
+
+
 def test_pick_num_splits_formula():
     from tritonkv_amd.kernels import pick_num_splits
 
@@ -244,8 +256,21 @@ def test_pick_num_splits_formula():
 def test_default_split_plan_covers_history_without_empty_splits(B, HKV, G, S):
     from tritonkv_amd.kernels import plan_splits
 
-    _, ns, size = plan_splits(S, 64, None, B, HKV, G)
-    assert ns >= 1 and size * ns >= S and size * (ns - 1) < S
+    for ragged in (False, True):
+        _, ns, size = plan_splits(S, 64, None, B, HKV, G, ragged=ragged)
+        assert ns >= 1 and size * ns >= S and size * (ns - 1) < S
+
+
+def test_ragged_batches_of_a_unit_per_cu_split_long_histories_in_two(monkeypatch):
+    from tritonkv_amd.kernels import fused_decode_attn as fda
+
+    monkeypatch.setattr(fda, "compute_units", lambda: 256)
+    assert fda.plan_splits(131072, 64, None, 64, 8, 8)[1] == 1
+    assert fda.plan_splits(131072, 64, None, 64, 8, 8, ragged=True)[1] == 2
+    assert fda.plan_splits(8192, 64, None, 64, 8, 8, ragged=True)[1] == 1  # short: unsplit
+    # below one unit per CU the ordinary policy applies either way
+    assert fda.plan_splits(32768, 64, None, 4, 8, 4, ragged=True) == \
+        fda.plan_splits(32768, 64, None, 4, 8, 4)
 
 
 def test_timing_stats_match_reference_definition():

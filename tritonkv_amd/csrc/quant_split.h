@@ -331,8 +331,8 @@ quant_split_lds_kernel(SplitParams prm) {
 
   __shared__ __attribute__((aligned(16))) uint8_t smem[NW * SM::WAVE + SM::PATCH];
 
-  const int split = blockIdx.x;
-  const int unit = blockIdx.y;
+  const int unit = blockIdx.x;   // fastest: consecutive workgroups (which the
+  const int split = blockIdx.y;  // dispatcher deals to the 8 XCDs in turn) take other units
   const int b = unit / prm.HKV, hk = unit % prm.HKV;
   const int hb0 = blockIdx.z * 16;
   const int nh = min(16, prm.G - hb0);

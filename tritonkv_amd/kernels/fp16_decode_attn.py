@@ -60,7 +60,8 @@ def fp16_decode_attention(
     group = HQ // HKV
     sm_scale = 1.0 / math.sqrt(D) if sm_scale is None else sm_scale
     _, num_splits, split_size = plan_splits(S, block_n, num_splits, B, HKV, group,
-                                            TOKENS_PER_WORKGROUP_FP16)
+                                            TOKENS_PER_WORKGROUP_FP16,
+                                            ragged=seq_lens is not None)
 
     if q.dtype not in (torch.float16, torch.float32):
         q = q.float()

@@ -162,7 +162,8 @@ def paged_decode_attention(
 
     group = HQ // HKV
     sm_scale = 1.0 / math.sqrt(D) if sm_scale is None else sm_scale
-    _, num_splits, split_size = plan_splits(S, block_n, num_splits, B, HKV, group)
+    _, num_splits, split_size = plan_splits(S, block_n, num_splits, B, HKV, group,
+                                            ragged=seq_lens is not None)
     if q.dtype not in (torch.float16, torch.float32):
         q = q.float()
     q = _aligned16(q)
