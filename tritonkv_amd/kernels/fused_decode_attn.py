@@ -47,8 +47,6 @@ from ..quantize import QuantizedTensor
 
 LOG2E = 1.4426950408889634
 
-# Fewest tokens one workgroup should stream: 4 waves x 32-token chunks.
-_MIN_SPLIT_TOKENS = 128
 
 
 def triton_available() -> tuple[bool, str]:
@@ -116,15 +114,20 @@ def default_num_splits(B: int, HKV: int, G: int, S: int, block_n: int,
 
     * a batch that already offers one (b, kv head, 16-head block) unit per
       compute unit or more runs unsplit -- no partials, no combine launch --
-      and so does a history of at most 1024 tokens, where one workgroup per
-      unit beats any split-plus-combine on latency;
+      and so does a history of at most ``tokens_per_workgroup`` tokens (512
+      for the fused kernel, 256 for the fp16 control, whose tokens are 3-6x
+      larger);
     * otherwise the history is cut so that each workgroup streams about
-      ``tokens_per_workgroup`` tokens (512 for the fused kernel, 256 for the
-      fp16 control, whose tokens are 3-6x larger), with at least 32 and at
-      most one workgroup per compute unit in total.  Fewer, longer workgroups
-      win at small caches (the Qwen2.5-1.5B shape, fused: 64 workgroups at
-      ctx 16384); one per CU wins as soon as the cache is tens of MB (e.g. 3x
-      over a fixed 64 at B=16, ctx 32768).
+      ``tokens_per_workgroup`` tokens, with at least 32 and at most one
+      workgroup per compute unit in total, and no split shorter than a
+      quarter of that (128 / 64 tokens).  Fewer, longer workgroups win at
+      small caches (the Qwen2.5-1.5B shape, fused: 64 workgroups at ctx
+      16384); one per CU wins as soon as the cache is tens of MB (e.g. 3x
+      over a fixed 64 at B=16, ctx 32768).  Even a short history gains from
+      the split: a workgroup's 8 waves take about 1 us of compute per two
+      chunks each, more than the combine launch costs (Qwen2.5-1.5B shape,
+      ctx 1024: 7.3 us at 8 splits vs 9.6 unsplit; fp16 control at ctx 512:
+      6.6 us at 8 splits vs 7.9 unsplit).
 
     With per-row lengths (``ragged``: the call passes ``seq_lens``, which the
     host cannot read without a sync), a batch of at least one unit per compute
@@ -138,13 +141,13 @@ def default_num_splits(B: int, HKV: int, G: int, S: int, block_n: int,
     """
     cu = compute_units() or 256
     units = B * HKV * _cdiv(G, 16)
-    if S <= 1024:
+    if S <= tokens_per_workgroup:
         return 1
     if units >= cu:
         return min(2, _cdiv(S, block_n)) if ragged and S >= 16384 else 1
     workgroups = min(cu, max(32, units * S // tokens_per_workgroup))
     want = max(1, workgroups // units)
-    max_splits = max(1, S // max(_MIN_SPLIT_TOKENS, block_n))
+    max_splits = max(1, S // max(tokens_per_workgroup // 4, block_n))
     return max(1, min(want, max_splits, _cdiv(S, block_n)))
 
 
