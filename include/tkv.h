@@ -90,6 +90,22 @@ typedef struct tkv_decode_args {
    * GPU append). */
   const void *k_new, *v_new;
   int32_t new_is_fp32;
+  /* Per-channel keys (quantized path only): key_block == 32 makes k_scale /
+   * k_zero (B, HKV, S/32, D) -- one fp16 scale and zero per (32-token block,
+   * channel), as tkv_quantize_keys_channel writes them -- instead of per-token
+   * groups; V keeps its per-token groups, whose group_size must then be 16 or
+   * 32.  Contiguous caches only, no fused append, S a multiple of 32.
+   * key_block == 0: per-token key groups.  The reference plans this format
+   * (docs/future_work.md:229-293) and has no implementation of it. */
+  int32_t key_block;
+  /* Partials placement: this launch's num_splits splits are partial rows
+   * split_base .. split_base + num_splits - 1 of num_splits_total per (b, head)
+   * (num_splits_total == 0 means num_splits), so that two launches -- e.g. a
+   * quantized history and an fp16 residual window -- fill one set of partials
+   * for one combine.  num_splits_total == 1 writes out directly.  The
+   * *_attention entry points need split_base == 0 and num_splits_total equal
+   * to num_splits (or 0); counters likewise. */
+  int32_t split_base, num_splits_total;
 } tkv_decode_args;
 
 /* Fused 2/4-bit split-P decode attention: the split kernel, then (if
@@ -143,6 +159,35 @@ int tkv_paged_quantize_pack(const void *x, int32_t x_is_fp32, int32_t B, int32_t
                             uint8_t *packed, uint16_t *scale, uint16_t *zero,
                             tkv_stream_t stream);
 
+/* Decode over per-channel quantized keys plus an fp16 residual window, the
+ * format the reference plans (docs/future_work.md:229-293: "the fp16 residual
+ * tail goes through the existing fp16 control kernel as one more split, and
+ * the existing combine kernel merges it").  args describes the quantized
+ * history: key_block == 32, seq_lens (or S) its per-row lengths, num_splits
+ * its splits; acc/maxs/sums must hold num_splits + 1 partial rows per
+ * (b, head); split_base / num_splits_total / counters are ignored.  k_res,
+ * v_res: fp16 (B, HKV, res_cap, D), the window; row b attends to its first
+ * res_lens[b] window tokens (0 <= res_lens[b] <= res_cap; NULL = res_cap)
+ * after its quantized ones.  Three launches: the quantized split kernel, the
+ * fp16 split kernel over the window (partial row num_splits), the combine. */
+int tkv_channel_decode_attention(const tkv_decode_args *args, const void *k_res,
+                                 const void *v_res, const int32_t *res_lens, int32_t res_cap,
+                                 tkv_stream_t stream);
+
+/* Per-channel (KIVI-style) key quantization: x (B, HKV, N, D) fp16/fp32 with
+ * N a multiple of 32 is cut into 32-token blocks; within a block every
+ * channel is one group (the group-wise arithmetic of quantize_groupwise,
+ * quantize.py:209-226, along the token axis).  Codes go to packed
+ * (B, HKV, S_cap, D/P) in the split-P row layout, fp16 scale and zero to
+ * (B, HKV, S_cap/32, D).  Row b's blocks land at tokens positions[b] + 32k
+ * (positions NULL = 0); a block that does not start on a 32-token boundary
+ * or does not fit [0, S_cap) is not written.  The reference plans this format
+ * (docs/future_work.md:229-293) and has no implementation of it. */
+int tkv_quantize_keys_channel(const void *x, int32_t x_is_fp32, int32_t B, int32_t HKV,
+                              int32_t N, int32_t D, int32_t nbits, const int32_t *positions,
+                              int32_t S_cap, uint8_t *packed, uint16_t *scale, uint16_t *zero,
+                              tkv_stream_t stream);
+
 /* Split-P pack of uint8 codes (rows, D) -> (rows, D/P), as pack_codes
  * (quantize.py:149-169). */
 int tkv_pack_codes(const uint8_t *codes, int64_t rows, int32_t D, int32_t nbits,
@@ -178,7 +223,8 @@ const char *tkv_status_string(int status);
 
 /* ABI version of this library (bumped on any incompatible change; 3 added the
  * paged-cache fields of tkv_decode_args and tkv_paged_quantize_pack, 4 the
- * fused-append fields). */
+ * fused-append fields, 5 the per-channel key and partials-placement fields,
+ * tkv_quantize_keys_channel and tkv_channel_decode_attention). */
 int tkv_abi_version(void);
 
 #ifdef __cplusplus

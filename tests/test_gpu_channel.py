@@ -1,0 +1,191 @@
+"""GPU parity of per-channel (KIVI-style) keys with an fp16 residual window.
+
+* The key quantizer (``tkv_quantize_keys_channel``) is bit-exact with the
+  oracle (``oracle/channel.py``), itself pinned through the golden-pinned
+  per-token quantizer on transposed blocks.
+* The decode step (per-channel key path of the split kernel, the fp16 control
+  over the window as one more split, the combine) is within the north-star
+  tolerance of the oracle's fp32 attention over the dequantized history
+  followed by the window, with ragged history and window lengths (including
+  empty ones) and NaN garbage past every length.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oatt
+from oracle import channel as och
+from oracle import quant as oq
+from tests.helpers import assert_close_to_reference, qt_to_np
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _bits16(t):
+    return t.detach().cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("nbits", [2, 4])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_channel_key_quantizer_matches_oracle_bitwise(D, nbits, dtype):
+    from tritonkv_amd.channel import quantize_keys_per_channel
+
+    print(f"channel quantize D={D} nbits={nbits} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(D + nbits)
+    k = (torch.randn(2, 3, 96, D, generator=g) * 2).to(dtype)
+    k[0, 1, 32:64, 5] = 0.75       # a constant group
+    k[1, 0, :, 9] *= 40            # an outlier channel
+    ck = quantize_keys_per_channel(k.to(DEV), nbits)
+    ref = och.quantize_keys_per_channel(k.numpy(), nbits)
+    assert np.array_equal(ck.packed.cpu().numpy(), ref.packed)
+    assert np.array_equal(_bits16(ck.scale), ref.scale.view(np.uint16))
+    assert np.array_equal(_bits16(ck.zero), ref.zero.view(np.uint16))
+
+
+def test_channel_key_append_positions():
+    """Blocks land at per-row positions; unaligned or out-of-range blocks are not written."""
+    from tritonkv_amd.channel import append_keys_per_channel, empty_channel_keys
+
+    B, H, D, S = 4, 2, 128, 128
+    g = torch.Generator().manual_seed(4)
+    k = torch.randn(B, H, 64, D, generator=g).half()
+    ck = empty_channel_keys(B, H, S, D, 4, DEV)
+    for t in (ck.packed, ck.scale, ck.zero):
+        t.view(torch.uint8).fill_(0xAB)
+    pos = torch.tensor([0, 32, 96, 16], dtype=torch.int32, device=DEV)
+    append_keys_per_channel(ck, k.to(DEV), pos)
+    ref = och.quantize_keys_per_channel(k.numpy(), 4)
+    packed, scale = ck.packed.cpu().numpy(), _bits16(ck.scale)
+    assert np.array_equal(packed[0, :, 0:64], ref.packed[0])
+    assert np.array_equal(scale[0, :, 0:2], ref.scale[0].view(np.uint16))
+    assert np.array_equal(packed[1, :, 32:96], ref.packed[1])
+    assert np.array_equal(packed[2, :, 96:128], ref.packed[2, :, :32])   # second block past S
+    assert (packed[2, :, :96] == 0xAB).all()
+    assert (packed[3] == 0xAB).all()                                     # position 16: unaligned
+
+
+def _window_case(B, HQ, HKV, D, S, kbits, vbits, gs, q_lens, r_lens, seed):
+    from tritonkv_amd.channel import quantize_keys_per_channel
+    from tritonkv_amd.quantize import quantize_groupwise
+
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, HQ, D, generator=g).half()
+    k = torch.randn(B, HKV, S, D, generator=g)
+    k[:, :, :, 3] *= 12                     # fixed outlier channels
+    k[:, :, :, 70 % D] *= 8
+    k = k.half()
+    v = torch.randn(B, HKV, S, D, generator=g).half()
+    kres = torch.randn(B, HKV, 32, D, generator=g).half()
+    vres = torch.randn(B, HKV, 32, D, generator=g).half()
+    ck = quantize_keys_per_channel(k.to(DEV), kbits)
+    vq = quantize_groupwise(v.to(DEV), vbits, gs)
+    ql = torch.tensor(q_lens, dtype=torch.int32)
+    rl = torch.tensor(r_lens, dtype=torch.int32)
+    return q, ck, vq, kres, vres, ql, rl
+
+
+def _oracle(q, ck, vq, kres, vres, ql, rl):
+    ckn = och.ChannelKeysNP(ck.packed.cpu().numpy(), ck.scale.cpu().numpy(), ck.zero.cpu().numpy(),
+                            ck.nbits, 32, ck.head_dim)
+    kh, vh, lens = och.history(ckn, qt_to_np(vq), kres.numpy(), vres.numpy(), ql.tolist(),
+                               rl.tolist())
+    HKV = kh.shape[1]
+    return oatt.reference_grouped(q.float().numpy(), lambda s, e: kh[:, :, s:e],
+                                  lambda s, e: vh[:, :, s:e], kh.shape[2], HKV, seq_lens=lens)
+
+
+CASES = [
+    # (kbits, vbits, gs, D, HQ, HKV)
+    (2, 2, 32, 128, 16, 4),
+    (4, 4, 32, 128, 12, 2),
+    (2, 4, 16, 128, 8, 2),
+    (4, 2, 32, 64, 32, 4),
+    (2, 2, 16, 64, 4, 1),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "K{}V{}-gs{}-D{}-G{}".format(
+    c[0], c[1], c[2], c[3], c[4] // c[5]))
+@pytest.mark.parametrize("ns", [None, 1, 3])
+def test_channel_decode_matches_oracle(case, ns):
+    from tritonkv_amd.channel import channel_decode_attention
+
+    kbits, vbits, gs, D, HQ, HKV = case
+    S = 640
+    q_lens, r_lens = [640, 0, 96, 320, 32], [31, 7, 0, 32, 1]
+    B = len(q_lens)
+    print(f"channel decode {case} ns={ns}", flush=True)
+    q, ck, vq, kres, vres, ql, rl = _window_case(B, HQ, HKV, D, S, kbits, vbits, gs, q_lens,
+                                                 r_lens, seed=kbits + 10 * vbits + gs + D)
+    got = channel_decode_attention(q.to(DEV), ck, vq, kres.to(DEV), vres.to(DEV),
+                                   q_lens=ql.to(DEV), res_lens=rl.to(DEV), num_splits=ns)
+    torch.cuda.synchronize()
+    assert torch.isfinite(got).all()
+    ref = _oracle(q, ck, vq, kres, vres, ql, rl)
+    assert_close_to_reference(got, ref, f"channel decode {case} ns={ns}")
+
+
+def test_channel_decode_ignores_garbage_past_the_lengths():
+    """NaN bit patterns past every row's history and window change nothing."""
+    from tritonkv_amd.channel import ChannelQuantizedKeys, channel_decode_attention
+    from tritonkv_amd.quantize import QuantizedTensor
+
+    B, HQ, HKV, D, S = 3, 8, 2, 128, 256
+    q_lens, r_lens = [96, 256, 0], [5, 0, 20]
+    q, ck, vq, kres, vres, ql, rl = _window_case(B, HQ, HKV, D, S, 4, 2, 32, q_lens, r_lens, 9)
+    args = dict(q_lens=ql.to(DEV), res_lens=rl.to(DEV), num_splits=2)
+    clean = channel_decode_attention(q.to(DEV), ck, vq, kres.to(DEV), vres.to(DEV), **args)
+    ck2 = ChannelQuantizedKeys(ck.packed.clone(), ck.scale.clone(), ck.zero.clone(), ck.nbits, D)
+    vq2 = QuantizedTensor(vq.packed.clone(), vq.scale.clone(), vq.zero.clone(), vq.nbits,
+                          vq.group_size, D)
+    kr2, vr2 = kres.clone().to(DEV), vres.clone().to(DEV)
+    for b in range(B):
+        a, r = q_lens[b], r_lens[b]
+        for t in (ck2.packed, vq2.packed, vq2.scale, vq2.zero):
+            t[b, :, a:].view(torch.uint8).fill_(0xFF)
+        for t in (ck2.scale, ck2.zero):
+            t[b, :, a // 32:].view(torch.uint8).fill_(0xFF)
+        for t in (kr2, vr2):
+            t[b, :, r:].view(torch.uint8).fill_(0xFF)
+    dirty = channel_decode_attention(q.to(DEV), ck2, vq2, kr2, vr2, **args)
+    torch.cuda.synchronize()
+    assert torch.equal(dirty, clean)
+
+
+def test_channel_kv_cache_prefill_and_decode_steps():
+    """The cache manager: prefill, then single-token steps across window flushes."""
+    from tritonkv_amd.channel import ChannelKVCache
+
+    B, HQ, HKV, D = 2, 8, 2, 128
+    g = torch.Generator().manual_seed(11)
+    n0, steps = 70, 40
+    k = torch.randn(B, HKV, n0 + steps, D, generator=g).half()
+    v = torch.randn(B, HKV, n0 + steps, D, generator=g).half()
+    q = torch.randn(B, HQ, D, generator=g).half()
+    cache = ChannelKVCache(B, HKV, 256, D, k_nbits=2, v_nbits=4, group_size=32, device=DEV)
+    cache.extend(k[:, :, :n0].to(DEV), v[:, :, :n0].to(DEV))
+    assert (cache.quantized, cache.window) == (64, 6)
+    checked = 0
+    for s in range(steps):
+        cache.extend(k[:, :, n0 + s:n0 + s + 1].to(DEV), v[:, :, n0 + s:n0 + s + 1].to(DEV))
+        n = n0 + s + 1
+        if s not in (0, 25, 26, 39):   # before, at and after the flush at 96 tokens
+            continue
+        got = cache.attend(q.to(DEV))
+        torch.cuda.synchronize()
+        nq = (n // 32) * 32
+        ckn = och.quantize_keys_per_channel(k[:, :, :nq].numpy(), 2) if nq else None
+        vqn = oq.quantize_groupwise(v[:, :, :nq].numpy(), 4, 32)
+        kd = och.dequantize_keys_per_channel(ckn) if nq else np.zeros((B, HKV, 0, D), np.float32)
+        vd = oq.dequantize_groupwise(vqn) if nq else np.zeros((B, HKV, 0, D), np.float32)
+        kh = np.concatenate([kd, k[:, :, nq:n].float().numpy()], axis=2)
+        vh = np.concatenate([vd, v[:, :, nq:n].float().numpy()], axis=2)
+        ref = oatt.reference_decode_attention(q.float().numpy(), kh, vh)
+        assert_close_to_reference(got, ref, f"cache step {s} (n={n})")
+        checked += 1
+    assert checked == 4 and len(cache) == n0 + steps

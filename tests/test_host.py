@@ -45,7 +45,7 @@ def test_library_exports_every_declared_symbol():
     for name in _declared_symbols():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.tkv_abi_version() == 4
+    assert lib.tkv_abi_version() == 5
 
 
 def test_library_is_gfx950_only():
@@ -69,13 +69,14 @@ def test_decode_args_layout_matches_c():
     #include <stddef.h>
     #include "tkv.h"
     int main(void) {
-      printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\n", sizeof(tkv_decode_args),
+      printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\n", sizeof(tkv_decode_args),
              offsetof(tkv_decode_args, q_is_fp32), offsetof(tkv_decode_args, seq_lens),
              offsetof(tkv_decode_args, B), offsetof(tkv_decode_args, sm_scale),
              offsetof(tkv_decode_args, num_splits), offsetof(tkv_decode_args, counters),
              offsetof(tkv_decode_args, waves), offsetof(tkv_decode_args, block_table),
              offsetof(tkv_decode_args, page_size), offsetof(tkv_decode_args, num_pages),
              offsetof(tkv_decode_args, k_new), offsetof(tkv_decode_args, new_is_fp32),
+             offsetof(tkv_decode_args, key_block), offsetof(tkv_decode_args, num_splits_total),
              sizeof(tkv_device_info_t));
       return 0;
     }"""
@@ -90,7 +91,8 @@ def test_decode_args_layout_matches_c():
     assert vals == [ctypes.sizeof(A), A.q_is_fp32.offset, A.seq_lens.offset, A.B.offset,
                     A.sm_scale.offset, A.num_splits.offset, A.counters.offset, A.waves.offset,
                     A.block_table.offset, A.page_size.offset, A.num_pages.offset,
-                    A.k_new.offset, A.new_is_fp32.offset, ctypes.sizeof(_lib.DeviceInfo)]
+                    A.k_new.offset, A.new_is_fp32.offset, A.key_block.offset,
+                    A.num_splits_total.offset, ctypes.sizeof(_lib.DeviceInfo)]
 
 
 def test_c_entry_points_reject_bad_arguments_without_a_gpu():

@@ -62,6 +62,9 @@ class DecodeArgs(ctypes.Structure):
         ("k_new", ctypes.c_void_p),
         ("v_new", ctypes.c_void_p),
         ("new_is_fp32", ctypes.c_int32),
+        ("key_block", ctypes.c_int32),
+        ("split_base", ctypes.c_int32),
+        ("num_splits_total", ctypes.c_int32),
     ]
 
 
@@ -93,6 +96,10 @@ SIGNATURES = {
                           ctypes.c_int),
     "tkv_paged_quantize_pack": ([_P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P, _I32, _I32,
                                  _I32, _P, _P, _P, _P], ctypes.c_int),
+    "tkv_quantize_keys_channel": ([_P, _I32, _I32, _I32, _I32, _I32, _I32, _P, _I32, _P, _P, _P,
+                                   _P], ctypes.c_int),
+    "tkv_channel_decode_attention": ([ctypes.POINTER(DecodeArgs), _P, _P, _P, _I32, _P],
+                                     ctypes.c_int),
     "tkv_pack_codes": ([_P, _I64, _I32, _I32, _P, _P], ctypes.c_int),
     "tkv_unpack_dequant": ([_P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P], ctypes.c_int),
     "tkv_device_info": ([ctypes.POINTER(DeviceInfo)], ctypes.c_int),

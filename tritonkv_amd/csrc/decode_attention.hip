@@ -274,7 +274,14 @@ static int validate_common(const tkv_decode_args* a) {
   if (a->split_size <= 0 || a->num_splits <= 0 || a->num_splits > 65535) return TKV_EINVAL;
   if ((int64_t)a->split_size * (a->num_splits - 1) >= a->S) return TKV_EINVAL;  // empty split
   if ((int64_t)a->split_size * a->num_splits < a->S) return TKV_EINVAL;        // uncovered
-  if (a->num_splits > 1 && (!a->acc || !a->maxs || !a->sums)) return TKV_EINVAL;
+  const int total = a->num_splits_total ? a->num_splits_total : a->num_splits;
+  if (a->split_base < 0 || a->num_splits_total < 0 || total > 65535 ||
+      a->split_base + a->num_splits > total)
+    return TKV_EINVAL;
+  if (total > 1 && (!a->acc || !a->maxs || !a->sums)) return TKV_EINVAL;
+  if (a->counters && (a->split_base != 0 || total != a->num_splits)) return TKV_EINVAL;
+  if (a->key_block != 0 && a->key_block != 32) return TKV_EINVAL;
+  if (a->key_block && (a->S % 32 || a->page_size > 0 || a->k_new)) return TKV_EINVAL;
   // Vector loads: caches 16-byte aligned, metadata 4-byte, partials 8-byte.
   if (((uintptr_t)a->k | (uintptr_t)a->v) & 15) return TKV_EINVAL;
   if (((uintptr_t)a->k_scale | (uintptr_t)a->k_zero | (uintptr_t)a->v_scale |
@@ -328,6 +335,9 @@ static SplitParams make_params(const tkv_decode_args* a) {
   p.split_size = a->split_size;
   p.q_fp32 = a->q_is_fp32 ? 1 : 0;
   p.qk_scale = a->sm_scale * kLog2e;
+  p.key_block = a->key_block;
+  p.split_base = a->split_base;
+  p.ns_total = a->num_splits_total ? a->num_splits_total : a->num_splits;
   return p;
 }
 
@@ -402,6 +412,7 @@ static int launch_fused_split(const tkv_decode_args* a, hipStream_t st) {
   if (gs <= 0 || gs > a->D || a->D % gs) return TKV_EINVAL;
   if ((a->k_nbits != 2 && a->k_nbits != 4) || (a->v_nbits != 2 && a->v_nbits != 4))
     return TKV_EINVAL;
+  if (a->key_block && gs > 32) return TKV_EUNSUPPORTED;  // per-channel keys: V groups of 16 or 32
   const SplitParams p = make_params(a);
   const dim3 grid = split_grid(a);
   (void)hipGetLastError();
@@ -415,7 +426,7 @@ static int launch_fp16_split(const tkv_decode_args* a, hipStream_t st) {
   const int rc = validate_common(a);
   if (rc) return rc;
   // the fp16 control reads contiguous caches and has no fused append
-  if (a->page_size > 0 || a->k_new) return TKV_EUNSUPPORTED;
+  if (a->page_size > 0 || a->k_new || a->key_block) return TKV_EUNSUPPORTED;
   const SplitParams p = make_params(a);
   const dim3 grid = split_grid(a);
   (void)hipGetLastError();
@@ -450,16 +461,58 @@ extern "C" int tkv_fp16_decode_split(const tkv_decode_args* a, tkv_stream_t stre
   return tkv::launch_fp16_split(a, reinterpret_cast<hipStream_t>(stream));
 }
 
+// The whole-attention entry points run every split themselves.
+static bool own_all_splits(const tkv_decode_args* a) {
+  return a && a->split_base == 0 && (a->num_splits_total == 0 || a->num_splits_total == a->num_splits);
+}
+
 extern "C" int tkv_fused_decode_attention(const tkv_decode_args* a, tkv_stream_t stream) {
+  if (a && !own_all_splits(a)) return TKV_EINVAL;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int rc = tkv::launch_fused_split(a, st);
   return rc ? rc : tkv::finish_combine(a, st);
 }
 
 extern "C" int tkv_fp16_decode_attention(const tkv_decode_args* a, tkv_stream_t stream) {
+  if (a && !own_all_splits(a)) return TKV_EINVAL;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int rc = tkv::launch_fp16_split(a, st);
   return rc ? rc : tkv::finish_combine(a, st);
+}
+
+extern "C" int tkv_channel_decode_attention(const tkv_decode_args* a, const void* k_res,
+                                            const void* v_res, const int32_t* res_lens,
+                                            int32_t res_cap, tkv_stream_t stream) {
+  using namespace tkv;
+  if (!a || !k_res || !v_res || res_cap <= 0) return TKV_EINVAL;
+  if (a->key_block != 32) return TKV_EINVAL;
+  if (((uintptr_t)k_res | (uintptr_t)v_res) & 15) return TKV_EINVAL;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int total = a->num_splits + 1;
+  tkv_decode_args qa = *a;  // the quantized history: partial rows 0 .. num_splits - 1
+  qa.split_base = 0;
+  qa.num_splits_total = total;
+  qa.counters = nullptr;
+  int rc = launch_fused_split(&qa, st);
+  if (rc) return rc;
+  tkv_decode_args ra = *a;  // the fp16 window: partial row num_splits
+  ra.k = k_res;
+  ra.v = v_res;
+  ra.k_scale = ra.k_zero = ra.v_scale = ra.v_zero = nullptr;
+  ra.seq_lens = res_lens;
+  ra.S = res_cap;
+  ra.split_size = res_cap;
+  ra.num_splits = 1;
+  ra.split_base = a->num_splits;
+  ra.num_splits_total = total;
+  ra.counters = nullptr;
+  ra.key_block = 0;
+  ra.waves = 4;
+  rc = launch_fp16_split(&ra, st);
+  if (rc) return rc;
+  (void)hipGetLastError();
+  launch_combine(a->acc, a->maxs, a->sums, a->out, a->B, a->HQ, total, a->D, st);
+  return status_of_launch();
 }
 
 extern "C" int tkv_combine_splits(const float* acc, const float* maxs, const float* sums,

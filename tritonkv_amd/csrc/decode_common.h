@@ -39,6 +39,11 @@ struct SplitParams {
   int new_fp32;
   int HQ, HKV, S, G, num_splits, split_size, q_fp32;
   float qk_scale;  // sm_scale * log2(e)
+  // Per-channel keys (quantized path): key_block == 32 makes ks/kz
+  // (B, HKV, S/32, D), one fp16 scale and zero per (32-token block, channel).
+  int key_block;
+  // This launch's splits are partial rows split_base + split of ns_total.
+  int split_base, ns_total;
 };
 
 constexpr int kChunk = 32;  // tokens per wave iteration (two 16-row MFMA tiles)
@@ -144,10 +149,10 @@ __device__ void merge_and_store(const SplitParams& prm, const MergeView& mv, int
       }
     }
     const int64_t row = (int64_t)b * prm.HQ + h0 + n;
-    if (prm.num_splits == 1) {
+    if (prm.ns_total == 1) {
       prm.out[row * D + d] = o / l;
     } else {
-      const int64_t pr = row * prm.num_splits + split;
+      const int64_t pr = row * prm.ns_total + prm.split_base + split;
       prm.acc[pr * D + d] = o;
       if (d == 0) {
         prm.maxs[pr] = mstar;
@@ -155,7 +160,7 @@ __device__ void merge_and_store(const SplitParams& prm, const MergeView& mv, int
       }
     }
   }
-  if (prm.num_splits == 1 || prm.counters == nullptr) return;
+  if (prm.ns_total == 1 || prm.counters == nullptr) return;  // counters: split_base 0, all splits
 
   // Fused combine.  Each workgroup releases its partials (agent scope: the
   // reader may sit on another XCD with its own L2) and takes a ticket; the
@@ -215,6 +220,9 @@ template <int D, int KNB, int GS>
 struct QOperands {
   u4 qf[KLayout<D, KNB, GS>::NKM];
   u2 qzb;
+  // The same dims of step m in natural order, unscaled fp16 pairs (CB/2 used):
+  // for per-channel keys, whose zero-point term is a dot product with q.
+  u4 qn[KLayout<D, KNB, GS>::NKM];
 };
 
 template <int D, int KNB, int GS>
@@ -270,6 +278,11 @@ __device__ __forceinline__ void load_q_operands(const SplitParams& prm, int b, i
         wv[s2 / 2] = pack_h2(q0 * pre, q1 * pre);
       }
       qf[m] = u4{wv[0], wv[1], wv[2], wv[3]};
+      uint32_t nv[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int s2 = 0; s2 < KL::CB; s2 += 2)
+        nv[s2 / 2] = hv ? pack_h2(qv[m][s2], qv[m][s2 + 1]) : 0u;
+      qo.qn[m] = u4{nv[0], nv[1], nv[2], nv[3]};
     }
 #pragma unroll
     for (int g = 0; g < NG; ++g) qz[g] = xor_sum16_32(qz[g]);

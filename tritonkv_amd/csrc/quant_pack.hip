@@ -215,6 +215,73 @@ quantize_pack_wide_kernel(const void* __restrict__ x, int rows, int HKV, int N,
   }
 }
 
+// Per-channel (KIVI-style) keys: one wave per block of 32 tokens of one
+// (b, kv head).  Every channel of the block is one group of 32 values
+// (min/max, fp16 scale and zero, codes), the group-wise arithmetic of
+// quantize_row applied along the token axis.  Lane j owns byte column j of
+// the block's rows, i.e. channels j + p*DP (p < P), so the min/max need no
+// cross-lane step and the lane packs each token's byte j itself.  Lanes >= DP
+// repeat lanes j - DP and store nothing.  A block whose destination does not
+// start on a 32-token boundary, or does not fit [0, S_cap), is not written.
+template <int D, int NB, bool F32>
+__global__ void __launch_bounds__(256)
+quantize_keys_channel_kernel(const void* __restrict__ x, int64_t blocks, int HKV, int NBLK,
+                             const int32_t* __restrict__ positions, int S_cap,
+                             uint8_t* __restrict__ packed, uint16_t* __restrict__ scale,
+                             uint16_t* __restrict__ zero) {
+  constexpr int P = 8 / NB, DP = D / P, QMAX = (1 << NB) - 1, T = 32;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int64_t blk = (int64_t)blockIdx.x * 4 + w;
+  if (blk >= blocks) return;  // whole wave
+  const int j = lane % DP;
+  const int64_t bh = blk / NBLK;
+  const int tb = (int)(blk - bh * NBLK);
+  const int b = (int)(bh / HKV);
+  const int64_t src0 = (bh * NBLK + tb) * T;  // first source row
+  float v[P][T];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int64_t e = (src0 + t) * D + j + p * DP;
+      v[p][t] = F32 ? static_cast<const float*>(x)[e] : (float)static_cast<const _Float16*>(x)[e];
+    }
+  const int64_t dst_t = (int64_t)(positions ? positions[b] : 0) + (int64_t)tb * T;
+  const bool ok = dst_t >= 0 && dst_t % T == 0 && dst_t + T <= S_cap && lane < DP;
+  uint32_t bytes[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) bytes[t] = 0;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    float mn = v[p][0], mx = v[p][0];
+#pragma unroll
+    for (int t = 1; t < T; ++t) {
+      mn = fminf(mn, v[p][t]);
+      mx = fmaxf(mx, v[p][t]);
+    }
+    float sc = (mx - mn) / (float)QMAX;
+    if (!(sc > 0.0f)) sc = 1.0f;
+    const _Float16 s16 = (_Float16)sc;
+    const _Float16 z16 = (_Float16)mn;
+    const float sf = (float)s16, zf = (float)z16, rs = __builtin_amdgcn_rcpf(sf);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      float c = rint_quotient(v[p][t] - zf, sf, rs);
+      if (c != c) c = 0.0f;
+      c = fminf(fmaxf(c, 0.0f), (float)QMAX);
+      bytes[t] |= (uint32_t)c << (p * NB);
+    }
+    if (ok) {
+      const int64_t m = (bh * (S_cap / T) + dst_t / T) * D + j + p * DP;
+      scale[m] = __builtin_bit_cast(uint16_t, s16);
+      zero[m] = __builtin_bit_cast(uint16_t, z16);
+    }
+  }
+  if (!ok) return;
+#pragma unroll
+  for (int t = 0; t < T; ++t) packed[(bh * S_cap + dst_t + t) * DP + j] = (uint8_t)bytes[t];
+}
+
 // One thread per packed dword.
 __global__ void __launch_bounds__(256)
 pack_codes_kernel(const uint8_t* __restrict__ codes, int64_t rows, int D, int NB,
@@ -458,6 +525,45 @@ extern "C" int tkv_paged_quantize_pack(const void* x, int32_t x_is_fp32, int32_t
   launch_quantize<Dv, NBv, GSv>(x, x_is_fp32 != 0, rows, HKV, N, positions, S_cap, pm, packed, scale, zero, st)
   TKV_DISPATCH_DNG(D, nbits, group_size, TKV_Q);
 #undef TKV_Q
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? TKV_OK : (int)e;
+}
+
+extern "C" int tkv_quantize_keys_channel(const void* x, int32_t x_is_fp32, int32_t B, int32_t HKV,
+                                         int32_t N, int32_t D, int32_t nbits,
+                                         const int32_t* positions, int32_t S_cap, uint8_t* packed,
+                                         uint16_t* scale, uint16_t* zero, tkv_stream_t stream) {
+  using namespace tkv;
+  constexpr int T = 32;
+  if (!x || !packed || !scale || !zero) return TKV_EINVAL;
+  if (B <= 0 || HKV <= 0 || N <= 0 || D <= 0 || S_cap <= 0) return TKV_EINVAL;
+  if (N % T || S_cap % T) return TKV_EINVAL;
+  if (!positions && N > S_cap) return TKV_EINVAL;
+  if (nbits != 2 && nbits != 4) return TKV_EINVAL;
+  if (((uintptr_t)scale & 1) || ((uintptr_t)zero & 1)) return TKV_EINVAL;
+  if ((uintptr_t)x & (x_is_fp32 ? 3 : 1)) return TKV_EINVAL;
+  const int64_t blocks = (int64_t)B * HKV * (N / T);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)((blocks + 3) / 4));
+  const bool f32 = x_is_fp32 != 0;
+  (void)hipGetLastError();
+#define TKV_KC(Dv, NBv)                                                                       \
+  do {                                                                                        \
+    if (f32)                                                                                  \
+      quantize_keys_channel_kernel<Dv, NBv, true><<<grid, 256, 0, st>>>(                      \
+          x, blocks, HKV, N / T, positions, S_cap, packed, scale, zero);                      \
+    else                                                                                      \
+      quantize_keys_channel_kernel<Dv, NBv, false><<<grid, 256, 0, st>>>(                     \
+          x, blocks, HKV, N / T, positions, S_cap, packed, scale, zero);                      \
+  } while (0)
+  if (D == 128) {
+    if (nbits == 4) TKV_KC(128, 4); else TKV_KC(128, 2);
+  } else if (D == 64) {
+    if (nbits == 4) TKV_KC(64, 4); else TKV_KC(64, 2);
+  } else {
+    return TKV_EUNSUPPORTED;
+  }
+#undef TKV_KC
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? TKV_OK : (int)e;
 }

@@ -137,7 +137,7 @@ __device__ __forceinline__ void wait_lgkmcnt0() {
 // Issue the DMA of one chunk into a stage.  `valid` false turns every lane's
 // offset out of the buffer range, so the instructions still retire (keeping
 // the vmcnt arithmetic static) but read nothing and write zeros.
-template <int D, int KNB, int VNB, int GS>
+template <int D, int KNB, int VNB, int GS, bool KCH = false>
 __device__ __forceinline__ void issue_chunk(uint8_t* stage, const rsrc_t& rk, const rsrc_t& rv,
                                             const rsrc_t (&rm)[4], int cb, bool valid, int lane) {
   // cb: index, within the resources, of the chunk's first row
@@ -165,13 +165,21 @@ __device__ __forceinline__ void issue_chunk(uint8_t* stage, const rsrc_t& rk, co
       dma16<kPolDma>(rv, to_lds(stage + SG::V_OFF + 1024 * q), off);
   }
   // metadata: the chunk's [t][g] rows are contiguous; lane L copies dword L
-  // (NG == 1: the fp16 of token L, into dword L).
+  // (NG == 1: the fp16 of token L, into dword L).  Per-channel keys: the K
+  // scale and zero tensors hold one row of D fp16 per 32-token block, the
+  // chunk's block; its 2D bytes go to the front of the tensor's MB bytes
+  // (MB >= 2D for the group sizes that allow them); further instructions read
+  // nothing, keeping the instruction count of the vmcnt arithmetic.
 #pragma unroll
   for (int tsr = 0; tsr < 4; ++tsr)
 #pragma unroll
     for (int q = 0; q < SG::NMI; ++q) {
       uint8_t* dst = stage + SG::M_OFF + tsr * SG::MB + 256 * q;
-      if constexpr (SG::NG == 1) {
+      if (KCH && tsr < 2) {
+        static_assert(!KCH || SG::MB >= 2 * D, "per-channel key row must fit the K metadata slot");
+        const uint32_t off = valid && q == 0 ? (uint32_t)(cb / kChunk) * D * 2 + 4 * lane : kOut;
+        if (lane < D / 2) dma4<kPolDma>(rm[tsr], to_lds(dst), off);
+      } else if constexpr (SG::NG == 1) {
         const uint32_t off = valid ? (uint32_t)(cb + lane) * 2 : kOut;
         if (lane < kChunk) dma2<kPolDma>(rm[tsr], to_lds(dst), off);
       } else {
@@ -315,7 +323,7 @@ struct LdsKernelSmem {
   static constexpr int PATCH = (PATCH_META + 4 * SG::NG * 2 + 15) / 16 * 16;
 };
 
-template <int D, int KNB, int VNB, int GS, int NW, int NSTAGE, bool PAGED, bool PT>
+template <int D, int KNB, int VNB, int GS, int NW, int NSTAGE, bool PAGED, bool PT, bool KCH = false>
 __global__ void __launch_bounds__(NW * 64)
 quant_split_lds_kernel(SplitParams prm) {
   using SG = StageGeom<D, KNB, VNB, GS>;
@@ -328,6 +336,7 @@ quant_split_lds_kernel(SplitParams prm) {
   constexpr int NI = SG::NINSTR;
   static_assert(2 * NG <= 16, "zero-point MFMA holds hi/lo of at most 8 groups");
   static_assert((NSTAGE - 1) * NI < 64, "vmcnt range");
+  static_assert(!KCH || (!PAGED && !PT && GS <= 32), "per-channel keys: contiguous, one-tile path");
 
   __shared__ __attribute__((aligned(16))) uint8_t smem[NW * SM::WAVE + SM::PATCH];
 
@@ -363,7 +372,12 @@ quant_split_lds_kernel(SplitParams prm) {
                      make_rsrc(prm.vz + slab * rows * NG, (uint32_t)rows * NG * 2)},
                     row};
   };
-  const ChunkSrc unit_src = slab_src(PAGED ? 0 : (int64_t)unit, PAGED ? prm.page_size : prm.S, 0);
+  ChunkSrc unit_src = slab_src(PAGED ? 0 : (int64_t)unit, PAGED ? prm.page_size : prm.S, 0);
+  if constexpr (KCH) {  // K scale / zero: (S/32, D) per (b, kv head)
+    const int64_t nblk = prm.S / kChunk;
+    unit_src.m[0] = make_rsrc(prm.ks + (int64_t)unit * nblk * D, (uint32_t)(nblk * D * 2));
+    unit_src.m[1] = make_rsrc(prm.kz + (int64_t)unit * nblk * D, (uint32_t)(nblk * D * 2));
+  }
   auto chunk_src = [&](int cb, int page) -> ChunkSrc {
     if constexpr (PAGED)
       return slab_src((int64_t)page * prm.HKV + hk, prm.page_size,
@@ -401,7 +415,7 @@ quant_split_lds_kernel(SplitParams prm) {
     const int page0 = to_page(e0);
     page_next = to_page(e1);
     const ChunkSrc src = chunk_src(cb0, page0);
-    issue_chunk<D, KNB, VNB, GS>(ring, src.k, src.v, src.m, src.row, cb0 < hi, lane);
+    issue_chunk<D, KNB, VNB, GS, KCH>(ring, src.k, src.v, src.m, src.row, cb0 < hi, lane);
     tab_pending = tab_entry(cb0 + 2 * cstride);
   } else {
     // the first NSTAGE - 1 chunks into stages 0 .. NSTAGE - 2
@@ -409,7 +423,7 @@ quant_split_lds_kernel(SplitParams prm) {
       constexpr int SS = decltype(s)::value;
       const int c = cb0 + SS * cstride;
       const ChunkSrc src = chunk_src(c, 0);
-      issue_chunk<D, KNB, VNB, GS>(ring + SS * SG::BYTES, src.k, src.v, src.m, src.row, c < hi, lane);
+      issue_chunk<D, KNB, VNB, GS, KCH>(ring + SS * SG::BYTES, src.k, src.v, src.m, src.row, c < hi, lane);
     });
   }
 
@@ -548,7 +562,7 @@ quant_split_lds_kernel(SplitParams prm) {
       asm volatile("" ::: "memory");
       const bool valid = !TAIL && cn < hi;
       const ChunkSrc src = chunk_src(cn, page_next);
-      issue_chunk<D, KNB, VNB, GS>(ring + ((SK + NSTAGE - 1) % NSTAGE) * SG::BYTES, src.k, src.v,
+      issue_chunk<D, KNB, VNB, GS, KCH>(ring + ((SK + NSTAGE - 1) % NSTAGE) * SG::BYTES, src.k, src.v,
                                    src.m, src.row, valid, lane);
     }
     // Paged: one more vector load in flight, behind the DMA just issued.
@@ -651,6 +665,75 @@ quant_split_lds_kernel(SplitParams prm) {
     } else {
       // ---- scores S^T for the two 16-token tiles ---------------------------
       float x[8];
+      if constexpr (KCH) {
+        // Per-channel keys: score = sum_d (q_d s_d) c_d + sum_d q_d z_d with
+        // the chunk's (block's) scale and zero of channel d.  The B operands
+        // become q * s for the chunk, in the slot order of qf, as two fp16
+        // parts: hi = fp16(q s) and lo = q s - hi, exact by one fused
+        // multiply-add (the error of an fp16 product is an fp16 number), so
+        // the two MFMAs per step see q s to about 22 bits -- a single fp16
+        // product alone put the scores of keys with large channels off by up
+        // to 2^-12 of each term.  The zero term is one fp32 dot product per
+        // head, summed over the lane groups.
+        u4 qs[NKM], ql[NKM];
+        float bias = 0.0f;
+#pragma unroll
+        for (int m = 0; m < NKM; ++m) {
+          const int d0 = m * KL::KSTEP + KL::CB * j;
+          u4 sn, zn;
+          if constexpr (KL::CB == 8) {
+            sn = *reinterpret_cast<const u4*>(mks + 2 * d0);
+            zn = *reinterpret_cast<const u4*>(mkz + 2 * d0);
+          } else {
+            const u2 s2 = *reinterpret_cast<const u2*>(mks + 2 * d0);
+            const u2 z2 = *reinterpret_cast<const u2*>(mkz + 2 * d0);
+            sn = u4{s2[0], s2[1], 0u, 0u};
+            zn = u4{z2[0], z2[1], 0u, 0u};
+          }
+          // slot pairs (0,2) (1,3) (4,6) (5,7) of the step's dims
+          const uint32_t ss[4] = {perm(sn[1], sn[0], 0x05040100u), perm(sn[1], sn[0], 0x07060302u),
+                                  perm(sn[3], sn[2], 0x05040100u), perm(sn[3], sn[2], 0x07060302u)};
+          qs[m] = u4{pk_mul(qf[m][0], ss[0]), pk_mul(qf[m][1], ss[1]),
+                     KL::CB == 8 ? pk_mul(qf[m][2], ss[2]) : 0u,
+                     KL::CB == 8 ? pk_mul(qf[m][3], ss[3]) : 0u};
+          ql[m] = u4{pk_fma_rem(qf[m][0], ss[0], qs[m][0]), pk_fma_rem(qf[m][1], ss[1], qs[m][1]),
+                     KL::CB == 8 ? pk_fma_rem(qf[m][2], ss[2], qs[m][2]) : 0u,
+                     KL::CB == 8 ? pk_fma_rem(qf[m][3], ss[3], qs[m][3]) : 0u};
+          // Whole-vector casts: this compiler folds a loop's per-element casts of
+          // an integer vector's elements (here to h2) to element 0.
+          const h8 qh = __builtin_bit_cast(h8, qo.qn[m]), zh = __builtin_bit_cast(h8, zn);
+#pragma unroll
+          for (int i = 0; i < KL::CB / 2; ++i)
+            bias = __builtin_amdgcn_fdot2(h2{qh[2 * i], qh[2 * i + 1]}, h2{zh[2 * i], zh[2 * i + 1]},
+                                          bias, false);
+        }
+        const float bias24 = xor_sum16_32(bias) * kTwoM24;
+  #pragma unroll
+        for (int a = 0; a < 2; ++a) {
+          f4 c = f4{0.f, 0.f, 0.f, 0.f};
+          typename std::conditional<KL::CB == 8, u2, uint32_t>::type kx[KL::NLOAD];
+  #pragma unroll
+          for (int Lh = 0; Lh < KL::NLOAD; ++Lh) {
+            constexpr int kTile = 16 * (KL::DP / 16) * 16;
+            if constexpr (KL::CB == 8) kx[Lh] = *reinterpret_cast<const u2*>(st + koff[Lh] + kTile * a);
+            else kx[Lh] = *reinterpret_cast<const uint32_t*>(st + koff[Lh] + kTile * a);
+          }
+  #pragma unroll
+          for (int m = 0; m < NKM; ++m) {
+            if constexpr (KL::CB == 8) {
+              const u4 a8 = k_extract8(kx[KL::load_of_step(m)], kmask[m]);
+              c = mfma_k32(a8, qs[m], c);
+              c = mfma_k32(a8, ql[m], c);
+            } else {
+              const u2 a4 = k_extract4(kx[KL::load_of_step(m)], kmask[m]);
+              c = mfma_k16(a4, u2{qs[m][0], qs[m][1]}, c);
+              c = mfma_k16(a4, u2{ql[m][0], ql[m][1]}, c);
+            }
+          }
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) x[4 * a + i] = c[i] + bias24;
+        }
+      } else {
   #pragma unroll
       for (int a = 0; a < 2; ++a) {
         f4 c[NG];
@@ -702,6 +785,7 @@ quant_split_lds_kernel(SplitParams prm) {
           x[4 * a + i] = sc;
         }
       }
+      }  // per-token key groups
       if constexpr (TAIL) {
   #pragma unroll
         for (int a = 0; a < 2; ++a)
@@ -862,6 +946,15 @@ constexpr int kPairedTilesMinSplit = 8192;
 
 template <int D, int KNB, int VNB, int GS>
 void launch_quant(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
+  if constexpr (GS <= 32) {
+    if (p.key_block) {  // per-channel keys (the host checked: contiguous, no fused append)
+      if (waves == 8)
+        quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, false, true><<<grid, dim3(8 * 64), 0, st>>>(p);
+      else
+        quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false, false, true><<<grid, dim3(4 * 64), 0, st>>>(p);
+      return;
+    }
+  }
   if (p.G <= 8 && p.split_size >= kPairedTilesMinSplit)
     launch_quant_pt<D, KNB, VNB, GS, true>(p, grid, waves, st);
   else launch_quant_pt<D, KNB, VNB, GS, false>(p, grid, waves, st);

@@ -96,6 +96,13 @@ __device__ __forceinline__ float half_lo(uint32_t w) {
 __device__ __forceinline__ float half_hi(uint32_t w) {
   return (float)__builtin_bit_cast(h2, w)[1];
 }
+// a * b - p for two fp16 lanes with one rounding (v_pk_fma_f16): with
+// p = pk_mul(a, b), the exact rounding error of that product.
+__device__ __forceinline__ uint32_t pk_fma_rem(uint32_t a, uint32_t b, uint32_t p) {
+  const h2 r = __builtin_elementwise_fma(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b),
+                                         -__builtin_bit_cast(h2, p));
+  return __builtin_bit_cast(uint32_t, r);
+}
 __device__ __forceinline__ uint32_t pk_mul(uint32_t a, uint32_t b) {
   h2 r = __builtin_bit_cast(h2, a) * __builtin_bit_cast(h2, b);
   return __builtin_bit_cast(uint32_t, r);
