@@ -589,6 +589,91 @@ def ragged_70b(steps, warmup, seed=2024):
     return res
 
 
+def channel_keys(steps, warmup, B=32, HQ=32, HKV=8, S=32768, D=128, window=16):
+    """Per-channel (KIVI-style) keys at the Llama-3-8B shape: keys quantized per
+    (32-token block, channel), values per token (group 32), a 16-token fp16
+    window; one step = split kernel (per-channel key path) + fp16 window split
+    + combine.  Accuracy on the same synthetic keys (4 x8 outlier channels per
+    KV head): relative L2 error of dequantized keys and of the attention output
+    of batch rows 0-3 against fp32 attention over the original fp16 K/V, for
+    per-token and per-channel keys (values per token either way)."""
+    import torch
+
+    from tritonkv_amd.channel import channel_decode_attention, quantize_keys_per_channel
+    from tritonkv_amd.kernels import fused_decode_attention
+    from tritonkv_amd.quantize import (dequantize_groupwise, quantize_groupwise, unpack_codes)
+
+    res = {}
+    for nb in (2, 4):
+        calls, first = [], None
+        for c in range(2):
+            q, k, v = llama_inputs(seed=10 + c, B=B, HQ=HQ, HKV=HKV, S=S, D=D)
+            g = torch.Generator(device="cuda").manual_seed(50 + c)
+            kr = torch.randn(B, HKV, 32, D, device="cuda", generator=g, dtype=torch.float16)
+            vr = torch.randn(B, HKV, 32, D, device="cuda", generator=g, dtype=torch.float16)
+            ck = quantize_keys_per_channel(k, nb)
+            vq = quantize_groupwise(v, nb, 32)
+            ql = torch.full((B,), S, dtype=torch.int32, device="cuda")
+            rl = torch.full((B,), window, dtype=torch.int32, device="cuda")
+            out = torch.empty(B, HQ, D, device="cuda")
+            ws = {}
+
+            def step(q=q, ck=ck, vq=vq, kr=kr, vr=vr, ql=ql, rl=rl, out=out, ws=ws):
+                channel_decode_attention(q, ck, vq, kr, vr, q_lens=ql, res_lens=rl, out=out,
+                                         _workspace=ws)
+            step()
+            calls.append(step)
+            if c == 0:
+                first = (q, k, v, ck, vq)
+            else:
+                del k, v
+        us, _, _ = timed_steps(calls, steps, warmup)
+        krow = D * nb // 8 + 4 * D // 32
+        vrow = D * nb // 8 + 4 * (D // 32)
+        nbytes = B * HKV * (S * (krow + vrow) + window * 2 * D * 2) + B * HQ * D * (2 + 4)
+        entry = {"us_per_step": round(us, 2), "algorithmic_bytes": nbytes,
+                 "gbps_step": round(nbytes / us / 1e3, 1),
+                 "frac_of_hbm_peak_step": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+        # accuracy, batch rows 0-3
+        q, k, v, ck, vq = first
+        r = slice(0, 4)
+        kf, vf = k[r].float(), v[r].float()
+        codes = unpack_codes(ck.packed[r], nb, D).float()
+        kd_ch = codes * ck.scale[r].float().repeat_interleave(32, dim=2) + \
+            ck.zero[r].float().repeat_interleave(32, dim=2)
+        kq_tok = quantize_groupwise(k[r].contiguous(), nb, 32)
+        kd_tok = dequantize_groupwise(kq_tok)
+        rel = lambda a, b: float((a - b).norm() / b.norm())
+        entry["key_rel_l2_per_token"] = round(rel(kd_tok, kf), 4)
+        entry["key_rel_l2_per_channel"] = round(rel(kd_ch, kf), 4)
+
+        def truth(qr):
+            G = HQ // HKV
+            qg = qr.float().reshape(4, HKV, G, D)
+            sc = torch.matmul(qg, kf.transpose(-1, -2)) / math.sqrt(D)
+            return torch.matmul(torch.softmax(sc, dim=-1), vf).reshape(4, HQ, D)
+
+        ref = truth(q[r])
+        vq4 = type(vq)(vq.packed[r].contiguous(), vq.scale[r].contiguous(),
+                       vq.zero[r].contiguous(), vq.nbits, vq.group_size, D)
+        ck4 = type(ck)(ck.packed[r].contiguous(), ck.scale[r].contiguous(),
+                       ck.zero[r].contiguous(), ck.nbits, D)
+        kr0 = torch.zeros(4, HKV, 32, D, device="cuda", dtype=torch.float16)
+        got_ch = channel_decode_attention(q[r].contiguous(), ck4, vq4, kr0, kr0.clone(),
+                                          res_lens=torch.zeros(4, dtype=torch.int32, device="cuda"))
+        got_tok = fused_decode_attention(q[r].contiguous(), kq_tok, vq4)
+        entry["attn_rel_l2_per_token_keys"] = round(rel(got_tok, ref), 4)
+        entry["attn_rel_l2_per_channel_keys"] = round(rel(got_ch, ref), 4)
+        res[f"k{nb}v{nb}"] = entry
+        print(f"# llama per-channel keys {nb}-bit: step {us:.2f} us; key rel-L2 per-token "
+              f"{entry['key_rel_l2_per_token']} vs per-channel {entry['key_rel_l2_per_channel']}; "
+              f"attention rel-L2 {entry['attn_rel_l2_per_token_keys']} vs "
+              f"{entry['attn_rel_l2_per_channel_keys']}", file=sys.stderr, flush=True)
+        del calls, first, q, k, v, ck, vq, kf, vf, codes, kd_ch, kd_tok, kq_tok
+        torch.cuda.empty_cache()
+    return res
+
+
 # ---------------------------------------------------------------------------
 # Qwen2.5-1.5B table (BASELINE.json configs 2 and 3)
 # ---------------------------------------------------------------------------
@@ -931,6 +1016,7 @@ def main() -> int:
         detail["qwen2.5-1.5b_serving_step"] = qwen_serving_steps()
         detail["qwen2.5-1.5b_e2e_decode"] = qwen_e2e()
         detail["ragged_70b_k4v2"] = ragged_70b(a.steps, a.warmup)
+        detail["channel_keys"] = channel_keys(a.steps, a.warmup)
 
     line = {
         "metric": METRIC,

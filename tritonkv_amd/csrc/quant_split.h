@@ -673,10 +673,9 @@ quant_split_lds_kernel(SplitParams prm) {
         // multiply-add (the error of an fp16 product is an fp16 number), so
         // the two MFMAs per step see q s to about 22 bits -- a single fp16
         // product alone put the scores of keys with large channels off by up
-        // to 2^-12 of each term.  The zero term is one fp32 dot product per
-        // head, summed over the lane groups.
+        // to 2^-12 of each term.
         u4 qs[NKM], ql[NKM];
-        float bias = 0.0f;
+        f4 cz = f4{0.f, 0.f, 0.f, 0.f};  // the zero term, in every token row of head n
 #pragma unroll
         for (int m = 0; m < NKM; ++m) {
           const int d0 = m * KL::KSTEP + KL::CB * j;
@@ -699,15 +698,14 @@ quant_split_lds_kernel(SplitParams prm) {
           ql[m] = u4{pk_fma_rem(qf[m][0], ss[0], qs[m][0]), pk_fma_rem(qf[m][1], ss[1], qs[m][1]),
                      KL::CB == 8 ? pk_fma_rem(qf[m][2], ss[2], qs[m][2]) : 0u,
                      KL::CB == 8 ? pk_fma_rem(qf[m][3], ss[3], qs[m][3]) : 0u};
-          // Whole-vector casts: this compiler folds a loop's per-element casts of
-          // an integer vector's elements (here to h2) to element 0.
-          const h8 qh = __builtin_bit_cast(h8, qo.qn[m]), zh = __builtin_bit_cast(h8, zn);
-#pragma unroll
-          for (int i = 0; i < KL::CB / 2; ++i)
-            bias = __builtin_amdgcn_fdot2(h2{qh[2 * i], qh[2 * i + 1]}, h2{zh[2 * i], zh[2 * i + 1]},
-                                          bias, false);
+          // zero term by MFMA: every A row is the step's zero points (natural
+          // order), B is q of the same dims (natural order, unscaled), so each
+          // output row holds sum_d z_d q_{n,d} over the step: exact fp16
+          // products, fp32 sums, no cross-lane reduction.
+          if constexpr (KL::CB == 8) cz = mfma_k32(zn, qo.qn[m], cz);
+          else cz = mfma_k16(u2{zn[0], zn[1]}, u2{qo.qn[m][0], qo.qn[m][1]}, cz);
         }
-        const float bias24 = xor_sum16_32(bias) * kTwoM24;
+        const float bias24 = cz[0] * kTwoM24;
   #pragma unroll
         for (int a = 0; a < 2; ++a) {
           f4 c = f4{0.f, 0.f, 0.f, 0.f};
