@@ -10,7 +10,11 @@ surface:
 * ``tritonkv_amd.quantize``: ``QuantizedTensor`` and the split-P
   pack/scale/zero layout (reference ``quantize.py``), plus ``append_kv``;
 * ``tritonkv_amd.paged``: the same cache format in page pools addressed
-  through a block table (``paged_append``, ``paged_decode_attention``).
+  through a block table (``paged_append``, ``paged_decode_attention``);
+* ``tritonkv_amd.channel``: per-channel (KIVI-style) keys with an fp16
+  residual window, the key format the reference plans
+  (``ChannelKVCache``, ``channel_decode_attention``);
+* ``tritonkv_amd.hf``: a ``transformers`` cache and attention function.
 
 The kernels live in ``libtkv_hip.so`` (C ABI in ``include/tkv.h``), built by
 ``python -m tritonkv_amd.build``.  There is no CPU or Triton fallback.
