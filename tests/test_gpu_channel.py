@@ -112,12 +112,18 @@ CASES = [
 @pytest.mark.parametrize("case", CASES, ids=lambda c: "K{}V{}-gs{}-D{}-G{}".format(
     c[0], c[1], c[2], c[3], c[4] // c[5]))
 @pytest.mark.parametrize("ns", [None, 1, 3])
-def test_channel_decode_matches_oracle(case, ns):
+@pytest.mark.parametrize("lens", ["blocks", "ragged"])
+def test_channel_decode_matches_oracle(case, ns, lens):
+    """History lengths on block boundaries (what the cache manager makes) and
+    anywhere inside a block (the tail chunk's masking)."""
     from tritonkv_amd.channel import channel_decode_attention
 
     kbits, vbits, gs, D, HQ, HKV = case
     S = 640
-    q_lens, r_lens = [640, 0, 96, 320, 32], [31, 7, 0, 32, 1]
+    if lens == "blocks":
+        q_lens, r_lens = [640, 0, 96, 320, 32], [31, 7, 0, 32, 1]
+    else:
+        q_lens, r_lens = [77, 639, 33, 5, 1], [0, 3, 31, 1, 32]
     B = len(q_lens)
     print(f"channel decode {case} ns={ns}", flush=True)
     q, ck, vq, kres, vres, ql, rl = _window_case(B, HQ, HKV, D, S, kbits, vbits, gs, q_lens,
