@@ -1,0 +1,72 @@
+"""CPU tests of the per-channel key surface: validation and the C ABI's
+argument checks (nothing is launched)."""
+
+from __future__ import annotations
+
+import ctypes
+
+import pytest
+import torch
+
+
+def test_channel_keys_container():
+    from tritonkv_amd.channel import empty_channel_keys
+
+    ck = empty_channel_keys(2, 3, 64, 128, 2, device="cpu")
+    assert ck.shape == (2, 3, 64, 128)
+    assert ck.packed.shape == (2, 3, 64, 32) and ck.scale.shape == (2, 3, 2, 128)
+    assert ck.effective_bits_per_element() == 3.0
+    assert ck.nbytes() == 2 * 3 * (64 * 32 + 2 * 2 * 128 * 2)
+    with pytest.raises(ValueError):
+        empty_channel_keys(1, 1, 40, 128, 4, device="cpu")
+    with pytest.raises(ValueError):
+        empty_channel_keys(1, 1, 64, 128, 3, device="cpu")
+
+
+def test_channel_decode_validates_before_the_backend_check():
+    from tritonkv_amd.channel import channel_decode_attention, empty_channel_keys
+    from tritonkv_amd.quantize import empty_cache
+
+    ck = empty_channel_keys(1, 2, 64, 128, 4, device="cpu")
+    q = torch.zeros(1, 8, 128, dtype=torch.float16)
+    kr = torch.zeros(1, 2, 32, 128, dtype=torch.float16)
+    with pytest.raises(ValueError, match="group_size"):
+        channel_decode_attention(q, ck, empty_cache(1, 2, 64, 128, 4, 64, "cpu"), kr, kr)
+    with pytest.raises(ValueError, match="inconsistent"):
+        channel_decode_attention(q, ck, empty_cache(1, 2, 32, 128, 4, 32, "cpu"), kr, kr)
+    with pytest.raises(ValueError, match="k_res"):
+        channel_decode_attention(q, ck, empty_cache(1, 2, 64, 128, 4, 32, "cpu"), kr.float(), kr)
+
+
+def test_channel_c_entry_points_reject_bad_arguments_without_a_gpu():
+    from tritonkv_amd import _lib
+
+    lib = _lib.load()
+    d = 0x1000
+    # token count not a multiple of 32 / capacity not a multiple of 32
+    assert lib.tkv_quantize_keys_channel(d, 0, 1, 1, 40, 128, 4, None, 64, d, d, d, None) == \
+        _lib.TKV_EINVAL
+    assert lib.tkv_quantize_keys_channel(d, 0, 1, 1, 32, 128, 4, None, 48, d, d, d, None) == \
+        _lib.TKV_EINVAL
+    assert lib.tkv_quantize_keys_channel(d, 0, 1, 1, 32, 128, 3, None, 64, d, d, d, None) == \
+        _lib.TKV_EINVAL
+    a = _lib.DecodeArgs(q=d, k=d, v=d, k_scale=d, k_zero=d, v_scale=d, v_zero=d, out=d, acc=d,
+                        maxs=d, sums=d, B=1, HQ=8, HKV=2, S=64, D=128, k_nbits=4, v_nbits=4,
+                        group_size=32, sm_scale=0.1, split_size=64, num_splits=1, key_block=0)
+    # the channel entry needs key_block == 32 and a window
+    assert lib.tkv_channel_decode_attention(ctypes.byref(a), d, d, None, 32, None) == _lib.TKV_EINVAL
+    a.key_block = 32
+    assert lib.tkv_channel_decode_attention(ctypes.byref(a), None, d, None, 32, None) == \
+        _lib.TKV_EINVAL
+    a.key_block = 16
+    assert lib.tkv_fused_decode_split(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    # partials placement: the window's row must fit, the whole-attention entry owns all splits
+    a.key_block, a.split_base, a.num_splits_total = 0, 1, 1
+    assert lib.tkv_fused_decode_split(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    a.split_base, a.num_splits_total = 0, 2
+    assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    # per-channel keys need V groups of 16 or 32, and no paged cache
+    a.num_splits_total, a.key_block, a.group_size = 0, 32, 64
+    assert lib.tkv_fused_decode_split(ctypes.byref(a), None) == _lib.TKV_EUNSUPPORTED
+    a.group_size, a.page_size, a.block_table, a.block_table_stride, a.num_pages = 32, 32, d, 2, 4
+    assert lib.tkv_fused_decode_split(ctypes.byref(a), None) == _lib.TKV_EINVAL
