@@ -791,7 +791,9 @@ def qwen_e2e(ctxs=(8192, 32768), B=16, steps=8, seed=11):
     model (transformers, fp16 weights, 28 layers, HQ=12, HKV=2, D=128) at batch B
     with the cache pre-filled to ctx tokens of synthetic K/V: stock transformers
     (SDPA + DynamicCache, eager), the fp16 control kernel and the fused 4-bit
-    kernel (``tritonkv_amd.hf``, eager and as one captured HIP graph per step)."""
+    kernel (``tritonkv_amd.hf``, eager and as one captured HIP graph per step),
+    and 2-bit per-channel keys with an fp16 window (eager only: its lengths are
+    host-side)."""
     import torch
     from transformers import DynamicCache, Qwen2Config, Qwen2ForCausalLM
 
@@ -827,14 +829,15 @@ def qwen_e2e(ctxs=(8192, 32768), B=16, steps=8, seed=11):
     with torch.no_grad():
         for L in ctxs:
             row = {}
-            for name in ("stock_sdpa", "tkv_fp16", "tkv_4bit"):
+            for name in ("stock_sdpa", "tkv_fp16", "tkv_4bit", "tkv_2bit_channel"):
                 if name == "stock_sdpa":
                     model.set_attn_implementation("sdpa")
                     cache = DynamicCache(config=model.config)
                 else:
                     model.set_attn_implementation(hf.ATTN_NAME)
-                    cache = hf.TkvCache(model.config, capacity=L + 4 * steps + 8,
-                                        nbits=16 if name == "tkv_fp16" else 4)
+                    nb = {"tkv_fp16": 16, "tkv_4bit": 4, "tkv_2bit_channel": 2}[name]
+                    cache = hf.TkvCache(model.config, capacity=L + 4 * steps + 8, nbits=nb,
+                                        keys="channel" if name == "tkv_2bit_channel" else "token")
                 fill(cache, L)
                 ids = torch.zeros(B, 1, dtype=torch.long, device="cuda")
                 pos = torch.full((B, 1), L, dtype=torch.long, device="cuda")
@@ -846,7 +849,7 @@ def qwen_e2e(ctxs=(8192, 32768), B=16, steps=8, seed=11):
 
                 step()  # warm-up
                 entry = {"eager_us": round(timed(step, steps), 1)}
-                if name != "stock_sdpa":
+                if name not in ("stock_sdpa", "tkv_2bit_channel"):
                     try:
                         g = capture([step])
                         entry["graph_us"] = round(timed(g.replay, steps), 1)

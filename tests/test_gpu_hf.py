@@ -122,3 +122,26 @@ def test_generate_with_tkv_cache():
     out = model.generate(ids, past_key_values=cache, max_new_tokens=6, do_sample=False)
     assert out.shape == (1, 22)
     assert cache.get_seq_length() == 21  # the last generated token is never fed back
+
+
+def test_channel_keys_inside_the_model():
+    """keys="channel": per-channel keys plus an fp16 window; the window flushes
+    into the quantized history during decode (60-token prompt, 8 steps)."""
+    from tritonkv_amd import hf
+
+    hf.register()
+    model = _model()
+    model.set_attn_implementation(hf.ATTN_NAME)
+    ids = torch.randint(0, 512, (2, 60), generator=torch.Generator().manual_seed(4)).to(DEV)
+    cache16 = hf.TkvCache(model.config, capacity=128, nbits=16)
+    toks, ref = _run(model, cache16, ids)
+    cache = hf.TkvCache(model.config, capacity=128, nbits=4, keys="channel")
+    _, got = _run(model, cache, ids, forced=toks)
+    layer = cache.layers[0]
+    assert cache.get_seq_length() == 68
+    assert (layer.cc.quantized, layer.cc.window) == (64, 4)
+    assert cache.nbytes > 0
+    for a, b in zip(got, ref):
+        assert torch.isfinite(a).all()
+        cos = torch.nn.functional.cosine_similarity(a, b, dim=-1).min().item()
+        assert cos > 0.99, cos

@@ -54,3 +54,13 @@ def test_capacity_and_decode_errors_without_a_gpu():
             model(input_ids=ids[:, :1], past_key_values=cache, use_cache=True)
     with pytest.raises(ValueError, match="nbits"):
         hf.TkvLayer(16, nbits=8)
+
+
+def test_channel_key_mode_arguments():
+    from tritonkv_amd import hf
+
+    with pytest.raises(ValueError):
+        hf.TkvLayer(64, nbits=16, keys="channel")
+    with pytest.raises(ValueError):
+        hf.TkvLayer(64, nbits=4, keys="block")
+    assert hf.TkvLayer(64, nbits=2, keys="channel").key_format == "channel"

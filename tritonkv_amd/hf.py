@@ -12,7 +12,10 @@ fp16 SDPA and runs decode (``q_len == 1``) on the fused kernel.  Here:
   (the GPU quantize/pack append for 2/4 bits).  A decode step only advances
   the length: the new token's K/V reach the attention call, which appends them
   inside the split kernel (``k_new``/``v_new``), so a quantized decode step is
-  one launch per layer.
+  one launch per layer.  ``keys="channel"`` instead keeps per-channel
+  (KIVI-style) keys with an fp16 window (:class:`~tritonkv_amd.channel.ChannelKVCache`,
+  the key format of ``docs/future_work.md:229-293``); its lengths live on the
+  host, so those decode steps are not graph-capturable.
 * ``"tkv"`` -- the attention function (:func:`register`): SDPA over the prompt
   for prefill; for decode, :func:`~tritonkv_amd.kernels.fused_decode_attention`
   over the quantized cache, or the fp16 control
@@ -36,6 +39,7 @@ from __future__ import annotations
 import torch
 import torch.nn.functional as F
 
+from .channel import ChannelKVCache
 from .kernels import fp16_decode_attention, fused_decode_attention
 from .quantize import append_kv, empty_cache
 
@@ -55,21 +59,29 @@ class TkvLayer(_LayerBase):
     is_compileable = False
     is_sliding = False
 
-    def __init__(self, capacity: int, nbits: int = 4, group_size: int = 32):
+    def __init__(self, capacity: int, nbits: int = 4, group_size: int = 32, keys: str = "token"):
         if _LayerBase is not object:
             super().__init__()
         self.keys = self.values = None
         self.is_initialized = False
         if nbits not in (2, 4, 16):
             raise ValueError(f"nbits must be 2, 4 or 16, got {nbits}")
+        if keys not in ("token", "channel") or (keys == "channel" and nbits == 16):
+            raise ValueError(f"keys must be 'token' or (2/4 bits) 'channel', got {keys!r}")
         self.capacity, self.nbits, self.group_size = capacity, nbits, group_size
+        self.key_format = keys
         self.length = 0  # tokens held (the same for every row)
 
     # -- storage ---------------------------------------------------------------
     def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
         B, HKV, _, D = key_states.shape
         self.dtype, self.device = key_states.dtype, key_states.device
-        if self.nbits == 16:
+        if self.key_format == "channel":
+            self.cc = ChannelKVCache(B, HKV, self.capacity, D, k_nbits=self.nbits,
+                                     v_nbits=self.nbits, group_size=self.group_size,
+                                     device=self.device)
+            self.keys, self.values = self.cc.keys.packed, self.cc.values.packed
+        elif self.nbits == 16:
             self.kc = torch.zeros(B, HKV, self.capacity, D, dtype=torch.float16, device=self.device)
             self.vc = torch.zeros_like(self.kc)
             self.keys, self.values = self.kc, self.vc
@@ -101,7 +113,9 @@ class TkvLayer(_LayerBase):
             return key_states, value_states
         if self.length:
             raise NotImplementedError("prefill into a non-empty TkvCache (chunked prefill)")
-        if self.nbits == 16:
+        if self.key_format == "channel":
+            self.cc.extend(key_states, value_states)
+        elif self.nbits == 16:
             self.kc[:, :, :n] = key_states
             self.vc[:, :, :n] = value_states
         else:
@@ -125,6 +139,8 @@ class TkvLayer(_LayerBase):
         self.length = 0
         if self.is_initialized:
             self.lens.zero_()
+            if self.key_format == "channel":
+                self.cc.quantized = self.cc.window = 0
 
     def decode(self, module, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                scaling: float) -> torch.Tensor:
@@ -133,7 +149,10 @@ class TkvLayer(_LayerBase):
         if self.out is None:
             self.out = torch.empty(B, HQ, D, dtype=torch.float32, device=query.device)
         q = query[:, :, 0].to(torch.float16)
-        if self.nbits == 16:
+        if self.key_format == "channel":
+            self.cc.extend(key, value)
+            out = self.cc.attend(q, sm_scale=scaling, out=self.out)
+        elif self.nbits == 16:
             pos = (self.lens[:1] - 1).long()  # all rows share one length
             self.kc.index_copy_(2, pos, key.to(torch.float16))
             self.vc.index_copy_(2, pos, value.to(torch.float16))
@@ -150,9 +169,10 @@ class TkvLayer(_LayerBase):
 class TkvCache(_Cache):
     """A ``transformers`` cache of :class:`TkvLayer`, one per decoder layer."""
 
-    def __init__(self, config, capacity: int, nbits: int = 4, group_size: int = 32):
+    def __init__(self, config, capacity: int, nbits: int = 4, group_size: int = 32,
+                 keys: str = "token"):
         cfg = config.get_text_config() if hasattr(config, "get_text_config") else config
-        layers = [TkvLayer(capacity, nbits, group_size) for _ in range(cfg.num_hidden_layers)]
+        layers = [TkvLayer(capacity, nbits, group_size, keys) for _ in range(cfg.num_hidden_layers)]
         super().__init__(layers=layers)
 
     @property
@@ -160,7 +180,9 @@ class TkvCache(_Cache):
         """Device bytes held by the caches of all layers."""
         total = 0
         for layer in self.layers:
-            if layer.is_initialized:
+            if layer.is_initialized and layer.key_format == "channel":
+                total += layer.cc.nbytes()
+            elif layer.is_initialized:
                 cs = (layer.kc, layer.vc)
                 if layer.nbits == 16:
                     total += sum(c.numel() * c.element_size() for c in cs)
