@@ -792,8 +792,7 @@ def qwen_e2e(ctxs=(8192, 32768), B=16, steps=8, seed=11):
     with the cache pre-filled to ctx tokens of synthetic K/V: stock transformers
     (SDPA + DynamicCache, eager), the fp16 control kernel and the fused 4-bit
     kernel (``tritonkv_amd.hf``, eager and as one captured HIP graph per step),
-    and 2-bit per-channel keys with an fp16 window (eager only: its lengths are
-    host-side)."""
+    and 2-bit per-channel keys with an fp16 window (the same two ways)."""
     import torch
     from transformers import DynamicCache, Qwen2Config, Qwen2ForCausalLM
 
@@ -849,7 +848,7 @@ def qwen_e2e(ctxs=(8192, 32768), B=16, steps=8, seed=11):
 
                 step()  # warm-up
                 entry = {"eager_us": round(timed(step, steps), 1)}
-                if name not in ("stock_sdpa", "tkv_2bit_channel"):
+                if name != "stock_sdpa":
                     try:
                         g = capture([step])
                         entry["graph_us"] = round(timed(g.replay, steps), 1)

@@ -195,3 +195,58 @@ def test_channel_kv_cache_prefill_and_decode_steps():
         assert_close_to_reference(got, ref, f"cache step {s} (n={n})")
         checked += 1
     assert checked == 4 and len(cache) == n0 + steps
+
+
+def test_channel_kv_cache_step_replays_in_a_graph():
+    """``step`` (append to the window, attend, flush a full window) captured
+    once and replayed across two window flushes: every replay equals an eager
+    twin's step bit for bit, and matches the oracle on the step's partition of
+    the history (quantized blocks, then the window including the new token)."""
+    from tritonkv_amd.channel import ChannelKVCache
+
+    B, HQ, HKV, D = 2, 8, 2, 128
+    g = torch.Generator().manual_seed(12)
+    n0, steps = 70, 60
+    k = torch.randn(B, HKV, n0 + steps, D, generator=g).half()
+    v = torch.randn(B, HKV, n0 + steps, D, generator=g).half()
+    q = torch.randn(B, HQ, D, generator=g).half().to(DEV)
+    caches = [ChannelKVCache(B, HKV, 256, D, k_nbits=4, v_nbits=2, group_size=32, device=DEV)
+              for _ in range(2)]
+    for c in caches:
+        c.extend(k[:, :, :n0].to(DEV), v[:, :, :n0].to(DEV))
+    eager, graphed = caches
+    kb = torch.empty(B, HKV, 1, D, dtype=torch.float16, device=DEV)
+    vb = torch.empty_like(kb)
+    out = torch.empty(B, HQ, D, device=DEV)
+    for c in caches:  # the first step eagerly on both (allocates the workspace)
+        c.step(k[:, :, n0:n0 + 1].to(DEV), v[:, :, n0:n0 + 1].to(DEV), q, out=out)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        graphed.step(kb, vb, q, out=out)
+    checked = 0
+    for s in range(1, steps):
+        t = n0 + s
+        kb.copy_(k[:, :, t:t + 1].to(DEV))
+        vb.copy_(v[:, :, t:t + 1].to(DEV))
+        graph.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        want = eager.step(k[:, :, t:t + 1].to(DEV), v[:, :, t:t + 1].to(DEV), q)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), s
+        n = t + 1
+        if s in (1, 25, 26, 58):   # around the flushes at 96 and 128 tokens
+            nq = ((n - 1) // 32) * 32
+            ckn = och.quantize_keys_per_channel(k[:, :, :nq].numpy(), 4)
+            vqn = oq.quantize_groupwise(v[:, :, :nq].numpy(), 2, 32)
+            kh = np.concatenate([och.dequantize_keys_per_channel(ckn),
+                                 k[:, :, nq:n].float().numpy()], axis=2)
+            vh = np.concatenate([oq.dequantize_groupwise(vqn), v[:, :, nq:n].float().numpy()],
+                                axis=2)
+            ref = oatt.reference_decode_attention(q.float().cpu().numpy(), kh, vh)
+            assert_close_to_reference(got, ref, f"graph step {s} (n={n})")
+            checked += 1
+    assert checked == 4
+    assert torch.equal(graphed.keys.packed, eager.keys.packed)
+    assert torch.equal(graphed.values.scale, eager.values.scale)

@@ -197,12 +197,18 @@ def channel_decode_attention(
 class ChannelKVCache:
     """One layer's cache: per-channel keys, per-token values, fp16 window.
 
-    All batch rows hold the same number of tokens.  Every 32 tokens the window
-    is quantized into the history (keys per channel, values per token) and
-    emptied.  ``append`` and ``attend`` allocate nothing once the workspace
-    exists; the host-side lengths make a step's launches depend on the step
-    index, so a graph of one step is valid only for that window fill.
+    All batch rows hold the same number of tokens.  ``extend`` appends any
+    number of tokens from the host (prefill): whole blocks go straight into the
+    history, the rest into the window, which is quantized into the history
+    whenever it holds 32 tokens.  ``step`` is one decode step -- append one
+    token to the window, attend, quantize the window if it is now full -- with
+    the lengths and the flush decision kept on the device, so it allocates no
+    host-dependent state and a captured step stays right when its graph is
+    replayed for any window fill.  The host-side counters (``quantized``,
+    ``window``) follow eager calls only.
     """
+
+    _NEVER = -(1 << 30)  # a position no block is written at
 
     def __init__(self, B: int, HKV: int, capacity: int, D: int, k_nbits: int = 2,
                  v_nbits: int = 2, group_size: int = 32, device="cuda"):
@@ -220,6 +226,7 @@ class ChannelKVCache:
         self._pos = torch.zeros(B, dtype=torch.int32, device=device)
         self._qlens = torch.zeros(B, dtype=torch.int32, device=device)
         self._rlens = torch.zeros(B, dtype=torch.int32, device=device)
+        self._never = torch.full((B,), self._NEVER, dtype=torch.int32, device=device)
         self.workspace: dict = {}
 
     def __len__(self) -> int:
@@ -236,7 +243,7 @@ class ChannelKVCache:
         self.window = 0
 
     def extend(self, k: torch.Tensor, v: torch.Tensor) -> None:
-        """Append ``(B, HKV, N, D)`` keys and values (prefill or decode)."""
+        """Append ``(B, HKV, N, D)`` keys and values from the host (prefill)."""
         if k.dtype != torch.float16:
             k = k.to(torch.float16)
         if v.dtype != torch.float16:
@@ -260,15 +267,39 @@ class ChannelKVCache:
             i += take
             if self.window == BLOCK:
                 self._flush()
+        self._qlens.fill_(self.quantized)
+        self._rlens.fill_(self.window)
 
     def attend(self, q: torch.Tensor, sm_scale: float | None = None,
                out: torch.Tensor | None = None) -> torch.Tensor:
         """Attention of ``q`` ``(B, HQ, D)`` over everything appended so far."""
-        self._qlens.fill_(self.quantized)
-        self._rlens.fill_(self.window)
         return channel_decode_attention(q, self.keys, self.values, self.k_res, self.v_res,
                                         q_lens=self._qlens, res_lens=self._rlens,
                                         sm_scale=sm_scale, out=out, _workspace=self.workspace)
+
+    def step(self, k: torch.Tensor, v: torch.Tensor, q: torch.Tensor,
+             sm_scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+        """One decode step: append ``k``/``v`` ``(B, HKV, 1, D)`` to the window,
+        attend with ``q`` ``(B, HQ, D)``, then quantize the window into the
+        history if it is full.  Device-side lengths only (graph-capturable)."""
+        if len(self) + 1 > self.capacity:
+            raise ValueError(f"cache capacity {self.capacity} exceeded")
+        idx = self._rlens[:1].long()          # every row has the same fill
+        self.k_res.index_copy_(2, idx, k.to(torch.float16))
+        self.v_res.index_copy_(2, idx, v.to(torch.float16))
+        self._rlens.add_(1)
+        out = self.attend(q, sm_scale=sm_scale, out=out)
+        full = self._rlens == BLOCK
+        torch.where(full, self._qlens, self._never, out=self._pos)  # elsewhere: nothing written
+        append_keys_per_channel(self.keys, self.k_res, self._pos)
+        append_kv(self.values, self.v_res, self._pos)
+        self._qlens.add_(full.to(torch.int32) * BLOCK)
+        self._rlens.masked_fill_(full, 0)
+        self.window += 1
+        if self.window == BLOCK:
+            self.quantized += BLOCK
+            self.window = 0
+        return out
 
 
 __all__ = ["BLOCK", "ChannelQuantizedKeys", "empty_channel_keys", "append_keys_per_channel",

@@ -14,8 +14,9 @@ fp16 SDPA and runs decode (``q_len == 1``) on the fused kernel.  Here:
   inside the split kernel (``k_new``/``v_new``), so a quantized decode step is
   one launch per layer.  ``keys="channel"`` instead keeps per-channel
   (KIVI-style) keys with an fp16 window (:class:`~tritonkv_amd.channel.ChannelKVCache`,
-  the key format of ``docs/future_work.md:229-293``); its lengths live on the
-  host, so those decode steps are not graph-capturable.
+  the key format of ``docs/future_work.md:229-293``); its decode step keeps
+  the window fill and the flush decision on the device, so it is
+  graph-capturable too.
 * ``"tkv"`` -- the attention function (:func:`register`): SDPA over the prompt
   for prefill; for decode, :func:`~tritonkv_amd.kernels.fused_decode_attention`
   over the quantized cache, or the fp16 control
@@ -150,8 +151,7 @@ class TkvLayer(_LayerBase):
             self.out = torch.empty(B, HQ, D, dtype=torch.float32, device=query.device)
         q = query[:, :, 0].to(torch.float16)
         if self.key_format == "channel":
-            self.cc.extend(key, value)
-            out = self.cc.attend(q, sm_scale=scaling, out=self.out)
+            out = self.cc.step(key, value, q, sm_scale=scaling, out=self.out)
         elif self.nbits == 16:
             pos = (self.lens[:1] - 1).long()  # all rows share one length
             self.kc.index_copy_(2, pos, key.to(torch.float16))
