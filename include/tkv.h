@@ -188,6 +188,31 @@ int tkv_quantize_keys_channel(const void *x, int32_t x_is_fp32, int32_t B, int32
                               int32_t S_cap, uint8_t *packed, uint16_t *scale, uint16_t *zero,
                               tkv_stream_t stream);
 
+/* The fp16 window of per-channel keys, as two launches per decode step that
+ * keep every length on the device (so a captured step replays correctly for
+ * any window fill).  k_res / v_res: fp16 (B, HKV, res_cap, D) with res_cap
+ * == 32; res_lens / q_lens: int32 (B,) window fills and quantized lengths.
+ *
+ * tkv_channel_window_append: token (B, HKV, D) fp16 of k_new / v_new goes to
+ * window row res_lens[b], which then grows by one (a full window is left
+ * unchanged: flush it first).
+ *
+ * tkv_channel_window_flush: for each row whose window holds 32 tokens, the
+ * window is quantized into the history at token q_lens[b] -- keys per channel
+ * exactly as tkv_quantize_keys_channel, values per token exactly as
+ * tkv_quantize_pack (V group_size 16 or 32) -- then q_lens[b] += 32 and
+ * res_lens[b] = 0.  Other rows are untouched.  No counterpart in the
+ * reference (it plans the format, docs/future_work.md:229-293). */
+int tkv_channel_window_append(const void *k_new, const void *v_new, int32_t B, int32_t HKV,
+                              int32_t D, void *k_res, void *v_res, int32_t res_cap,
+                              int32_t *res_lens, tkv_stream_t stream);
+int tkv_channel_window_flush(const void *k_res, const void *v_res, int32_t B, int32_t HKV,
+                             int32_t D, int32_t k_nbits, int32_t v_nbits, int32_t group_size,
+                             int32_t res_cap, int32_t *q_lens, int32_t *res_lens, int32_t S_cap,
+                             uint8_t *k_packed, uint16_t *k_scale, uint16_t *k_zero,
+                             uint8_t *v_packed, uint16_t *v_scale, uint16_t *v_zero,
+                             tkv_stream_t stream);
+
 /* Split-P pack of uint8 codes (rows, D) -> (rows, D/P), as pack_codes
  * (quantize.py:149-169). */
 int tkv_pack_codes(const uint8_t *codes, int64_t rows, int32_t D, int32_t nbits,
@@ -224,7 +249,8 @@ const char *tkv_status_string(int status);
 /* ABI version of this library (bumped on any incompatible change; 3 added the
  * paged-cache fields of tkv_decode_args and tkv_paged_quantize_pack, 4 the
  * fused-append fields, 5 the per-channel key and partials-placement fields,
- * tkv_quantize_keys_channel and tkv_channel_decode_attention). */
+ * tkv_quantize_keys_channel, tkv_channel_decode_attention and the
+ * tkv_channel_window_* calls). */
 int tkv_abi_version(void);
 
 #ifdef __cplusplus

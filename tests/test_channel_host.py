@@ -70,3 +70,26 @@ def test_channel_c_entry_points_reject_bad_arguments_without_a_gpu():
     assert lib.tkv_fused_decode_split(ctypes.byref(a), None) == _lib.TKV_EUNSUPPORTED
     a.group_size, a.page_size, a.block_table, a.block_table_stride, a.num_pages = 32, 32, d, 2, 4
     assert lib.tkv_fused_decode_split(ctypes.byref(a), None) == _lib.TKV_EINVAL
+
+
+def test_channel_window_entry_points_reject_bad_arguments_without_a_gpu():
+    from tritonkv_amd import _lib
+
+    lib = _lib.load()
+    d, lens = 0x1000, 0x2000
+    # window capacity must be 32, D 64 or 128, pointers 16-byte aligned
+    assert lib.tkv_channel_window_append(d, d, 2, 2, 128, d, d, 16, lens, None) == _lib.TKV_EINVAL
+    assert lib.tkv_channel_window_append(d, d, 2, 2, 96, d, d, 32, lens, None) == _lib.TKV_EINVAL
+    assert lib.tkv_channel_window_append(d + 2, d, 2, 2, 128, d, d, 32, lens, None) == \
+        _lib.TKV_EINVAL
+    assert lib.tkv_channel_window_append(d, d, 2, 2, 128, d, d, 32, None, None) == _lib.TKV_EINVAL
+    args = [d, d, 2, 2, 128, 4, 2, 32, 32, lens, lens, 256, d, d, d, d, d, d, None]
+    bad_cap = list(args)
+    bad_cap[11] = 250
+    assert lib.tkv_channel_window_flush(*bad_cap) == _lib.TKV_EINVAL
+    bad_bits = list(args)
+    bad_bits[5] = 3
+    assert lib.tkv_channel_window_flush(*bad_bits) == _lib.TKV_EINVAL
+    bad_gs = list(args)
+    bad_gs[7] = 64
+    assert lib.tkv_channel_window_flush(*bad_gs) == _lib.TKV_EUNSUPPORTED

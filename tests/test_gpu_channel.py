@@ -248,5 +248,15 @@ def test_channel_kv_cache_step_replays_in_a_graph():
             assert_close_to_reference(got, ref, f"graph step {s} (n={n})")
             checked += 1
     assert checked == 4
-    assert torch.equal(graphed.keys.packed, eager.keys.packed)
-    assert torch.equal(graphed.values.scale, eager.values.scale)
+    for a, b in ((graphed.keys, eager.keys), (graphed.values, eager.values)):
+        assert torch.equal(a.packed, b.packed) and torch.equal(a.scale, b.scale)
+    # the flushes quantized exactly what the host path quantizes
+    nq = int(graphed._qlens[0])
+    assert nq == ((n0 + steps) // 32) * 32
+    ref = ChannelKVCache(B, HKV, 256, D, k_nbits=4, v_nbits=2, group_size=32, device=DEV)
+    ref.extend(k[:, :, :nq].to(DEV), v[:, :, :nq].to(DEV))
+    assert torch.equal(graphed.keys.packed[:, :, :nq], ref.keys.packed[:, :, :nq])
+    assert torch.equal(graphed.keys.scale[:, :, :nq // 32], ref.keys.scale[:, :, :nq // 32])
+    assert torch.equal(graphed.keys.zero[:, :, :nq // 32], ref.keys.zero[:, :, :nq // 32])
+    assert torch.equal(graphed.values.packed[:, :, :nq], ref.values.packed[:, :, :nq])
+    assert torch.equal(graphed.values.zero[:, :, :nq], ref.values.zero[:, :, :nq])

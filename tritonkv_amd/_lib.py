@@ -100,6 +100,9 @@ SIGNATURES = {
                                    _P], ctypes.c_int),
     "tkv_channel_decode_attention": ([ctypes.POINTER(DecodeArgs), _P, _P, _P, _I32, _P],
                                      ctypes.c_int),
+    "tkv_channel_window_append": ([_P, _P, _I32, _I32, _I32, _P, _P, _I32, _P, _P], ctypes.c_int),
+    "tkv_channel_window_flush": ([_P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P, _I32,
+                                  _P, _P, _P, _P, _P, _P, _P], ctypes.c_int),
     "tkv_pack_codes": ([_P, _I64, _I32, _I32, _P, _P], ctypes.c_int),
     "tkv_unpack_dequant": ([_P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P], ctypes.c_int),
     "tkv_device_info": ([ctypes.POINTER(DeviceInfo)], ctypes.c_int),

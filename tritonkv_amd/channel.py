@@ -208,8 +208,6 @@ class ChannelKVCache:
     ``window``) follow eager calls only.
     """
 
-    _NEVER = -(1 << 30)  # a position no block is written at
-
     def __init__(self, B: int, HKV: int, capacity: int, D: int, k_nbits: int = 2,
                  v_nbits: int = 2, group_size: int = 32, device="cuda"):
         cap = -(-capacity // BLOCK) * BLOCK
@@ -226,7 +224,6 @@ class ChannelKVCache:
         self._pos = torch.zeros(B, dtype=torch.int32, device=device)
         self._qlens = torch.zeros(B, dtype=torch.int32, device=device)
         self._rlens = torch.zeros(B, dtype=torch.int32, device=device)
-        self._never = torch.full((B,), self._NEVER, dtype=torch.int32, device=device)
         self.workspace: dict = {}
 
     def __len__(self) -> int:
@@ -281,20 +278,30 @@ class ChannelKVCache:
              sm_scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
         """One decode step: append ``k``/``v`` ``(B, HKV, 1, D)`` to the window,
         attend with ``q`` ``(B, HQ, D)``, then quantize the window into the
-        history if it is full.  Device-side lengths only (graph-capturable)."""
+        history if it is full.  Three kinds of launches (window append,
+        attention, window flush), device-side lengths only: graph-capturable."""
         if len(self) + 1 > self.capacity:
             raise ValueError(f"cache capacity {self.capacity} exceeded")
-        idx = self._rlens[:1].long()          # every row has the same fill
-        self.k_res.index_copy_(2, idx, k.to(torch.float16))
-        self.v_res.index_copy_(2, idx, v.to(torch.float16))
-        self._rlens.add_(1)
+        B, HKV, _, D = self.k_res.shape
+        kk = k.to(torch.float16).contiguous()
+        vv = v.to(torch.float16).contiguous()
+        if kk.numel() != B * HKV * D or vv.numel() != B * HKV * D:
+            raise ValueError(f"k / v must hold one (B, HKV, D) token, got {tuple(k.shape)}")
+        lib, st = _lib.load(), _lib.stream_handle(self.k_res.device)
+        with torch.cuda.device(self.k_res.device):
+            rc = lib.tkv_channel_window_append(kk.data_ptr(), vv.data_ptr(), B, HKV, D,
+                                               self.k_res.data_ptr(), self.v_res.data_ptr(), BLOCK,
+                                               self._rlens.data_ptr(), st)
+            _lib.check(rc, "ChannelKVCache.step (window append)")
         out = self.attend(q, sm_scale=sm_scale, out=out)
-        full = self._rlens == BLOCK
-        torch.where(full, self._qlens, self._never, out=self._pos)  # elsewhere: nothing written
-        append_keys_per_channel(self.keys, self.k_res, self._pos)
-        append_kv(self.values, self.v_res, self._pos)
-        self._qlens.add_(full.to(torch.int32) * BLOCK)
-        self._rlens.masked_fill_(full, 0)
+        ks, vs = self.keys, self.values
+        with torch.cuda.device(self.k_res.device):
+            rc = lib.tkv_channel_window_flush(
+                self.k_res.data_ptr(), self.v_res.data_ptr(), B, HKV, D, ks.nbits, vs.nbits,
+                vs.group_size, BLOCK, self._qlens.data_ptr(), self._rlens.data_ptr(),
+                self.capacity, ks.packed.data_ptr(), ks.scale.data_ptr(), ks.zero.data_ptr(),
+                vs.packed.data_ptr(), vs.scale.data_ptr(), vs.zero.data_ptr(), st)
+            _lib.check(rc, "ChannelKVCache.step (window flush)")
         self.window += 1
         if self.window == BLOCK:
             self.quantized += BLOCK

@@ -215,39 +215,32 @@ quantize_pack_wide_kernel(const void* __restrict__ x, int rows, int HKV, int N,
   }
 }
 
-// Per-channel (KIVI-style) keys: one wave per block of 32 tokens of one
-// (b, kv head).  Every channel of the block is one group of 32 values
+// Per-channel (KIVI-style) keys.  One wave quantizes one block of 32 tokens
+// of one (b, kv head): every channel of the block is one group of 32 values
 // (min/max, fp16 scale and zero, codes), the group-wise arithmetic of
 // quantize_row applied along the token axis.  Lane j owns byte column j of
 // the block's rows, i.e. channels j + p*DP (p < P), so the min/max need no
 // cross-lane step and the lane packs each token's byte j itself.  Lanes >= DP
-// repeat lanes j - DP and store nothing.  A block whose destination does not
-// start on a 32-token boundary, or does not fit [0, S_cap), is not written.
+// repeat lanes j - DP and store nothing.
+//   src: element index of the block's first row in x (rows D apart);
+//   dst_row: the block's first destination row in packed;
+//   meta: element index of the block's scale / zero row (D values).
 template <int D, int NB, bool F32>
-__global__ void __launch_bounds__(256)
-quantize_keys_channel_kernel(const void* __restrict__ x, int64_t blocks, int HKV, int NBLK,
-                             const int32_t* __restrict__ positions, int S_cap,
-                             uint8_t* __restrict__ packed, uint16_t* __restrict__ scale,
-                             uint16_t* __restrict__ zero) {
+__device__ __forceinline__ void quantize_key_block(const void* __restrict__ x, int64_t src, int lane,
+                                                   bool ok, uint8_t* __restrict__ packed,
+                                                   int64_t dst_row, uint16_t* __restrict__ scale,
+                                                   uint16_t* __restrict__ zero, int64_t meta) {
   constexpr int P = 8 / NB, DP = D / P, QMAX = (1 << NB) - 1, T = 32;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int64_t blk = (int64_t)blockIdx.x * 4 + w;
-  if (blk >= blocks) return;  // whole wave
   const int j = lane % DP;
-  const int64_t bh = blk / NBLK;
-  const int tb = (int)(blk - bh * NBLK);
-  const int b = (int)(bh / HKV);
-  const int64_t src0 = (bh * NBLK + tb) * T;  // first source row
+  ok = ok && lane < DP;
   float v[P][T];
 #pragma unroll
   for (int t = 0; t < T; ++t)
 #pragma unroll
     for (int p = 0; p < P; ++p) {
-      const int64_t e = (src0 + t) * D + j + p * DP;
+      const int64_t e = src + (int64_t)t * D + j + p * DP;
       v[p][t] = F32 ? static_cast<const float*>(x)[e] : (float)static_cast<const _Float16*>(x)[e];
     }
-  const int64_t dst_t = (int64_t)(positions ? positions[b] : 0) + (int64_t)tb * T;
-  const bool ok = dst_t >= 0 && dst_t % T == 0 && dst_t + T <= S_cap && lane < DP;
   uint32_t bytes[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) bytes[t] = 0;
@@ -272,14 +265,103 @@ quantize_keys_channel_kernel(const void* __restrict__ x, int64_t blocks, int HKV
       bytes[t] |= (uint32_t)c << (p * NB);
     }
     if (ok) {
-      const int64_t m = (bh * (S_cap / T) + dst_t / T) * D + j + p * DP;
-      scale[m] = __builtin_bit_cast(uint16_t, s16);
-      zero[m] = __builtin_bit_cast(uint16_t, z16);
+      scale[meta + j + p * DP] = __builtin_bit_cast(uint16_t, s16);
+      zero[meta + j + p * DP] = __builtin_bit_cast(uint16_t, z16);
     }
   }
   if (!ok) return;
 #pragma unroll
-  for (int t = 0; t < T; ++t) packed[(bh * S_cap + dst_t + t) * DP + j] = (uint8_t)bytes[t];
+  for (int t = 0; t < T; ++t) packed[(dst_row + t) * DP + j] = (uint8_t)bytes[t];
+}
+
+// One wave per block of 32 tokens of one (b, kv head).  A block whose
+// destination does not start on a 32-token boundary, or does not fit
+// [0, S_cap), is not written.
+template <int D, int NB, bool F32>
+__global__ void __launch_bounds__(256)
+quantize_keys_channel_kernel(const void* __restrict__ x, int64_t blocks, int HKV, int NBLK,
+                             const int32_t* __restrict__ positions, int S_cap,
+                             uint8_t* __restrict__ packed, uint16_t* __restrict__ scale,
+                             uint16_t* __restrict__ zero) {
+  constexpr int T = 32;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int64_t blk = (int64_t)blockIdx.x * 4 + w;
+  if (blk >= blocks) return;  // whole wave
+  const int64_t bh = blk / NBLK;
+  const int tb = (int)(blk - bh * NBLK);
+  const int b = (int)(bh / HKV);
+  const int64_t dst_t = (int64_t)(positions ? positions[b] : 0) + (int64_t)tb * T;
+  const bool ok = dst_t >= 0 && dst_t % T == 0 && dst_t + T <= S_cap;
+  quantize_key_block<D, NB, F32>(x, (bh * NBLK + tb) * T * D, lane, ok, packed, bh * S_cap + dst_t,
+                                 scale, zero, (bh * (S_cap / T) + dst_t / T) * D);
+}
+
+// The fp16 window of per-channel keys: K and V windows (B, HKV, 32, D), row b
+// holding res_lens[b] tokens after q_lens[b] quantized ones.
+//
+// Append: one workgroup per batch row writes the new token of every kv head
+// at window row res_lens[b] (if it is below 32) and then advances res_lens[b].
+__global__ void __launch_bounds__(256)
+channel_window_append_kernel(const uint16_t* __restrict__ k_new, const uint16_t* __restrict__ v_new,
+                             int HKV, int D, uint16_t* __restrict__ k_res,
+                             uint16_t* __restrict__ v_res, int32_t* __restrict__ res_lens) {
+  constexpr int T = 32;
+  const int b = blockIdx.x;
+  const int r = res_lens[b];
+  if (r < 0 || r >= T) return;  // whole workgroup: a full window must be flushed first
+  const int n = HKV * D / 8;    // 16-byte vectors per token and tensor
+  for (int i = threadIdx.x; i < 2 * n; i += blockDim.x) {
+    const int which = i / n, e = (i % n) * 8, kv = e / D, d = e % D;
+    const uint16_t* src = (which ? v_new : k_new) + (int64_t)b * HKV * D + e;
+    uint16_t* dst = (which ? v_res : k_res) + (((int64_t)b * HKV + kv) * T + r) * D + d;
+    *reinterpret_cast<u4*>(dst) = *reinterpret_cast<const u4*>(src);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) res_lens[b] = r + 1;
+}
+
+// Flush: one workgroup per batch row; if its window holds 32 tokens, wave w
+// quantizes the blocks of kv heads w, w + 4, ...: keys per channel
+// (quantize_key_block), values per token (quantize_row, as the append kernel)
+// into the history at q_lens[b]; then q_lens[b] += 32 and res_lens[b] = 0.
+// A block that does not fit [0, S_cap) is not written (the lengths still move).
+template <int D, int KNB, int VNB, int GS>
+__global__ void __launch_bounds__(256)
+channel_window_flush_kernel(const uint16_t* __restrict__ k_res, const uint16_t* __restrict__ v_res,
+                            int HKV, int S_cap, int32_t* __restrict__ q_lens,
+                            int32_t* __restrict__ res_lens, uint8_t* __restrict__ kp,
+                            uint16_t* __restrict__ ks, uint16_t* __restrict__ kz,
+                            uint8_t* __restrict__ vp, uint16_t* __restrict__ vs,
+                            uint16_t* __restrict__ vz) {
+  using R = RowQuant<D, VNB, GS>;
+  constexpr int T = 32, VDP = R::DP, VNG = R::NG;
+  const int b = blockIdx.x;
+  if (res_lens[b] != T) return;  // whole workgroup
+  const int q = q_lens[b];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const bool ok = q >= 0 && q % T == 0 && q + T <= S_cap;
+  for (int kv = w; kv < HKV; kv += 4) {
+    const int64_t bh = (int64_t)b * HKV + kv;
+    quantize_key_block<D, KNB, false>(k_res, bh * T * D, lane, ok, kp, bh * S_cap + q, ks, kz,
+                                      (bh * (S_cap / T) + q / T) * D);
+    for (int t = 0; t < T; ++t) {
+      float x[R::P];
+      load_row_for_quant<D, VNB>(v_res + (bh * T + t) * D, false, lane, x);
+      const R r = quantize_row<D, VNB, GS>(x, lane);
+      if (!ok) continue;
+      const int64_t row = bh * S_cap + q + t;
+      if (lane < VDP) vp[row * VDP + lane] = (uint8_t)r.byte;
+      if (lane < VNG) {
+        vs[row * VNG + lane] = (uint16_t)(r.meta & 0xFFFFu);
+        vz[row * VNG + lane] = (uint16_t)(r.meta >> 16);
+      }
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    q_lens[b] = q + T;
+    res_lens[b] = 0;
+  }
 }
 
 // One thread per packed dword.
@@ -564,6 +646,71 @@ extern "C" int tkv_quantize_keys_channel(const void* x, int32_t x_is_fp32, int32
     return TKV_EUNSUPPORTED;
   }
 #undef TKV_KC
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? TKV_OK : (int)e;
+}
+
+extern "C" int tkv_channel_window_append(const void* k_new, const void* v_new, int32_t B,
+                                         int32_t HKV, int32_t D, void* k_res, void* v_res,
+                                         int32_t res_cap, int32_t* res_lens, tkv_stream_t stream) {
+  using namespace tkv;
+  if (!k_new || !v_new || !k_res || !v_res || !res_lens) return TKV_EINVAL;
+  if (B <= 0 || HKV <= 0 || (D != 64 && D != 128)) return TKV_EINVAL;
+  if (res_cap != 32) return TKV_EINVAL;
+  if (((uintptr_t)k_new | (uintptr_t)v_new | (uintptr_t)k_res | (uintptr_t)v_res) & 15)
+    return TKV_EINVAL;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  (void)hipGetLastError();
+  channel_window_append_kernel<<<dim3((unsigned)B), 256, 0, st>>>(
+      static_cast<const uint16_t*>(k_new), static_cast<const uint16_t*>(v_new), HKV, D,
+      static_cast<uint16_t*>(k_res), static_cast<uint16_t*>(v_res), res_lens);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? TKV_OK : (int)e;
+}
+
+extern "C" int tkv_channel_window_flush(const void* k_res, const void* v_res, int32_t B,
+                                        int32_t HKV, int32_t D, int32_t k_nbits, int32_t v_nbits,
+                                        int32_t group_size, int32_t res_cap, int32_t* q_lens,
+                                        int32_t* res_lens, int32_t S_cap, uint8_t* k_packed,
+                                        uint16_t* k_scale, uint16_t* k_zero, uint8_t* v_packed,
+                                        uint16_t* v_scale, uint16_t* v_zero, tkv_stream_t stream) {
+  using namespace tkv;
+  if (!k_res || !v_res || !q_lens || !res_lens || !k_packed || !k_scale || !k_zero || !v_packed ||
+      !v_scale || !v_zero)
+    return TKV_EINVAL;
+  if (B <= 0 || HKV <= 0 || S_cap <= 0 || S_cap % 32 || res_cap != 32) return TKV_EINVAL;
+  if ((k_nbits != 2 && k_nbits != 4) || (v_nbits != 2 && v_nbits != 4)) return TKV_EINVAL;
+  if (((uintptr_t)k_res | (uintptr_t)v_res) & 1) return TKV_EINVAL;
+  if ((((uintptr_t)k_scale | (uintptr_t)k_zero | (uintptr_t)v_scale | (uintptr_t)v_zero) & 1))
+    return TKV_EINVAL;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)B);
+  const uint16_t* kr = static_cast<const uint16_t*>(k_res);
+  const uint16_t* vr = static_cast<const uint16_t*>(v_res);
+  (void)hipGetLastError();
+#define TKV_FL(Dv, KB, VB, GSv)                                                                  \
+  channel_window_flush_kernel<Dv, KB, VB, GSv><<<grid, 256, 0, st>>>(                            \
+      kr, vr, HKV, S_cap, q_lens, res_lens, k_packed, k_scale, k_zero, v_packed, v_scale, v_zero)
+#define TKV_FL_GS(Dv, KB, VB)                                                                    \
+  do {                                                                                           \
+    if (group_size == 16) TKV_FL(Dv, KB, VB, 16);                                                \
+    else if (group_size == 32) TKV_FL(Dv, KB, VB, 32);                                           \
+    else return TKV_EUNSUPPORTED;                                                                \
+  } while (0)
+#define TKV_FL_V(Dv, KB)                                                                         \
+  do {                                                                                           \
+    if (v_nbits == 4) TKV_FL_GS(Dv, KB, 4); else TKV_FL_GS(Dv, KB, 2);                          \
+  } while (0)
+  if (D == 128) {
+    if (k_nbits == 4) TKV_FL_V(128, 4); else TKV_FL_V(128, 2);
+  } else if (D == 64) {
+    if (k_nbits == 4) TKV_FL_V(64, 4); else TKV_FL_V(64, 2);
+  } else {
+    return TKV_EUNSUPPORTED;
+  }
+#undef TKV_FL_V
+#undef TKV_FL_GS
+#undef TKV_FL
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? TKV_OK : (int)e;
 }
