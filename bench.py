@@ -63,6 +63,8 @@ def _args():
     ap.add_argument("--kernel", default="quant_split_kernel<128, 4, 4, 32",
                     help="kernel-name substring the summary and traffic figures are for")
     ap.add_argument("--command", default="", help="command line recorded in the summary")
+    ap.add_argument("--title", default="", help="first line of the summary (default: the headline)")
+    ap.add_argument("--rows", type=int, default=8, help="kernels listed in the summary")
     ap.add_argument("--regime-probe", choices=("hot", "cold"), default=None,
                     help="no timing: 60 eager Qwen2.5-1.5B ctx-16384 4-bit decode calls on one "
                          "cache (hot) or rotating copies >= 768 MB (cold), for rocprofv3 --pmc")
@@ -369,7 +371,7 @@ def _counter_per_dispatch(directory, kernel):
 
 def rocprof_summary(a) -> int:
     out = []
-    out.append(f"# rocprofv3 summary -- kernel {a.kernel}..., Llama-3-8B decode step "
+    out.append(a.title or f"# rocprofv3 summary -- kernel {a.kernel}..., Llama-3-8B decode step "
                f"(B=32 HQ=32 HKV=8 D=128 ctx=32768, 4-bit gs32), bench.py --quick")
     if a.command:
         out.append(f"command: {a.command}")
@@ -378,7 +380,7 @@ def rocprof_summary(a) -> int:
     out.append("")
     out.append("## kernel stats (rocprofv3 --stats, all dispatches of the run)")
     out.append(f"{'calls':>6} {'avg_us':>10} {'min_us':>10} {'max_us':>10} {'pct':>6}  kernel")
-    for r in sorted(stats, key=lambda r: -float(r["TotalDurationNs"]))[:8]:
+    for r in sorted(stats, key=lambda r: -float(r["TotalDurationNs"]))[:a.rows]:
         out.append(f"{int(r['Calls']):>6} {float(r['AverageNs']) / 1e3:>10.2f} "
                    f"{float(r['MinNs']) / 1e3:>10.2f} {float(r['MaxNs']) / 1e3:>10.2f} "
                    f"{float(r['Percentage']):>6.2f}  {_short(r['Name'])}")
@@ -391,7 +393,7 @@ def rocprof_summary(a) -> int:
         dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
         groups.setdefault((r["Kernel_Name"], grid, wg), []).append(dur)
     out.append(f"{'calls':>6} {'avg_us':>10} {'median_us':>10} {'grid':>18} {'wg':>5}  kernel")
-    for (name, grid, wg), d in sorted(groups.items(), key=lambda kv: -sum(kv[1]))[:10]:
+    for (name, grid, wg), d in sorted(groups.items(), key=lambda kv: -sum(kv[1]))[:a.rows + 2]:
         out.append(f"{len(d):>6} {statistics.mean(d):>10.2f} {statistics.median(d):>10.2f} "
                    f"{'x'.join(map(str, grid)):>18} {wg:>5}  {_short(name)}")
     if a.pmc_fetch and a.pmc_write:
