@@ -23,6 +23,11 @@ Unless ``--quick``, the line also carries the 2-bit and fp16-control numbers of
 the same shape, the same 4-bit step over shuffled page pools (page sizes 32
 and 256), and the Qwen2.5-1.5B table of BASELINE.json configs 2-3
 (cache-resident and DRAM-resident, ctx 512..16384).
+
+A background sampler reads the GPU's clocks, power and temperatures while the
+Llama-shape legs run (``clocks``: per-leg windows and the quotable gate).
+``python bench.py --compare A.json B.json ...`` compares complete runs row by
+row instead of measuring.
 """
 
 from __future__ import annotations
@@ -65,6 +70,10 @@ def _args():
     ap.add_argument("--command", default="", help="command line recorded in the summary")
     ap.add_argument("--title", default="", help="first line of the summary (default: the headline)")
     ap.add_argument("--rows", type=int, default=8, help="kernels listed in the summary")
+    ap.add_argument("--no-clocks", action="store_true",
+                    help="do not sample clocks/power/temperature during the timed legs")
+    ap.add_argument("--compare", nargs="+", metavar="RUN_JSON", default=None,
+                    help="no timing: compare the bench JSON lines of complete runs row by row")
     ap.add_argument("--regime-probe", choices=("hot", "cold"), default=None,
                     help="no timing: 60 eager Qwen2.5-1.5B ctx-16384 4-bit decode calls on one "
                          "cache (hot) or rotating copies >= 768 MB (cold), for rocprofv3 --pmc")
@@ -121,6 +130,27 @@ def capture(calls):
     return g
 
 
+_CLOCKS = None          # the running clocks.ClockMonitor, if any
+_LAST_WINDOW = None     # (t0, t1) wall-clock span of the last timed_steps (warmup included)
+
+
+def clock_record(timings, full=False):
+    """Clock window of the last ``timed_steps`` call plus the row gate, or None
+    without a sampler."""
+    from tritonkv_amd import clocks
+
+    if _CLOCKS is None or _LAST_WINDOW is None:
+        return None
+    win = _CLOCKS.window(*_LAST_WINDOW)
+    gate = clocks.row_gate(win, timings)
+    if win is None:
+        return gate
+    if not full:
+        win = {k: win[k] for k in ("n_samples", "gfx_mhz_min", "gfx_mhz_mean", "power_w_mean",
+                                   "junction_c_max", "stable") if k in win}
+    return {**win, **gate}
+
+
 def timed_steps(copies, steps, warmup, reps=3):
     """µs per step of ``steps`` rotating calls in one graph: the mean over
     ``reps`` timed replays (every timed launch counts, as in a profiler's
@@ -134,7 +164,9 @@ def timed_steps(copies, steps, warmup, reps=3):
     """
     import torch
 
+    global _LAST_WINDOW
     g = capture([copies[i % len(copies)] for i in range(steps)])
+    t_start = time.time()
     for _ in range(max(1, math.ceil(warmup / steps))):
         g.replay()
     torch.cuda.synchronize()
@@ -149,6 +181,7 @@ def timed_steps(copies, steps, warmup, reps=3):
         torch.cuda.synchronize()
         walls.append((time.perf_counter() - t0) * 1e3 / steps)
         us.append(s.elapsed_time(e) * 1e3 / steps)
+    _LAST_WINDOW = (t_start, time.time())
     del g
     return statistics.mean(us), walls[0], us
 
@@ -914,6 +947,8 @@ def main() -> int:
         return rocprof_summary(a)
     if a.regime_probe:
         return regime_probe(a.regime_probe)
+    if a.compare:
+        return compare(a.compare)
     if a.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU per box; the decode step shards "
                           "by (batch, kv head) with no communication, and no figure at "
@@ -932,6 +967,12 @@ def main() -> int:
     torch.backends.cuda.matmul.allow_tf32 = False
     B, HQ, HKV, S, D, gs = 32, 32, 8, 32768, 128, 32
     detail = {}
+    global _CLOCKS
+    if not a.no_clocks:
+        from tritonkv_amd.clocks import ClockMonitor
+
+        mon = ClockMonitor()
+        _CLOCKS = mon if mon.start() else None
 
     def build_copies(nbits, g_s=gs):
         out = []
@@ -951,8 +992,10 @@ def main() -> int:
     cache4, bytes4 = algorithmic_bytes(B, HQ, HKV, S, D, 4, 4, gs)
     steps4 = [fused_call(*c, num_splits=a.num_splits) for c in copies4]
     us4, wall4, samples4 = timed_steps(steps4, a.steps, a.warmup)
+    clocks4 = clock_record(samples4, full=True)
     split4 = [fused_call(*c, num_splits=a.num_splits, split_only=True) for c in copies4]
     split_us4, _, split_samples4 = timed_steps(split4, a.steps, a.warmup)
+    clocks_split4 = clock_record(split_samples4)
     kernel4 = split4[0].kernel
     achieved = bytes4 / split_us4 / 1e3
     print(f"# llama 4-bit: step {us4:.2f} us, split kernel {split_us4:.2f} us, "
@@ -967,7 +1010,8 @@ def main() -> int:
                         "gbps_step": round(bytes4 / us4 / 1e3, 1),
                         "num_splits": steps4[0].num_splits,
                         "step_us_per_replay": [round(x, 2) for x in samples4],
-                        "split_kernel_us_per_replay": [round(x, 2) for x in split_samples4]}
+                        "split_kernel_us_per_replay": [round(x, 2) for x in split_samples4],
+                        "clocks": clocks_split4}
     cpu = None
     if not a.quick and not a.no_cpu_baseline:
         q0, kq0, vq0 = copies4[0]
@@ -985,12 +1029,12 @@ def main() -> int:
                 vp, _ = to_pool(vq, page, seed=100 + i)
                 pools.append((q, kp, vp, table))
             us, _, _ = timed_steps([paged_call(*p) for p in pools], a.steps, a.warmup)
-            sp, _, _ = timed_steps([paged_call(*p, split_only=True) for p in pools], a.steps,
-                                   a.warmup)
+            sp, _, sps = timed_steps([paged_call(*p, split_only=True) for p in pools], a.steps,
+                                     a.warmup)
             detail["paged4"][f"page{page}"] = {
                 "us_per_step": round(us, 2), "split_kernel_us": round(sp, 2),
                 "frac_of_hbm_peak": round(bytes4 / sp / 1e3 / HBM_PEAK_GBS, 4),
-                "vs_contiguous_step": round(us / us4, 4)}
+                "vs_contiguous_step": round(us / us4, 4), "clocks": clock_record(sps)}
             print(f"# llama 4-bit paged (page {page}, shuffled): step {us:.2f} us, split "
                   f"{sp:.2f} us", file=sys.stderr, flush=True)
             del pools
@@ -1005,11 +1049,12 @@ def main() -> int:
             cache, nbytes = algorithmic_bytes(B, HQ, HKV, S, D, nbits, nbits, g_s)
             mk = fp16_call if nbits == 16 else fused_call
             us, _, _ = timed_steps([mk(*c) for c in cps], a.steps, a.warmup)
-            sp, _, _ = timed_steps([mk(*c, split_only=True) for c in cps], a.steps, a.warmup)
+            sp, _, sps = timed_steps([mk(*c, split_only=True) for c in cps], a.steps, a.warmup)
             detail[name] = {"us_per_step": round(us, 2), "split_kernel_us": round(sp, 2),
                             "cache_bytes": cache, "algorithmic_bytes": nbytes,
                             "gbps_split_kernel": round(nbytes / sp / 1e3, 1),
-                            "frac_of_hbm_peak": round(nbytes / sp / 1e3 / HBM_PEAK_GBS, 4)}
+                            "frac_of_hbm_peak": round(nbytes / sp / 1e3 / HBM_PEAK_GBS, 4),
+                            "clocks": clock_record(sps)}
             print(f"# llama {name}: step {us:.2f} us, split {sp:.2f} us", file=sys.stderr, flush=True)
             del cps
             torch.cuda.empty_cache()
@@ -1048,9 +1093,28 @@ def main() -> int:
                      "kernel": kernel4, "kernel_us": round(split_us4, 2),
                      "algorithmic_bytes": bytes4},
         "cpu_baseline": cpu,
+        "clocks": clocks4,
         "detail": detail,
     }
+    if _CLOCKS is not None:
+        _CLOCKS.stop()
     print(json.dumps(line))
+    return 0
+
+
+def compare(paths) -> int:
+    """Row-by-row comparison of complete runs' bench lines (one JSON per run):
+    prints one JSON object; the rows whose run-to-run spread exceeds 5% are
+    listed under ``moved``."""
+    from tritonkv_amd import clocks
+
+    runs = [clocks.load_run(p) for p in paths]
+    names = [os.path.basename(p) for p in paths]
+    recs = clocks.compare_runs(runs, names)
+    print(json.dumps({"runs": names, "rows": len(recs),
+                      "moved": [r["key"] for r in recs if r["moved"]],
+                      "max_spread_frac": max((r["spread_frac"] for r in recs), default=None),
+                      "records": recs}))
     return 0
 
 
