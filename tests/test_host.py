@@ -128,6 +128,12 @@ def test_c_entry_points_reject_bad_arguments_without_a_gpu():
     assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
     assert lib.tkv_fp16_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
     a.D, a.S, a.split_size, a.num_splits = 96, 64, 64, 1
+    # B * HQ rows must fit a 32-bit grid
+    a.D, a.B, a.HQ, a.HKV = 128, 1 << 20, 1 << 12, 1 << 12
+    assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    assert lib.tkv_combine_splits(dummy, dummy, dummy, dummy, 1 << 20, 1 << 12, 1, 128,
+                                  None) == _lib.TKV_EINVAL
+    a.B, a.HQ, a.HKV = 1, 12, 2
     # Paged caches: page size a multiple of 32, a block table covering S exactly.
     a.D, a.page_size, a.num_pages, a.block_table_stride = 128, 16, 8, 4
     assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL

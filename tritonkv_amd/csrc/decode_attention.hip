@@ -271,6 +271,7 @@ static int validate_common(const tkv_decode_args* a) {
   if (!a || !a->q || !a->k || !a->v || !a->out) return TKV_EINVAL;
   if (a->B <= 0 || a->HQ <= 0 || a->HKV <= 0 || a->S <= 0 || a->D <= 0) return TKV_EINVAL;
   if (a->HQ % a->HKV) return TKV_EINVAL;
+  if ((int64_t)a->B * a->HQ > INT32_MAX) return TKV_EINVAL;  // grid and row indices are int
   if (a->split_size <= 0 || a->num_splits <= 0 || a->num_splits > 65535) return TKV_EINVAL;
   if ((int64_t)a->split_size * (a->num_splits - 1) >= a->S) return TKV_EINVAL;  // empty split
   if ((int64_t)a->split_size * a->num_splits < a->S) return TKV_EINVAL;        // uncovered
@@ -520,6 +521,7 @@ extern "C" int tkv_combine_splits(const float* acc, const float* maxs, const flo
                                   int32_t D, tkv_stream_t stream) {
   using namespace tkv;
   if (!acc || !maxs || !sums || !out || B <= 0 || HQ <= 0 || num_splits <= 0) return TKV_EINVAL;
+  if ((int64_t)B * HQ > INT32_MAX) return TKV_EINVAL;
   if (((uintptr_t)acc | (uintptr_t)out) & 15) return TKV_EINVAL;
   if (D != 64 && D != 128) return TKV_EUNSUPPORTED;
   (void)hipGetLastError();
