@@ -131,7 +131,8 @@ def capture(calls):
 
 
 _CLOCKS = None          # the running clocks.ClockMonitor, if any
-_LAST_WINDOW = None     # (t0, t1) wall-clock span of the last timed_steps (warmup included)
+_LAST_WINDOW = None     # (t0, t1): the last timed_steps' timed replays plus a lead-in
+CLOCK_LEAD_IN_S = 0.1   # warm-up time before the timed replays that the clock window includes
 
 
 def clock_record(timings, full=False):
@@ -170,6 +171,7 @@ def timed_steps(copies, steps, warmup, reps=3):
     for _ in range(max(1, math.ceil(warmup / steps))):
         g.replay()
     torch.cuda.synchronize()
+    t_timed = time.time()
     us, walls = [], []
     for _ in range(reps):
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -181,7 +183,7 @@ def timed_steps(copies, steps, warmup, reps=3):
         torch.cuda.synchronize()
         walls.append((time.perf_counter() - t0) * 1e3 / steps)
         us.append(s.elapsed_time(e) * 1e3 / steps)
-    _LAST_WINDOW = (t_start, time.time())
+    _LAST_WINDOW = (max(t_start, t_timed - CLOCK_LEAD_IN_S), time.time())
     del g
     return statistics.mean(us), walls[0], us
 
@@ -971,7 +973,7 @@ def main() -> int:
     if not a.no_clocks:
         from tritonkv_amd.clocks import ClockMonitor
 
-        mon = ClockMonitor()
+        mon = ClockMonitor(interval_s=0.01)
         _CLOCKS = mon if mon.start() else None
 
     def build_copies(nbits, g_s=gs):
