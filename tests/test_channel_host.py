@@ -93,3 +93,24 @@ def test_channel_window_entry_points_reject_bad_arguments_without_a_gpu():
     bad_gs = list(args)
     bad_gs[7] = 64
     assert lib.tkv_channel_window_flush(*bad_gs) == _lib.TKV_EUNSUPPORTED
+
+
+def test_channel_cache_checks_token_shapes_before_any_launch():
+    from tritonkv_amd.channel import ChannelKVCache
+
+    c = ChannelKVCache(2, 2, 64, 128, device="cpu")
+    good = torch.zeros(2, 2, 3, 128, dtype=torch.float16)
+    with pytest.raises(ValueError, match="one shape"):
+        c.extend(torch.zeros(1, 2, 3, 128, dtype=torch.float16), good)   # would broadcast
+    with pytest.raises(ValueError, match="one shape"):
+        c.extend(good, torch.zeros(2, 2, 4, 128, dtype=torch.float16))
+    with pytest.raises(ValueError, match="one shape"):
+        c.step(good, good, torch.zeros(2, 8, 128, dtype=torch.float16))  # 3 tokens, not 1
+    with pytest.raises(TypeError):
+        c.extend(None, good)
+    assert len(c) == 0
+    c.quantized, c.window = 32, 5
+    c._qlens.fill_(32)
+    c._rlens.fill_(5)
+    c.reset()
+    assert len(c) == 0 and not c._qlens.any() and not c._rlens.any()

@@ -97,6 +97,8 @@ def append_keys_per_channel(ck: ChannelQuantizedKeys, k_new: torch.Tensor,
         raise ValueError(f"token count {N} must be a multiple of {BLOCK}")
     if k_new.dtype not in (torch.float16, torch.float32):
         raise TypeError(f"k_new must be float16 or float32, got {k_new.dtype}")
+    if k_new.device != ck.device:
+        raise ValueError(f"k_new is on {k_new.device}, the keys on {ck.device}")
     if positions is not None and (positions.dtype != torch.int32 or positions.numel() != B
                                   or positions.device != k_new.device):
         raise ValueError("positions must be an int32 tensor of B entries on the cache's device")
@@ -229,8 +231,26 @@ class ChannelKVCache:
     def __len__(self) -> int:
         return self.quantized + self.window
 
+    def reset(self) -> None:
+        """Forget every token (host counters and device-side lengths)."""
+        self.quantized = self.window = 0
+        self._qlens.zero_()
+        self._rlens.zero_()
+
     def nbytes(self) -> int:
         return self.keys.nbytes() + self.values.nbytes() + 2 * self.k_res.numel() * 2
+
+    def _check_tokens(self, k: torch.Tensor, v: torch.Tensor, n: int | None = None) -> None:
+        B, HKV, _, D = self.k_res.shape
+        if not isinstance(k, torch.Tensor) or not isinstance(v, torch.Tensor):
+            raise TypeError("k and v must be tensors")
+        if k.dim() != 4 or k.shape != v.shape or (k.shape[0], k.shape[1], k.shape[3]) != (B, HKV, D) \
+                or (n is not None and k.shape[2] != n):
+            want = f"({B}, {HKV}, {'N' if n is None else n}, {D})"
+            raise ValueError(f"k / v must be {want} tensors of one shape, got {tuple(k.shape)} "
+                             f"and {tuple(v.shape)}")
+        if k.device != self.k_res.device or v.device != self.k_res.device:
+            raise ValueError(f"k / v must be on the cache's device {self.k_res.device}")
 
     def _flush(self) -> None:
         self._pos.fill_(self.quantized)
@@ -241,6 +261,7 @@ class ChannelKVCache:
 
     def extend(self, k: torch.Tensor, v: torch.Tensor) -> None:
         """Append ``(B, HKV, N, D)`` keys and values from the host (prefill)."""
+        self._check_tokens(k, v)
         if k.dtype != torch.float16:
             k = k.to(torch.float16)
         if v.dtype != torch.float16:
@@ -282,11 +303,10 @@ class ChannelKVCache:
         attention, window flush), device-side lengths only: graph-capturable."""
         if len(self) + 1 > self.capacity:
             raise ValueError(f"cache capacity {self.capacity} exceeded")
+        self._check_tokens(k, v, 1)
         B, HKV, _, D = self.k_res.shape
         kk = k.to(torch.float16).contiguous()
         vv = v.to(torch.float16).contiguous()
-        if kk.numel() != B * HKV * D or vv.numel() != B * HKV * D:
-            raise ValueError(f"k / v must hold one (B, HKV, D) token, got {tuple(k.shape)}")
         lib, st = _lib.load(), _lib.stream_handle(self.k_res.device)
         with torch.cuda.device(self.k_res.device):
             rc = lib.tkv_channel_window_append(kk.data_ptr(), vv.data_ptr(), B, HKV, D,

@@ -141,7 +141,7 @@ class TkvLayer(_LayerBase):
         if self.is_initialized:
             self.lens.zero_()
             if self.key_format == "channel":
-                self.cc.quantized = self.cc.window = 0
+                self.cc.reset()
 
     def decode(self, module, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                scaling: float) -> torch.Tensor:
