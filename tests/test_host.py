@@ -192,6 +192,17 @@ def test_python_validation_precedes_backend_check():
         fused_decode_attention(q, _fake_qt(gs=8), _fake_qt(gs=8), fold_zp=True)
     with pytest.raises(ValueError, match="same shape"):
         fused_decode_attention(q, _fake_qt(S=64), _fake_qt(S=32))
+    # every tensor on one device: a host pointer handed to a kernel would fault the GPU
+    with pytest.raises(ValueError, match="same device"):
+        fused_decode_attention(q, _fake_qt(), _fake_qt(device="meta"))
+    from tritonkv_amd.kernels import fp16_decode_attention
+    from tritonkv_amd.kernels.fused_decode_attn import _check_out
+
+    kv = torch.zeros(1, 2, 64, 128, dtype=torch.float16)
+    with pytest.raises(ValueError, match="same device"):
+        fp16_decode_attention(q, kv, kv.to("meta"))
+    with pytest.raises(ValueError, match="tensor on"):
+        _check_out(torch.empty(1, 12, 128), 1, 12, 128, torch.device("cuda", 0))
 
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU error path")

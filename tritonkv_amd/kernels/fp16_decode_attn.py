@@ -52,6 +52,8 @@ def fp16_decode_attention(
         raise ValueError(f"HQ={HQ} must be a multiple of HKV={HKV}")
     if k.shape != v.shape or k.shape[0] != B or k.shape[3] != D:
         raise ValueError(f"k {tuple(k.shape)} / v {tuple(v.shape)} incompatible with q {tuple(q.shape)}")
+    if k.device != q.device or v.device != q.device:
+        raise ValueError("q, k and v must be on the same device")
 
     ok, why = triton_available()
     if not ok:

@@ -192,7 +192,7 @@ def _workspace_for(ws: dict | None, B: int, HQ: int, num_splits: int, D: int, de
             ws["dummy_acc"] = acc
         return None, None, None, None
     key = (B, HQ, num_splits, D)
-    if ws.get("key") != key:
+    if ws.get("key") != key or ws["acc"].device != torch.device(device):
         acc = torch.empty((B, HQ, num_splits, D), device=device, dtype=torch.float32)
         maxs = torch.empty((B, HQ, num_splits), device=device, dtype=torch.float32)
         sums = torch.empty((B, HQ, num_splits), device=device, dtype=torch.float32)
@@ -214,8 +214,9 @@ def _aligned16(t: torch.Tensor) -> torch.Tensor:
 def _check_out(out, B, HQ, D, device):
     if out is None:
         return torch.empty((B, HQ, D), device=device, dtype=torch.float32)
-    if out.shape != (B, HQ, D) or out.dtype != torch.float32 or not out.is_contiguous():
-        raise ValueError(f"out must be a contiguous float32 ({B}, {HQ}, {D}) tensor")
+    if out.shape != (B, HQ, D) or out.dtype != torch.float32 or not out.is_contiguous() \
+            or out.device != torch.device(device):
+        raise ValueError(f"out must be a contiguous float32 ({B}, {HQ}, {D}) tensor on {device}")
     return out
 
 
@@ -303,6 +304,8 @@ def fused_decode_attention(
         raise ValueError(f"head_dim {D} must be a multiple of group_size {kq.group_size}")
     if fold_zp and kq.group_size < 16:
         raise ValueError(f"fold_zp needs group_size >= 16, got {kq.group_size}")
+    if kq.packed.device != q.device or vq.packed.device != q.device:
+        raise ValueError("q and the K/V caches must be on the same device")
     kn, vn, new_f32 = new_token_args(k_new, v_new, B, HKV, D, q.device)
 
     ok, why = triton_available()

@@ -88,6 +88,8 @@ def paged_append(pool: QuantizedTensor, x_new: torch.Tensor, block_table: torch.
                          f"{tuple(pool.packed.shape)} (head_dim {pool.head_dim})")
     if x_new.dtype not in (torch.float16, torch.float32):
         raise TypeError(f"x_new must be float16 or float32, got {x_new.dtype}")
+    if pool.packed.device != x_new.device:
+        raise ValueError(f"x_new is on {x_new.device}, the pool on {pool.packed.device}")
     if positions is None or positions.dtype != torch.int32 or positions.numel() != B \
             or positions.device != x_new.device:
         raise ValueError("positions must be an int32 tensor of B entries on the pool's device")
@@ -153,7 +155,7 @@ def paged_decode_attention(
                                  or seq_lens.dtype != torch.int32 or seq_lens.numel() != B
                                  or seq_lens.device != q.device):
         raise ValueError("seq_lens must be an int32 tensor of B lengths on the pool's device")
-    if q.device != k_pool.device:
+    if q.device != k_pool.device or v_pool.device != k_pool.device:
         raise ValueError("q and the pools must be on the same device")
     kn, vn, new_f32 = new_token_args(k_new, v_new, B, HKV, D, q.device)
     ok, why = triton_available()
