@@ -168,8 +168,11 @@ int tkv_paged_quantize_pack(const void *x, int32_t x_is_fp32, int32_t B, int32_t
  * (b, head); split_base / num_splits_total / counters are ignored.  k_res,
  * v_res: fp16 (B, HKV, res_cap, D), the window; row b attends to its first
  * res_lens[b] window tokens (0 <= res_lens[b] <= res_cap; NULL = res_cap)
- * after its quantized ones.  Three launches: the quantized split kernel, the
- * fp16 split kernel over the window (partial row num_splits), the combine. */
+ * after its quantized ones.  Two launches when res_cap <= 32: the quantized
+ * split kernel (partial rows 0 .. num_splits-1), then the combine, which
+ * attends to the window itself and merges it as one more split.  A longer
+ * window takes a third launch, the fp16 split kernel over the window
+ * (partial row num_splits), before the combine. */
 int tkv_channel_decode_attention(const tkv_decode_args *args, const void *k_res,
                                  const void *v_res, const int32_t *res_lens, int32_t res_cap,
                                  tkv_stream_t stream);

@@ -69,7 +69,7 @@ def test_channel_key_append_positions():
     assert (packed[3] == 0xAB).all()                                     # position 16: unaligned
 
 
-def _window_case(B, HQ, HKV, D, S, kbits, vbits, gs, q_lens, r_lens, seed):
+def _window_case(B, HQ, HKV, D, S, kbits, vbits, gs, q_lens, r_lens, seed, R=32):
     from tritonkv_amd.channel import quantize_keys_per_channel
     from tritonkv_amd.quantize import quantize_groupwise
 
@@ -80,8 +80,8 @@ def _window_case(B, HQ, HKV, D, S, kbits, vbits, gs, q_lens, r_lens, seed):
     k[:, :, :, 70 % D] *= 8
     k = k.half()
     v = torch.randn(B, HKV, S, D, generator=g).half()
-    kres = torch.randn(B, HKV, 32, D, generator=g).half()
-    vres = torch.randn(B, HKV, 32, D, generator=g).half()
+    kres = torch.randn(B, HKV, R, D, generator=g).half()
+    vres = torch.randn(B, HKV, R, D, generator=g).half()
     ck = quantize_keys_per_channel(k.to(DEV), kbits)
     vq = quantize_groupwise(v.to(DEV), vbits, gs)
     ql = torch.tensor(q_lens, dtype=torch.int32)
@@ -134,6 +134,30 @@ def test_channel_decode_matches_oracle(case, ns, lens):
     assert torch.isfinite(got).all()
     ref = _oracle(q, ck, vq, kres, vres, ql, rl)
     assert_close_to_reference(got, ref, f"channel decode {case} ns={ns}")
+
+
+@pytest.mark.parametrize("R", [16, 48])
+@pytest.mark.parametrize("q_dtype", [torch.float16, torch.float32])
+def test_channel_decode_window_sizes(R, q_dtype):
+    """Windows of up to 32 tokens are attended inside the combine, longer ones
+    by the fp16 kernel as one more split; fp32 q is rounded to fp16 in both."""
+    from tritonkv_amd.channel import channel_decode_attention
+
+    q_lens, r_lens = [64, 0, 33, 128], [R, 5, 0, R - 1]
+    print(f"channel decode window R={R} q={q_dtype}", flush=True)
+    q, ck, vq, kres, vres, ql, rl = _window_case(4, 12, 2, 128, 128, 4, 2, 32, q_lens, r_lens,
+                                                 seed=R, R=R)
+    q = q.to(q_dtype)
+    got = channel_decode_attention(q.to(DEV), ck, vq, kres.to(DEV), vres.to(DEV),
+                                   q_lens=ql.to(DEV), res_lens=rl.to(DEV))
+    torch.cuda.synchronize()
+    ref = _oracle(q, ck, vq, kres, vres, ql, rl)
+    assert_close_to_reference(got, ref, f"channel decode window R={R}")
+    # no lengths: every window full
+    got = channel_decode_attention(q.to(DEV), ck, vq, kres.to(DEV), vres.to(DEV), q_lens=ql.to(DEV))
+    torch.cuda.synchronize()
+    ref = _oracle(q, ck, vq, kres, vres, ql, torch.full((4,), R, dtype=torch.int32))
+    assert_close_to_reference(got, ref, f"channel decode full window R={R}")
 
 
 def test_channel_decode_ignores_garbage_past_the_lengths():

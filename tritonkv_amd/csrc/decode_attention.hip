@@ -213,13 +213,33 @@ fp16_split_kernel(SplitParams prm) {
 // log-sum-exp merge (all loads of an iteration are independent of the
 // previous one, so they stay in flight together), then the SG split groups
 // are merged through LDS.  Empty splits (m_s = -inf, only possible with
-// per-row lengths) contribute nothing.
+// per-row lengths) contribute nothing.  Partial rows are `stride` apart; the
+// first `ns` of them are merged.
+//
+// WIN: the fp16 residual window of per-channel keys is attended here too, as
+// one more split.  Row b's window holds w.lens[b] <= kWinMax tokens of kv head
+// h / G.  Lanes 8t .. 8t+7 compute the score of token t (fp32 products of the
+// fp16-rounded q and the fp16 keys, as exact as the fp16 kernel's MFMA), the
+// scores meet in LDS, and thread (sg, dq) starts its merge state from the
+// window tokens sg, sg + SG, ... with the window's maximum.
 // ===========================================================================
-template <int D>
+constexpr int kWinMax = 32;
+
+struct WindowArgs {
+  const void* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const int32_t* lens;  // nullptr: every row's window holds R tokens
+  int q_fp32, R, HQ, G;
+  float qk_scale;       // sm_scale * log2(e)
+};
+
+template <int D, bool WIN>
 __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ acc,
                                                       const float* __restrict__ maxs,
                                                       const float* __restrict__ sums,
-                                                      float* __restrict__ out, int ns) {
+                                                      float* __restrict__ out, int ns, int stride,
+                                                      WindowArgs w) {
   constexpr int DQ = D / 4;     // float4 columns of a split row
   constexpr int SG = 256 / DQ;  // split groups
   __shared__ float sm_m[SG], sm_l[SG];
@@ -228,9 +248,62 @@ __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ 
   const int t = threadIdx.x, dq = t % DQ, sg = t / DQ;
   float m = -INFINITY, l = 0.0f;
   f4 a = f4{0.f, 0.f, 0.f, 0.f};
+  if constexpr (WIN) {
+    __shared__ float sm_s[kWinMax];
+    constexpr int DD = D / 8;  // dims per lane of a token's score
+    const int b = (int)(row / w.HQ), h = (int)(row % w.HQ);
+    const int L = w.lens ? min(max(w.lens[b], 0), w.R) : w.R;  // uniform in the workgroup
+    if (L > 0) {
+      const int64_t base = ((int64_t)b * (w.HQ / w.G) + h / w.G) * w.R;
+      const int tok = t >> 3, part = t & 7;
+      float dot = 0.0f;
+      if (tok < L) {
+        const uint16_t* kr = w.k + (base + tok) * D + part * DD;
+#pragma unroll
+        for (int i = 0; i < DD; i += 8) {
+          const h8 kv = *reinterpret_cast<const h8*>(kr + i);
+          float qv[8];
+          if (w.q_fp32) {
+            const float* qp = static_cast<const float*>(w.q) + row * D + part * DD + i;
+            const f4 q0 = *reinterpret_cast<const f4*>(qp), q1 = *reinterpret_cast<const f4*>(qp + 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              qv[e] = (float)(_Float16)q0[e];
+              qv[4 + e] = (float)(_Float16)q1[e];
+            }
+          } else {
+            const h8 qh = *reinterpret_cast<const h8*>(static_cast<const _Float16*>(w.q) + row * D +
+                                                       part * DD + i);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qv[e] = (float)qh[e];
+          }
+          const f4 k0 = __builtin_convertvector(kv.lo, f4), k1 = __builtin_convertvector(kv.hi, f4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            dot = fmaf(qv[e], k0[e], dot);
+            dot = fmaf(qv[4 + e], k1[e], dot);
+          }
+        }
+      }
+      dot += __shfl_xor(dot, 1, 64);
+      dot += __shfl_xor(dot, 2, 64);
+      dot += __shfl_xor(dot, 4, 64);
+      if (part == 0 && tok < kWinMax) sm_s[tok] = dot * w.qk_scale;
+      __syncthreads();
+      float mw = -INFINITY;
+      for (int i = 0; i < L; ++i) mw = fmaxf(mw, sm_s[i]);
+      for (int i = sg; i < L; i += SG) {
+        const float p = __builtin_amdgcn_exp2f(sm_s[i] - mw);
+        const h4 vh = *reinterpret_cast<const h4*>(w.v + (base + i) * D + 4 * dq);
+        a += __builtin_convertvector(vh, f4) * p;
+        l += p;
+      }
+      m = mw;
+    }
+  }
 #pragma unroll 4
   for (int s = sg; s < ns; s += SG) {
-    const int64_t ps = row * ns + s;
+    const int64_t ps = row * stride + s;
     const float ms = maxs[ps];
     const float ls = sums[ps];
     const f4 as = reinterpret_cast<const f4*>(acc + ps * D)[dq];
@@ -384,15 +457,23 @@ static int dispatch_bits(const SplitParams& p, dim3 grid, int knb, int vnb, int 
   return TKV_EUNSUPPORTED;
 }
 
+// Merges partial rows 0 .. ns-1 (of `stride` per output row), plus the fp16
+// window when `win` is given.
 static int launch_combine(const float* acc, const float* maxs, const float* sums, float* out,
-                          int B, int HQ, int ns, int D, hipStream_t st) {
+                          int B, int HQ, int ns, int D, hipStream_t st, int stride = 0,
+                          const WindowArgs* win = nullptr) {
   const dim3 grid((unsigned)(B * HQ));
-  if (D == 128)
-    combine_kernel<128><<<grid, dim3(256), 0, st>>>(acc, maxs, sums, out, ns);
-  else if (D == 64)
-    combine_kernel<64><<<grid, dim3(256), 0, st>>>(acc, maxs, sums, out, ns);
-  else
+  const int sd = stride ? stride : ns;
+  const WindowArgs w = win ? *win : WindowArgs{};
+  if (D == 128) {
+    if (win) combine_kernel<128, true><<<grid, dim3(256), 0, st>>>(acc, maxs, sums, out, ns, sd, w);
+    else combine_kernel<128, false><<<grid, dim3(256), 0, st>>>(acc, maxs, sums, out, ns, sd, w);
+  } else if (D == 64) {
+    if (win) combine_kernel<64, true><<<grid, dim3(256), 0, st>>>(acc, maxs, sums, out, ns, sd, w);
+    else combine_kernel<64, false><<<grid, dim3(256), 0, st>>>(acc, maxs, sums, out, ns, sd, w);
+  } else {
     return TKV_EUNSUPPORTED;
+  }
   return TKV_OK;
 }
 
@@ -496,6 +577,22 @@ extern "C" int tkv_channel_decode_attention(const tkv_decode_args* a, const void
   qa.counters = nullptr;
   int rc = launch_fused_split(&qa, st);
   if (rc) return rc;
+  if (res_cap <= kWinMax) {  // the window is attended inside the combine
+    WindowArgs w;
+    w.q = a->q;
+    w.k = static_cast<const uint16_t*>(k_res);
+    w.v = static_cast<const uint16_t*>(v_res);
+    w.lens = res_lens;
+    w.q_fp32 = a->q_is_fp32 ? 1 : 0;
+    w.R = res_cap;
+    w.HQ = a->HQ;
+    w.G = a->HQ / a->HKV;
+    w.qk_scale = a->sm_scale * kLog2e;
+    (void)hipGetLastError();
+    launch_combine(a->acc, a->maxs, a->sums, a->out, a->B, a->HQ, a->num_splits, a->D, st,
+                   total, &w);
+    return status_of_launch();
+  }
   tkv_decode_args ra = *a;  // the fp16 window: partial row num_splits
   ra.k = k_res;
   ra.v = v_res;
