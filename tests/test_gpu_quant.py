@@ -111,6 +111,28 @@ def test_gpu_quantize_unaligned_input_takes_the_row_kernel(nbits, gs, D, dtype):
     assert np.array_equal(qt.packed.cpu().numpy(), ref.packed)
 
 
+def test_gpu_quantize_unaligned_beyond_one_launch():
+    """More unaligned rows than one 2^32-work-item grid holds (4 * (2^24 - 1)):
+    the row kernel is launched in pieces; the result equals the wide kernel's
+    on the same (aligned) data bit for bit."""
+    from tritonkv_amd.quantize import quantize_groupwise
+
+    rows, D = 4 * ((1 << 24) - 1) + 100, 64
+    print(f"unaligned quantize of {rows} rows", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(7)
+    xa = torch.randn(1, 1, rows, D, device=DEV, generator=g, dtype=torch.float16)
+    buf = torch.empty(xa.numel() + 1, dtype=torch.float16, device=DEV)
+    xu = buf[1:].view(xa.shape)
+    xu.copy_(xa)
+    assert xu.data_ptr() % 16
+    want = quantize_groupwise(xa, 4, 32)
+    got = quantize_groupwise(xu, 4, 32)
+    del buf, xu, xa
+    assert torch.equal(got.packed, want.packed)
+    assert torch.equal(got.scale.view(torch.int16), want.scale.view(torch.int16))
+    assert torch.equal(got.zero.view(torch.int16), want.zero.view(torch.int16))
+
+
 def _boundary_rows(rows, D, nbits, gs, seed):
     """fp32 rows whose values sit on, and one or two ulps either side of, the
     half-integer code boundaries (x - zero) / scale = k + 1/2 of their group."""

@@ -36,7 +36,7 @@ struct PageMap {
 // aligned for the wide kernel below.
 template <int D, int NB, int GS, bool F32>
 __global__ void __launch_bounds__(256)
-quantize_pack_kernel(const void* __restrict__ x, int64_t rows, int HKV, int N,
+quantize_pack_kernel(const void* __restrict__ x, int64_t row0, int64_t rows, int HKV, int N,
                      const int32_t* __restrict__ positions, int S_cap, PageMap pm,
                      uint8_t* __restrict__ packed, uint16_t* __restrict__ scale,
                      uint16_t* __restrict__ zero) {
@@ -44,7 +44,7 @@ quantize_pack_kernel(const void* __restrict__ x, int64_t rows, int HKV, int N,
   constexpr int P = R::P, DP = R::DP, NG = R::NG;
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int64_t rr = (int64_t)blockIdx.x * 4 + w;
+  const int64_t rr = row0 + (int64_t)blockIdx.x * 4 + w;
   if (rr >= rows) return;  // whole wave
   float xv[P];
   load_row_for_quant<D, NB>(static_cast<const uint8_t*>(x) + rr * D * (F32 ? 4 : 2), F32, lane, xv);
@@ -505,11 +505,17 @@ static void launch_quantize(const void* x, bool f32, int64_t rows, int HKV, int 
     }
 #undef TKV_WIDE
   } else {
-    const dim3 grid((unsigned)((rows + 3) / 4));
-    if (f32)
-      quantize_pack_kernel<D, NB, GS, true><<<grid, 256, 0, st>>>(x, rows, HKV, N, pos, S_cap, pm, pk, sc, zr);
-    else
-      quantize_pack_kernel<D, NB, GS, false><<<grid, 256, 0, st>>>(x, rows, HKV, N, pos, S_cap, pm, pk, sc, zr);
+    // One wave per row, four per workgroup; launched in pieces so that no grid
+    // exceeds 2^32 work-items.
+    constexpr int64_t kMaxBlocks = (1 << 24) - 1;
+    for (int64_t row0 = 0; row0 < rows; row0 += 4 * kMaxBlocks) {
+      const int64_t n = rows - row0 < 4 * kMaxBlocks ? rows - row0 : 4 * kMaxBlocks;
+      const dim3 grid((unsigned)((n + 3) / 4));
+      if (f32)
+        quantize_pack_kernel<D, NB, GS, true><<<grid, 256, 0, st>>>(x, row0, rows, HKV, N, pos, S_cap, pm, pk, sc, zr);
+      else
+        quantize_pack_kernel<D, NB, GS, false><<<grid, 256, 0, st>>>(x, row0, rows, HKV, N, pos, S_cap, pm, pk, sc, zr);
+    }
   }
 }
 
