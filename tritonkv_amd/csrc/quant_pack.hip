@@ -364,24 +364,25 @@ channel_window_flush_kernel(const uint16_t* __restrict__ k_res, const uint16_t* 
   }
 }
 
-// One thread per packed dword.
+// One thread per packed dword (grid-stride: the grid is capped at 2^20 workgroups).
 __global__ void __launch_bounds__(256)
 pack_codes_kernel(const uint8_t* __restrict__ codes, int64_t rows, int D, int NB,
                   uint8_t* __restrict__ packed) {
   const int P = 8 / NB, DP = D / P, DW = DP / 4;
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= rows * DW) return;
-  const int64_t row = i / DW;
-  const int q = (int)(i % DW);
-  const uint8_t* c = codes + row * D;
-  uint32_t word = 0;
-  for (int k = 0; k < 4; ++k) {
-    const int jb = 4 * q + k;
-    uint32_t byte = 0;
-    for (int p = 0; p < P; ++p) byte |= (uint32_t)(c[jb + p * DP] & ((1 << NB) - 1)) << (p * NB);
-    word |= byte << (8 * k);
+  const int64_t n = rows * DW, step = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
+    const int64_t row = i / DW;
+    const int q = (int)(i % DW);
+    const uint8_t* c = codes + row * D;
+    uint32_t word = 0;
+    for (int k = 0; k < 4; ++k) {
+      const int jb = 4 * q + k;
+      uint32_t byte = 0;
+      for (int p = 0; p < P; ++p) byte |= (uint32_t)(c[jb + p * DP] & ((1 << NB) - 1)) << (p * NB);
+      word |= byte << (8 * k);
+    }
+    reinterpret_cast<uint32_t*>(packed + row * DP)[q] = word;
   }
-  reinterpret_cast<uint32_t*>(packed + row * DP)[q] = word;
 }
 
 __device__ __forceinline__ void emit(uint8_t* codes_out, float* values_out,
@@ -731,7 +732,8 @@ extern "C" int tkv_pack_codes(const uint8_t* codes, int64_t rows, int32_t D, int
   if ((uintptr_t)packed & 3) return TKV_EINVAL;
   const int64_t n = rows * (D / P / 4);
   (void)hipGetLastError();
-  pack_codes_kernel<<<dim3((unsigned)((n + 255) / 256)), 256, 0,
+  const int64_t blocks = (n + 255) / 256 < (1 << 20) ? (n + 255) / 256 : (1 << 20);  // grid-stride beyond
+  pack_codes_kernel<<<dim3((unsigned)blocks), 256, 0,
                       reinterpret_cast<hipStream_t>(stream)>>>(codes, rows, D, nbits, packed);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? TKV_OK : (int)e;
