@@ -32,8 +32,14 @@ enum {
   TKV_OK = 0,
   TKV_EINVAL = -1,       /* inconsistent or out-of-range argument */
   TKV_EUNSUPPORTED = -2, /* valid but not compiled: D, nbits, group size combination */
-  TKV_ENODEVICE = -3     /* no HIP device visible */
+  TKV_ENODEVICE = -3,    /* no HIP device visible */
+  TKV_ESCRATCH = -4      /* split partials larger than TKV_NOALLOC_SCRATCH_BYTES */
 };
+
+/* Bytes of device memory tkv_fused_decode_attention_noalloc keeps per GPU for
+ * the split partials of one call (16 MiB: B*HQ*num_splits*(D + 2)*4 bytes must
+ * fit, e.g. 32768 partial rows at D = 128). */
+#define TKV_NOALLOC_SCRATCH_BYTES (16u << 20)
 
 /* Arguments of one decode step.  For the quantized path k/v are the packed
  * codes and k_scale/k_zero/v_scale/v_zero the fp16 metadata; for the fp16
@@ -117,6 +123,20 @@ int tkv_fused_decode_attention(const tkv_decode_args *args, tkv_stream_t stream)
 /* fp16 control: identical split, softmax and combine; K/V read as fp16.
  * Replaces kernels/fp16_decode_attn.py:207-239 (_fp16_decode_attn_split :47-135). */
 int tkv_fp16_decode_attention(const tkv_decode_args *args, tkv_stream_t stream);
+
+/* tkv_fused_decode_attention that allocates nothing and takes no workspace:
+ * the split partials go to a static device array of TKV_NOALLOC_SCRATCH_BYTES
+ * that each GPU holds from the library's load until the process ends (its
+ * address is looked up once per device, on the first call there).  For callers
+ * that cannot call hipMalloc: code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation.  No counterpart in the reference.
+ * args->acc, maxs, sums and counters must be NULL; the partials of
+ * B * HQ * num_splits rows must fit the scratch (else TKV_ESCRATCH, nothing
+ * launched).  Inputs and out are the caller's, exactly as for
+ * tkv_fused_decode_attention, and the result is bit-identical to it.  All
+ * calls on one GPU share the array, which keeps the last call's contents:
+ * calls that overlap in time on one GPU (e.g. on two streams) race. */
+int tkv_fused_decode_attention_noalloc(const tkv_decode_args *args, tkv_stream_t stream);
 
 /* The split kernels alone (no combine launch): with num_splits == 1 they write
  * out; otherwise the partials acc/maxs/sums, merged into out by the last
@@ -253,7 +273,8 @@ const char *tkv_status_string(int status);
  * paged-cache fields of tkv_decode_args and tkv_paged_quantize_pack, 4 the
  * fused-append fields, 5 the per-channel key and partials-placement fields,
  * tkv_quantize_keys_channel, tkv_channel_decode_attention and the
- * tkv_channel_window_* calls). */
+ * tkv_channel_window_* calls, 6 tkv_fused_decode_attention_noalloc and
+ * TKV_ESCRATCH). */
 int tkv_abi_version(void);
 
 #ifdef __cplusplus

@@ -45,7 +45,7 @@ def test_library_exports_every_declared_symbol():
     for name in _declared_symbols():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.tkv_abi_version() == 5
+    assert lib.tkv_abi_version() == 6
 
 
 def test_library_is_gfx950_only():
@@ -159,6 +159,35 @@ def test_c_entry_points_reject_bad_arguments_without_a_gpu():
     assert lib.tkv_paged_quantize_pack(dummy, 0, 1, 1, 1, 128, 4, 32, dummy, dummy, 1, 48, 1,
                                        dummy, dummy, dummy, None) == _lib.TKV_EINVAL
     assert _lib.status_string(_lib.TKV_EINVAL) == "invalid argument"
+
+
+def test_noalloc_entry_point_rejects_before_touching_the_gpu():
+    """tkv_fused_decode_attention_noalloc: no workspace accepted, partials bounded by the scratch."""
+    from tritonkv_amd import _lib
+
+    lib = _lib.load()
+    assert lib.tkv_fused_decode_attention_noalloc(None, None) == _lib.TKV_EINVAL
+    dummy = 0x1000
+    a = _lib.DecodeArgs(q=dummy, k=dummy, v=dummy, k_scale=dummy, k_zero=dummy, v_scale=dummy,
+                        v_zero=dummy, out=dummy, B=1, HQ=12, HKV=2, S=4096, D=128, k_nbits=4,
+                        v_nbits=4, group_size=32, sm_scale=0.1, split_size=512, num_splits=8)
+    a.acc = a.maxs = a.sums = dummy  # the partials are the library's
+    assert lib.tkv_fused_decode_attention_noalloc(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    a.acc = a.maxs = a.sums = None
+    a.counters = dummy
+    assert lib.tkv_fused_decode_attention_noalloc(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    a.counters = None
+    a.split_base, a.num_splits_total = 1, 9  # must own every split
+    assert lib.tkv_fused_decode_attention_noalloc(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    a.split_base, a.num_splits_total = 0, 0
+    # 12 rows x 4096 splits x (128 + 2) floats = 24.4 MiB > 16 MiB
+    a.split_size, a.num_splits = 1, 4096
+    assert lib.tkv_fused_decode_attention_noalloc(ctypes.byref(a), None) == _lib.TKV_ESCRATCH
+    rows = _lib.NOALLOC_SCRATCH_BYTES // ((128 + 2) * 4)
+    assert 12 * 4096 > rows
+    assert "static scratch" in _lib.status_string(_lib.TKV_ESCRATCH)
+    with pytest.raises(ValueError, match="static scratch"):
+        _lib.check(_lib.TKV_ESCRATCH, "noalloc")
 
 
 def _fake_qt(B=1, HKV=2, S=64, D=128, nbits=4, gs=32, device="cpu"):

@@ -23,6 +23,8 @@ TKV_OK = 0
 TKV_EINVAL = -1
 TKV_EUNSUPPORTED = -2
 TKV_ENODEVICE = -3
+TKV_ESCRATCH = -4
+NOALLOC_SCRATCH_BYTES = 16 << 20  # TKV_NOALLOC_SCRATCH_BYTES
 
 
 class DecodeArgs(ctypes.Structure):
@@ -89,6 +91,7 @@ _P, _I32, _I64, _F32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c
 SIGNATURES = {
     "tkv_fused_decode_attention": ([ctypes.POINTER(DecodeArgs), _P], ctypes.c_int),
     "tkv_fp16_decode_attention": ([ctypes.POINTER(DecodeArgs), _P], ctypes.c_int),
+    "tkv_fused_decode_attention_noalloc": ([ctypes.POINTER(DecodeArgs), _P], ctypes.c_int),
     "tkv_fused_decode_split": ([ctypes.POINTER(DecodeArgs), _P], ctypes.c_int),
     "tkv_fp16_decode_split": ([ctypes.POINTER(DecodeArgs), _P], ctypes.c_int),
     "tkv_combine_splits": ([_P, _P, _P, _P, _I32, _I32, _I32, _I32, _P], ctypes.c_int),
@@ -153,7 +156,7 @@ def check(rc: int, what: str) -> None:
     if rc == TKV_OK:
         return
     msg = f"{what}: {status_string(rc)} (status {rc})"
-    if rc in (TKV_EINVAL, TKV_EUNSUPPORTED):
+    if rc in (TKV_EINVAL, TKV_EUNSUPPORTED, TKV_ESCRATCH):
         raise ValueError(msg)
     raise RuntimeError(msg)
 

@@ -27,6 +27,8 @@
 //   * Each chunk's codes and scale/zero rows reach LDS by direct-to-LDS loads
 //     (quantized kernel) or registers (fp16 control); the partial (m, l, acc)
 //     of the NW waves is merged in LDS and written once per workgroup.
+#include <mutex>
+
 #include "decode_common.h"
 
 namespace tkv {
@@ -630,6 +632,70 @@ extern "C" int tkv_channel_decode_attention(const tkv_decode_args* a, const void
   (void)hipGetLastError();
   launch_combine(a->acc, a->maxs, a->sums, a->out, a->B, a->HQ, total, a->D, st);
   return status_of_launch();
+}
+
+// ===========================================================================
+// The fused decode step without a workspace: the split partials (acc, maxs,
+// sums) of a call live in `scratch`, a device array each GPU holds from the
+// library's load until the process ends.  In host code `scratch` names a
+// host-side stand-in; its device address is taken once per device with
+// hipGetSymbolAddress (with that device current) and only that address is
+// handed to kernels.  Every split writes its partial rows (an empty split
+// writes max -inf, sum 0), so nothing has to be cleared between calls.  All
+// calls on one GPU share the array: calls that overlap in time there race.
+// ===========================================================================
+static __device__ __align__(256) unsigned char scratch[TKV_NOALLOC_SCRATCH_BYTES];
+
+namespace tkv {
+
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxScratchDevices];
+
+// Device address of `scratch` on the current device (looked up once per device).
+static int scratch_on_current_device(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxScratchDevices) return TKV_EINVAL;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!p) return TKV_ENODEVICE;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return TKV_OK;
+}
+
+constexpr uint64_t align256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
+
+}  // namespace tkv
+
+extern "C" int tkv_fused_decode_attention_noalloc(const tkv_decode_args* a, tkv_stream_t stream) {
+  using namespace tkv;
+  if (!a || !own_all_splits(a)) return TKV_EINVAL;
+  if (a->acc || a->maxs || a->sums || a->counters) return TKV_EINVAL;  // the partials are ours
+  if (a->B <= 0 || a->HQ <= 0 || a->D <= 0 || a->num_splits <= 0) return TKV_EINVAL;
+  tkv_decode_args s = *a;
+  if (a->num_splits > 1) {
+    const uint64_t rows = (uint64_t)a->B * (uint64_t)a->HQ * (uint64_t)a->num_splits;
+    const uint64_t acc_bytes = align256(rows * (uint64_t)a->D * 4);
+    const uint64_t ml_bytes = align256(rows * 4);
+    if (acc_bytes + 2 * ml_bytes > TKV_NOALLOC_SCRATCH_BYTES) return TKV_ESCRATCH;
+    void* base = nullptr;
+    const int rc = scratch_on_current_device(&base);
+    if (rc) return rc;
+    unsigned char* p = static_cast<unsigned char*>(base);
+    s.acc = reinterpret_cast<float*>(p);
+    s.maxs = reinterpret_cast<float*>(p + acc_bytes);
+    s.sums = reinterpret_cast<float*>(p + acc_bytes + ml_bytes);
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int rc = launch_fused_split(&s, st);
+  return rc ? rc : finish_combine(&s, st);
 }
 
 extern "C" int tkv_combine_splits(const float* acc, const float* maxs, const float* sums,

@@ -33,10 +33,13 @@ extern "C" const char* tkv_status_string(int status) {
     case TKV_EINVAL: return "invalid argument";
     case TKV_EUNSUPPORTED: return "unsupported head_dim / nbits / group_size combination";
     case TKV_ENODEVICE: return "no HIP device";
+    case TKV_ESCRATCH:
+      return "split partials exceed the static scratch of tkv_fused_decode_attention_noalloc "
+             "(TKV_NOALLOC_SCRATCH_BYTES)";
     default: break;
   }
   if (status > 0) return hipGetErrorString((hipError_t)status);
   return "unknown tritonkv_amd status";
 }
 
-extern "C" int tkv_abi_version(void) { return 5; }
+extern "C" int tkv_abi_version(void) { return 6; }
