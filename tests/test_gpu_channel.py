@@ -284,3 +284,43 @@ def test_channel_kv_cache_step_replays_in_a_graph():
     assert torch.equal(graphed.keys.zero[:, :, :nq // 32], ref.keys.zero[:, :, :nq // 32])
     assert torch.equal(graphed.values.packed[:, :, :nq], ref.values.packed[:, :, :nq])
     assert torch.equal(graphed.values.zero[:, :, :nq], ref.values.zero[:, :, :nq])
+
+
+def test_channel_kv_cache_replay_past_capacity_marks_the_row():
+    """Replayed steps are not counted on the host, so only the device guards the
+    capacity: the flush that would overrun the history writes nothing, moves no
+    length and marks the row (window length 33); further appends are refused
+    and the decode attends to the tokens held.  ``overflowed`` reports it."""
+    from tritonkv_amd.channel import ChannelKVCache
+
+    B, HQ, HKV, D = 2, 4, 1, 128
+    g = torch.Generator().manual_seed(31)
+    cache = ChannelKVCache(B, HKV, 64, D, k_nbits=4, v_nbits=4, group_size=32, device=DEV)
+    k = torch.randn(B, HKV, 33, D, generator=g).half().to(DEV)
+    cache.extend(k, k)  # one block + one window token
+    q = torch.randn(B, HQ, D, generator=g).half().to(DEV)
+    kb = torch.randn(B, HKV, 1, D, generator=g).half().to(DEV)
+    out = torch.empty(B, HQ, D, device=DEV)
+    cache.step(kb, kb, q, out=out)  # eager: window 2
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cache.step(kb, kb, q, out=out)
+    for _ in range(30):  # window 32 -> flushed into [32, 64): the history is full
+        graph.replay()
+    torch.cuda.synchronize()
+    assert not cache.overflowed()
+    assert cache._qlens.tolist() == [64, 64] and cache._rlens.tolist() == [0, 0]
+    history = [t.clone() for t in (cache.keys.packed, cache.values.packed)]
+    for _ in range(32):  # window fills again; its flush cannot fit
+        graph.replay()
+    torch.cuda.synchronize()
+    assert cache.overflowed()
+    assert cache._qlens.tolist() == [64, 64] and cache._rlens.tolist() == [33, 33]
+    assert torch.equal(cache.keys.packed, history[0]) and torch.equal(cache.values.packed, history[1])
+    graph.replay()  # a marked row stays as it is
+    torch.cuda.synchronize()
+    assert cache._rlens.tolist() == [33, 33]
+    assert torch.isfinite(out).all()
+    cache.reset()
+    assert not cache.overflowed()

@@ -64,3 +64,35 @@ def test_channel_key_mode_arguments():
     with pytest.raises(ValueError):
         hf.TkvLayer(64, nbits=4, keys="block")
     assert hf.TkvLayer(64, nbits=2, keys="channel").key_format == "channel"
+
+
+def test_padded_prefill_into_a_tkv_cache_is_refused():
+    """A left-padded batch (its mask hides key positions) cannot be stored with
+    one shared length: the prefill raises instead of letting decode attend to
+    the pad tokens.  An unpadded mask still prefills."""
+    from tritonkv_amd import hf
+
+    hf.register()
+    model = _model()
+    ids = torch.randint(0, 256, (2, 10), generator=torch.Generator().manual_seed(2))
+    mask = torch.ones(2, 10, dtype=torch.long)
+    mask[1, :3] = 0  # row 1 left-padded by 3 tokens
+    model.set_attn_implementation("tkv")
+    with torch.no_grad():
+        cache = hf.TkvCache(model.config, capacity=32, nbits=16)
+        with pytest.raises(NotImplementedError, match="padded batch"):
+            model(input_ids=ids, attention_mask=mask, past_key_values=cache, use_cache=True)
+        cache = hf.TkvCache(model.config, capacity=32, nbits=16)
+        model(input_ids=ids, attention_mask=torch.ones_like(mask), past_key_values=cache,
+              use_cache=True)
+    assert cache.get_seq_length() == 10
+    # the mask test itself: bool and additive forms, causal masking alone never counts
+    causal = torch.ones(4, 4, dtype=torch.bool).tril()[None, None]
+    assert not hf._masks_keys(None)
+    assert not hf._masks_keys(causal)
+    padded = causal.clone()
+    padded[..., :, 0] = False
+    assert hf._masks_keys(padded)
+    additive = torch.zeros(1, 1, 4, 4).masked_fill(~padded, float("-inf"))
+    assert hf._masks_keys(additive)
+    assert not hf._masks_keys(torch.zeros(1, 1, 4, 4).masked_fill(~causal, float("-inf")))

@@ -31,7 +31,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .kernels.fused_decode_attn import (_aligned16, _check_out, _seq_lens_arg, _workspace_for,
+from .kernels.fused_decode_attn import (_aligned16, _cache_arg, _check_out, _seq_lens_arg, _workspace_for,
                                         choose_waves, plan_splits, triton_available)
 from .quantize import QuantizedTensor, _check_bits, _require_gpu, append_kv, empty_cache
 
@@ -177,13 +177,16 @@ def channel_decode_attention(
     if q.dtype not in (torch.float16, torch.float32):
         q = q.float()
     q = _aligned16(q)
-    kr, vr = _aligned16(k_res.contiguous()), _aligned16(v_res.contiguous())
+    kr, vr = _cache_arg(k_res, 16, "k_res"), _cache_arg(v_res, 16, "v_res")
+    kp, vp = _cache_arg(ck.packed, 16, "ck.packed"), _cache_arg(vq.packed, 16, "vq.packed")
+    ks, kz, vs, vz = (_cache_arg(t, 4, n) for t, n in ((ck.scale, "ck.scale"), (ck.zero, "ck.zero"),
+                                                       (vq.scale, "vq.scale"), (vq.zero, "vq.zero")))
     out = _check_out(out, B, HQ, D, q.device)
     acc, maxs, sums, _ = _workspace_for(_workspace, B, HQ, num_splits + 1, D, q.device, HKV)
     args = _lib.DecodeArgs(
         q=q.data_ptr(), q_is_fp32=int(q.dtype == torch.float32),
-        k=ck.packed.data_ptr(), k_scale=ck.scale.data_ptr(), k_zero=ck.zero.data_ptr(),
-        v=vq.packed.data_ptr(), v_scale=vq.scale.data_ptr(), v_zero=vq.zero.data_ptr(),
+        k=kp.data_ptr(), k_scale=ks.data_ptr(), k_zero=kz.data_ptr(),
+        v=vp.data_ptr(), v_scale=vs.data_ptr(), v_zero=vz.data_ptr(),
         seq_lens=_lib.ptr(qlens), acc=_lib.ptr(acc), maxs=_lib.ptr(maxs), sums=_lib.ptr(sums),
         out=out.data_ptr(), B=B, HQ=HQ, HKV=HKV, S=S, D=D, k_nbits=ck.nbits,
         v_nbits=vq.nbits, group_size=vq.group_size, sm_scale=float(sm_scale),
@@ -207,7 +210,11 @@ class ChannelKVCache:
     the lengths and the flush decision kept on the device, so it allocates no
     host-dependent state and a captured step stays right when its graph is
     replayed for any window fill.  The host-side counters (``quantized``,
-    ``window``) follow eager calls only.
+    ``window``) follow eager calls only, so under replay only the device
+    guards the capacity: a full window that no longer fits the history is not
+    flushed and the row is marked (its device-side window length becomes 33);
+    from then on that row stores no new token.  :meth:`overflowed` reads the
+    marks (a host sync).
     """
 
     def __init__(self, B: int, HKV: int, capacity: int, D: int, k_nbits: int = 2,
@@ -239,6 +246,12 @@ class ChannelKVCache:
 
     def nbytes(self) -> int:
         return self.keys.nbytes() + self.values.nbytes() + 2 * self.k_res.numel() * 2
+
+    def overflowed(self) -> bool:
+        """Whether any row's window filled up with no room left in the history
+        (possible only through replayed steps, which the host does not count);
+        such a row has stopped storing tokens.  Synchronises with the device."""
+        return bool((self._rlens > BLOCK).any())
 
     def _check_tokens(self, k: torch.Tensor, v: torch.Tensor, n: int | None = None) -> None:
         B, HKV, _, D = self.k_res.shape

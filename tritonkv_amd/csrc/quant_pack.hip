@@ -324,7 +324,10 @@ channel_window_append_kernel(const uint16_t* __restrict__ k_new, const uint16_t*
 // quantizes the blocks of kv heads w, w + 4, ...: keys per channel
 // (quantize_key_block), values per token (quantize_row, as the append kernel)
 // into the history at q_lens[b]; then q_lens[b] += 32 and res_lens[b] = 0.
-// A block that does not fit [0, S_cap) is not written (the lengths still move).
+// A window that does not fit the history ([q, q + 32) outside [0, S_cap)) is
+// not written and the lengths do not move: res_lens[b] becomes 33, the
+// overflow mark, which the append kernel treats as full (nothing more is
+// appended) and the decode clamps to the 32 tokens the window holds.
 template <int D, int KNB, int VNB, int GS>
 __global__ void __launch_bounds__(256)
 channel_window_flush_kernel(const uint16_t* __restrict__ k_res, const uint16_t* __restrict__ v_res,
@@ -339,7 +342,11 @@ channel_window_flush_kernel(const uint16_t* __restrict__ k_res, const uint16_t* 
   if (res_lens[b] != T) return;  // whole workgroup
   const int q = q_lens[b];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const bool ok = q >= 0 && q % T == 0 && q + T <= S_cap;
+  if (!(q >= 0 && q % T == 0 && q + T <= S_cap)) {  // uniform over the workgroup
+    if (threadIdx.x == 0) res_lens[b] = T + 1;
+    return;
+  }
+  const bool ok = true;
   for (int kv = w; kv < HKV; kv += 4) {
     const int64_t bh = (int64_t)b * HKV + kv;
     quantize_key_block<D, KNB, false>(k_res, bh * T * D, lane, ok, kp, bh * S_cap + q, ks, kz,
@@ -348,7 +355,6 @@ channel_window_flush_kernel(const uint16_t* __restrict__ k_res, const uint16_t* 
       float x[R::P];
       load_row_for_quant<D, VNB>(v_res + (bh * T + t) * D, false, lane, x);
       const R r = quantize_row<D, VNB, GS>(x, lane);
-      if (!ok) continue;
       const int64_t row = bh * S_cap + q + t;
       if (lane < VDP) vp[row * VDP + lane] = (uint8_t)r.byte;
       if (lane < VNG) {

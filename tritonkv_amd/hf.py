@@ -30,8 +30,10 @@ Usage::
     cache = hf.TkvCache(model.config, capacity=8192, nbits=4)
     out = model.generate(input_ids, past_key_values=cache, max_new_tokens=64)
 
-All rows of a batch share one length (no padding).  Chunked prefill into a
-non-empty cache is not supported.  ``transformers`` is imported lazily, so the
+All rows of a batch share one length: a prefill whose mask hides key
+positions (a left-padded batch) raises ``NotImplementedError`` rather than
+letting decode attend to the pad tokens.  Chunked prefill into a non-empty
+cache is not supported.  ``transformers`` is imported lazily, so the
 rest of the package does not depend on it.
 """
 
@@ -124,6 +126,7 @@ class TkvLayer(_LayerBase):
             append_kv(self.vc, value_states.to(torch.float16).contiguous())
         self.length = n
         self.lens.fill_(n)
+        key_states._tkv_prefill = self
         return key_states, value_states
 
     # -- sizes -------------------------------------------------------------------
@@ -191,6 +194,18 @@ class TkvCache(_Cache):
         return total
 
 
+def _masks_keys(mask) -> bool:
+    """Whether a prefill mask hides any key position from the prompt's last
+    query (padding; causal masking never hides a key from the last query).
+    ``mask``: None, bool (True = attend) or additive float, (..., q_len, kv_len)."""
+    if mask is None:
+        return False
+    last = mask[..., -1, :]
+    if last.dtype == torch.bool:
+        return not bool(last.all())
+    return bool((last < 0).any())
+
+
 def tkv_attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kwargs):
     """``AttentionInterface`` entry: (B, HQ, q_len, D) query -> (B, q_len, HQ, D)."""
     layer = getattr(key, "_tkv_layer", None)
@@ -199,6 +214,11 @@ def tkv_attention(module, query, key, value, attention_mask, scaling=None, dropo
     if layer is not None and query.shape[2] == 1:
         return layer.decode(module, query, key, value, scaling), None
     # prefill (or no TkvCache): fp16 SDPA over the given keys and values
+    if getattr(key, "_tkv_prefill", None) is not None and _masks_keys(attention_mask):
+        raise NotImplementedError(
+            "TkvCache keeps one length for every row of the batch, and decode attends to "
+            "every cached token: a prompt mask that hides key positions (a padded batch) "
+            "would put the pad tokens into every decode step. Prefill rows of equal length.")
     groups = query.shape[1] // key.shape[1]
     if groups > 1:
         key = key.repeat_interleave(groups, dim=1)

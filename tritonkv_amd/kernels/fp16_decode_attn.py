@@ -1,12 +1,21 @@
 """fp16 flash-decoding attention on MI355X -- the *control* for the fused kernel.
 
 Drop-in for the reference's ``kernels/fp16_decode_attn.py``
-(``fp16_decode_attention`` :142-241).  It uses the same split arithmetic and
-workspace as the fused path and the same C-ABI skeleton
-(``tkv_fp16_decode_attention``): identical split, online softmax, GQA grouping,
-workgroup merge and combine kernel, with K/V read as fp16 instead of being
-unpacked -- so fused vs control isolates the quantization effect, and SDPA vs
-control the flash-decoding effect (reference :1-25).
+(``fp16_decode_attention`` :142-241).  It shares the fused path's split
+arithmetic, workspace, C-ABI skeleton (``tkv_fp16_decode_attention``), online
+softmax, GQA grouping, workgroup merge and combine kernel.  Two differences
+besides the unpack remain, both deliberate:
+
+* the default split targets 256 tokens per workgroup instead of 512 (an fp16
+  token is 3-6x the bytes of a packed one); ``num_splits=`` set to the fused
+  call's count gives the reference's identical split (``:161-163``), and the
+  benchmark reports the quantization effect both ways;
+* K/V rows are prefetched into registers (16-byte non-temporal loads, one
+  chunk ahead) rather than staged through LDS: two LDS stages of fp16 chunks
+  per wave would not fit 8 waves in a CU's LDS.
+
+So fused vs control isolates the quantization effect, and SDPA vs control the
+flash-decoding effect (reference :1-25).
 """
 
 from __future__ import annotations
@@ -19,6 +28,7 @@ from .. import _lib
 from .fused_decode_attn import (
     TOKENS_PER_WORKGROUP_FP16,
     _aligned16,
+    _cache_arg,
     _check_out,
     _seq_lens_arg,
     _workspace_for,
@@ -68,8 +78,8 @@ def fp16_decode_attention(
     if q.dtype not in (torch.float16, torch.float32):
         q = q.float()
     q = _aligned16(q)
-    k = _aligned16(k if k.dtype == torch.float16 else k.half())
-    v = _aligned16(v if v.dtype == torch.float16 else v.half())
+    k = _cache_arg(k if k.dtype == torch.float16 else k.half(), 16, "k")
+    v = _cache_arg(v if v.dtype == torch.float16 else v.half(), 16, "v")
     out = _check_out(out, B, HQ, D, q.device)
     acc, maxs, sums, counters = _workspace_for(_workspace, B, HQ, num_splits, D, q.device, HKV)
     lens = _seq_lens_arg(seq_lens, B, S, q.device)

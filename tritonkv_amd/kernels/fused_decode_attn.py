@@ -206,9 +206,27 @@ def _workspace_for(ws: dict | None, B: int, HQ: int, num_splits: int, D: int, de
 
 
 def _aligned16(t: torch.Tensor) -> torch.Tensor:
-    """Contiguous and 16-byte aligned (the kernels load rows as 16-byte vectors)."""
+    """q (a few KB) as the kernels load it: contiguous and 16-byte aligned,
+    copied if it is not."""
     t = t.contiguous()
     return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def _cache_arg(t: torch.Tensor, align: int, name: str, written: bool = False) -> torch.Tensor:
+    """A cache tensor as the kernels take it.  A non-contiguous cache that is
+    only read is made contiguous, as the reference does (``:489-491``; that is
+    a copy of the cache); one the step writes into (the fused append) must be
+    contiguous already, or the token would land in a temporary copy.  Caches
+    are never realigned: codes and fp16 rows need 16-byte, scale/zero 4-byte
+    aligned storage, which every contiguous allocation has."""
+    if not t.is_contiguous():
+        if written:
+            raise ValueError(f"{name} must be contiguous: the step writes the new token into it")
+        t = t.contiguous()
+    if t.data_ptr() % align:
+        raise ValueError(f"{name} must start on a {align}-byte boundary "
+                         f"(data_ptr % {align} = {t.data_ptr() % align})")
+    return t
 
 
 def _check_out(out, B, HQ, D, device):
@@ -307,6 +325,12 @@ def fused_decode_attention(
     if kq.packed.device != q.device or vq.packed.device != q.device:
         raise ValueError("q and the K/V caches must be on the same device")
     kn, vn, new_f32 = new_token_args(k_new, v_new, B, HKV, D, q.device)
+    w = kn is not None
+    kp, vp = (_cache_arg(t.packed, 16, f"{n}.packed", w) for t, n in ((kq, "kq"), (vq, "vq")))
+    ks, kz, vs, vz = (_cache_arg(t, 4, n, w) for t, n in ((kq.scale, "kq.scale"),
+                                                          (kq.zero, "kq.zero"),
+                                                          (vq.scale, "vq.scale"),
+                                                          (vq.zero, "vq.zero")))
 
     ok, why = triton_available()
     if not ok:
@@ -320,8 +344,6 @@ def fused_decode_attention(
     if q.dtype not in (torch.float16, torch.float32):
         q = q.float()
     q = _aligned16(q)
-    kp, ks, kz = _aligned16(kq.packed), _aligned16(kq.scale), _aligned16(kq.zero)
-    vp, vs, vz = _aligned16(vq.packed), _aligned16(vq.scale), _aligned16(vq.zero)
     out = _check_out(out, B, HQ, D, q.device)
     acc, maxs, sums, counters = _workspace_for(_workspace, B, HQ, num_splits, D, q.device, HKV)
     lens = _seq_lens_arg(seq_lens, B, S, q.device)
