@@ -146,6 +146,16 @@ int tkv_fused_decode_attention_noalloc(const tkv_decode_args *args, tkv_stream_t
 int tkv_fused_decode_split(const tkv_decode_args *args, tkv_stream_t stream);
 int tkv_fp16_decode_split(const tkv_decode_args *args, tkv_stream_t stream);
 
+/* Read-ceiling probe of the quantized split kernel: the same grid, waves,
+ * chunk order, two-stage ring and direct-to-LDS loads over the same
+ * contiguous caches (args as for tkv_fused_decode_split; no paged caches,
+ * fused append or per-channel keys), with no arithmetic behind them, so its
+ * duration gives the bandwidth that access pattern can stream.  Writes nothing
+ * the caller reads (out[blockIdx.x] only on a sentinel sum).  The measurement
+ * counterpart, for this kernel's reads, of the reference's device-copy
+ * bandwidth probe (benchmark.py:1160-1222). */
+int tkv_read_probe(const tkv_decode_args *args, tkv_stream_t stream);
+
 /* Log-sum-exp merge of split partials into out, as _combine_splits
  * (kernels/fused_decode_attn.py:355-395, launched at :558-568). */
 int tkv_combine_splits(const float *acc, const float *maxs, const float *sums, float *out,
@@ -224,7 +234,10 @@ int tkv_quantize_keys_channel(const void *x, int32_t x_is_fp32, int32_t B, int32
  * window is quantized into the history at token q_lens[b] -- keys per channel
  * exactly as tkv_quantize_keys_channel, values per token exactly as
  * tkv_quantize_pack (V group_size 16 or 32) -- then q_lens[b] += 32 and
- * res_lens[b] = 0.  Other rows are untouched.  No counterpart in the
+ * res_lens[b] = 0.  Other rows are untouched.  A full window that does not
+ * fit the history (q_lens[b] + 32 > S_cap) is not written and no length
+ * moves: res_lens[b] becomes 33, a device-side overflow mark that the append
+ * treats as full and the decode clamps to the window's 32 tokens.  No counterpart in the
  * reference (it plans the format, docs/future_work.md:229-293). */
 int tkv_channel_window_append(const void *k_new, const void *v_new, int32_t B, int32_t HKV,
                               int32_t D, void *k_res, void *v_res, int32_t res_cap,
@@ -273,8 +286,8 @@ const char *tkv_status_string(int status);
  * paged-cache fields of tkv_decode_args and tkv_paged_quantize_pack, 4 the
  * fused-append fields, 5 the per-channel key and partials-placement fields,
  * tkv_quantize_keys_channel, tkv_channel_decode_attention and the
- * tkv_channel_window_* calls, 6 tkv_fused_decode_attention_noalloc and
- * TKV_ESCRATCH). */
+ * tkv_channel_window_* calls, 6 tkv_fused_decode_attention_noalloc,
+ * TKV_ESCRATCH and tkv_read_probe). */
 int tkv_abi_version(void);
 
 #ifdef __cplusplus

@@ -93,6 +93,7 @@ SIGNATURES = {
     "tkv_fp16_decode_attention": ([ctypes.POINTER(DecodeArgs), _P], ctypes.c_int),
     "tkv_fused_decode_attention_noalloc": ([ctypes.POINTER(DecodeArgs), _P], ctypes.c_int),
     "tkv_fused_decode_split": ([ctypes.POINTER(DecodeArgs), _P], ctypes.c_int),
+    "tkv_read_probe": ([ctypes.POINTER(DecodeArgs), _P], ctypes.c_int),
     "tkv_fp16_decode_split": ([ctypes.POINTER(DecodeArgs), _P], ctypes.c_int),
     "tkv_combine_splits": ([_P, _P, _P, _P, _I32, _I32, _I32, _I32, _P], ctypes.c_int),
     "tkv_quantize_pack": ([_P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _P, _I32, _P, _P, _P, _P],

@@ -452,16 +452,26 @@ static dim3 split_grid(const tkv_decode_args* a) {
 // file per K/V bit-width pair, so the instantiations build in parallel).
 template <int D, int KNB, int VNB, int GS>
 void launch_quant(const SplitParams& p, dim3 grid, int waves, hipStream_t st);
+template <int D, int KNB, int VNB, int GS>
+void launch_read_probe(const SplitParams& p, dim3 grid, int waves, hipStream_t st);
+
+// probe: the read-ceiling probe of the same instantiation instead of the kernel
+template <int D, int KNB, int VNB, int GS>
+static void launch_one(bool probe, const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
+  if (probe) launch_read_probe<D, KNB, VNB, GS>(p, grid, waves, st);
+  else launch_quant<D, KNB, VNB, GS>(p, grid, waves, st);
+}
 
 template <int D, int KNB, int VNB>
-static int dispatch_gs(const SplitParams& p, dim3 grid, int gs, int waves, hipStream_t st) {
+static int dispatch_gs(const SplitParams& p, dim3 grid, int gs, int waves, hipStream_t st,
+                       bool probe) {
   switch (gs) {
-    case 16: launch_quant<D, KNB, VNB, 16>(p, grid, waves, st); return TKV_OK;
-    case 32: launch_quant<D, KNB, VNB, 32>(p, grid, waves, st); return TKV_OK;
-    case 64: launch_quant<D, KNB, VNB, 64>(p, grid, waves, st); return TKV_OK;
+    case 16: launch_one<D, KNB, VNB, 16>(probe, p, grid, waves, st); return TKV_OK;
+    case 32: launch_one<D, KNB, VNB, 32>(probe, p, grid, waves, st); return TKV_OK;
+    case 64: launch_one<D, KNB, VNB, 64>(probe, p, grid, waves, st); return TKV_OK;
     case 128:
       if constexpr (D >= 128) {
-        launch_quant<D, KNB, VNB, 128>(p, grid, waves, st);
+        launch_one<D, KNB, VNB, 128>(probe, p, grid, waves, st);
         return TKV_OK;
       }
       return TKV_EUNSUPPORTED;
@@ -471,11 +481,11 @@ static int dispatch_gs(const SplitParams& p, dim3 grid, int gs, int waves, hipSt
 
 template <int D>
 static int dispatch_bits(const SplitParams& p, dim3 grid, int knb, int vnb, int gs, int waves,
-                         hipStream_t st) {
-  if (knb == 4 && vnb == 4) return dispatch_gs<D, 4, 4>(p, grid, gs, waves, st);
-  if (knb == 2 && vnb == 2) return dispatch_gs<D, 2, 2>(p, grid, gs, waves, st);
-  if (knb == 4 && vnb == 2) return dispatch_gs<D, 4, 2>(p, grid, gs, waves, st);
-  if (knb == 2 && vnb == 4) return dispatch_gs<D, 2, 4>(p, grid, gs, waves, st);
+                         hipStream_t st, bool probe = false) {
+  if (knb == 4 && vnb == 4) return dispatch_gs<D, 4, 4>(p, grid, gs, waves, st, probe);
+  if (knb == 2 && vnb == 2) return dispatch_gs<D, 2, 2>(p, grid, gs, waves, st, probe);
+  if (knb == 4 && vnb == 2) return dispatch_gs<D, 4, 2>(p, grid, gs, waves, st, probe);
+  if (knb == 2 && vnb == 4) return dispatch_gs<D, 2, 4>(p, grid, gs, waves, st, probe);
   return TKV_EUNSUPPORTED;
 }
 
@@ -507,9 +517,10 @@ static int status_of_launch() {
 
 namespace tkv {
 
-static int launch_fused_split(const tkv_decode_args* a, hipStream_t st) {
+static int launch_fused_split(const tkv_decode_args* a, hipStream_t st, bool probe = false) {
   int rc = validate_common(a);
   if (rc) return rc;
+  if (probe && (a->page_size > 0 || a->k_new || a->key_block)) return TKV_EUNSUPPORTED;
   if (!a->k_scale || !a->k_zero || !a->v_scale || !a->v_zero) return TKV_EINVAL;
   const int gs = a->group_size;
   if (gs <= 0 || gs > a->D || a->D % gs) return TKV_EINVAL;
@@ -519,8 +530,8 @@ static int launch_fused_split(const tkv_decode_args* a, hipStream_t st) {
   const SplitParams p = make_params(a);
   const dim3 grid = split_grid(a);
   (void)hipGetLastError();
-  rc = a->D == 128 ? dispatch_bits<128>(p, grid, a->k_nbits, a->v_nbits, gs, a->waves, st)
-                   : dispatch_bits<64>(p, grid, a->k_nbits, a->v_nbits, gs, a->waves, st);
+  rc = a->D == 128 ? dispatch_bits<128>(p, grid, a->k_nbits, a->v_nbits, gs, a->waves, st, probe)
+                   : dispatch_bits<64>(p, grid, a->k_nbits, a->v_nbits, gs, a->waves, st, probe);
   if (rc) return rc;
   return status_of_launch();
 }
@@ -558,6 +569,10 @@ static int finish_combine(const tkv_decode_args* a, hipStream_t st) {
 
 extern "C" int tkv_fused_decode_split(const tkv_decode_args* a, tkv_stream_t stream) {
   return tkv::launch_fused_split(a, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int tkv_read_probe(const tkv_decode_args* a, tkv_stream_t stream) {
+  return tkv::launch_fused_split(a, reinterpret_cast<hipStream_t>(stream), true);
 }
 
 extern "C" int tkv_fp16_decode_split(const tkv_decode_args* a, tkv_stream_t stream) {

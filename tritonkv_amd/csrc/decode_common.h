@@ -211,10 +211,20 @@ __device__ __forceinline__ void wave_lds_fence() {
 
 
 // ---------------------------------------------------------------------------
-// Q^T as the B operand of the score MFMAs, in K slot order and pre-scaled by
-// 2^-(slice*KNB), plus the B operand of the K zero-point MFMA.  Lane-group j's
-// dims of step m are the contiguous run [m*KSTEP + CB*j, +CB): one vector load
-// per step, then slot order.  Lanes of heads >= nh hold zeros.
+// Q^T as the B operand of the score MFMAs, in K slot order, plus the B operand
+// of the K zero-point MFMA.  Lane-group j's dims of step m are the contiguous
+// run [m*KSTEP + CB*j, +CB): one vector load per step, then slot order.  Lanes
+// of heads >= nh hold zeros.
+//
+// Prescale.  Slice p of a packed byte enters the MFMA as the fp16 subnormal
+// c * 2^(p*KNB - 24), so q is scaled by 2^(eh - p*KNB) to give every slice the
+// same weight 2^(eh - 24).  eh is chosen per head, as large as EMAX and
+// max|q| * 2^eh < 2^15 allow: scaling *up* by a power of two is exact, while
+// scaling down (eh = 0) pushes |q| < 2^(p*KNB - 14) into fp16's subnormal
+// range and costs absolute precision -- at 2 bits, slice 3's q * 2^-6 kept
+// only 2^-18 of q, which against scale * code ~ 60 in outlier groups put
+// scores 1e-4 off and outputs 2-3e-3 off.  The kernel scales the code dots by
+// 2^(24 - eh) (zsc, lsc).
 // ---------------------------------------------------------------------------
 template <int D, int KNB, int GS>
 struct QOperands {
@@ -223,9 +233,15 @@ struct QOperands {
   // The same dims of step m in natural order, unscaled fp16 pairs (CB/2 used):
   // for per-channel keys, whose zero-point term is a dot product with q.
   u4 qn[KLayout<D, KNB, GS>::NKM];
+  int eh;  // this lane's head's prescale exponent
 };
 
-template <int D, int KNB, int GS>
+// Largest exponent e <= emax with amax * 2^e < 2^15 (amax >= 0).
+__device__ __forceinline__ int q_prescale_exp(float amax, int emax) {
+  return min(emax, 15 - __builtin_amdgcn_frexp_expf(amax));
+}
+
+template <int D, int KNB, int GS, int EMAX>
 __device__ __forceinline__ void load_q_operands(const SplitParams& prm, int b, int h0, int n, int nh,
                                                 int j, QOperands<D, KNB, GS>& qo) {
   using KL = KLayout<D, KNB, GS>;
@@ -265,10 +281,16 @@ __device__ __forceinline__ void load_q_operands(const SplitParams& prm, int b, i
         }
       }
     }
+    float amax = 0.0f;
+#pragma unroll
+    for (int m = 0; m < NKM; ++m)
+#pragma unroll
+      for (int c = 0; c < KL::CB; ++c) amax = fmaxf(amax, hv ? fabsf(qv[m][c]) : 0.0f);
+    qo.eh = q_prescale_exp(xor_max16_32(amax), EMAX);
 #pragma unroll
     for (int m = 0; m < NKM; ++m) {
       const int p = KL::slice_of(m, j);
-      const float pre = __builtin_ldexpf(1.0f, -p * KNB);
+      const float pre = __builtin_ldexpf(1.0f, qo.eh - p * KNB);
       uint32_t wv[4] = {0, 0, 0, 0};
 #pragma unroll
       for (int s2 = 0; s2 < KL::CB; s2 += 2) {

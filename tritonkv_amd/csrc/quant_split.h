@@ -213,6 +213,7 @@ struct QOperandsPT {
   static constexpr int NB = D / 16;   // 16-dim blocks: block p * NU + u = unit u of slice p
   u4 qb[NB];
   u4 qzb;  // zero-point MFMA (K = 32): slots 8j + g hold hi (j even) or lo (j odd) of sum q_g
+  int eh;  // this lane's head's prescale exponent (as QOperands::eh)
 };
 
 template <int D, int KNB, int GS>
@@ -252,12 +253,19 @@ __device__ __forceinline__ void load_q_operands_pt(const SplitParams& prm, int b
       for (int e = 0; e < 8; ++e) qv[bi][e] = (float)v[e];
     }
   }
+  // lanes j and j ^ 1 hold the two halves of each 16-dim block of the head
+  float amax = 0.0f;
+#pragma unroll
+  for (int bi = 0; bi < QO::NB; ++bi)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, hv ? fabsf(qv[bi][e]) : 0.0f);
+  qo.eh = q_prescale_exp(fmaxf(amax, __shfl_xor(amax, 16, 64)), (QO::P - 1) * KNB);
 #pragma unroll
   for (int p = 0; p < QO::P; ++p)
 #pragma unroll
     for (int u = 0; u < QO::NU; ++u) {
       const int g = (p * QO::DP + 16 * u) / GS;
-      const float pre = __builtin_ldexpf(1.0f, -p * KNB);
+      const float pre = __builtin_ldexpf(1.0f, qo.eh - p * KNB);
       uint32_t wv[4];
 #pragma unroll
       for (int s2 = 0; s2 < 8; s2 += 2) {
@@ -289,7 +297,7 @@ __device__ __forceinline__ void load_q_operands_pt(const SplitParams& prm, int b
 // head); the head's 32 tokens span lanes c and c ^ 8 of all four lane groups.
 // Returns whether any running max moved; ph holds the lane's fp16 pairs.
 __device__ __forceinline__ bool softmax_chunk_pt(const float (&x)[4], float lscale, float& m,
-                                                 float& alpha, uint32_t (&ph)[2]) {
+                                                 float& alpha, uint32_t (&ph)[2], float (&p)[4]) {
   float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
   mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
   mx = xor_max16_32(mx) * lscale;
@@ -301,7 +309,6 @@ __device__ __forceinline__ bool softmax_chunk_pt(const float (&x)[4], float lsca
     alpha = safe_exp2_diff(m, mn);
     m = mn;
   }
-  float p[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(fmaf(x[i], lscale, -m));
   ph[0] = pack_h2(p[0], p[1]);
@@ -322,6 +329,19 @@ struct LdsKernelSmem {
   static constexpr int PATCH_META = SG::KL::DP + SG::VL::DP;
   static constexpr int PATCH = (PATCH_META + 4 * SG::NG * 2 + 15) / 16 * 16;
 };
+
+// Probabilities enter the PV products as fp16 (B operands of the MFMAs), as
+// they do in the reference's tl.dot.  Their rounding reaches the output as
+// about 2^-11 * |v| / sqrt(L) for a row of L tokens, whichever chunk it falls
+// in, so rows of at most kHiLoMaxLen tokens take them as hi/lo fp16 pairs in
+// every chunk -- P = pb + pbl and P * s_g = pg + pgl to about 22 bits, one
+// more MFMA per product.  Measured with x8 outliers (2-bit codes): 33 tokens
+// 2.1e-3 -> 1.5e-4 max-abs; 2-5 tokens up to 2^-10 * max|v| -> 5e-5.  Longer
+// rows keep fp16 P: at 256 tokens the estimate is already about 8e-4 at the
+// same values, and the pairs cost 0.15-0.4 us per latency-bound Qwen-shape
+// step and 9-18% at the DRAM-bound Llama-3-8B shape.
+constexpr int kHiLoMaxLen = 256;
+
 
 template <int D, int KNB, int VNB, int GS, int NW, int NSTAGE, bool PAGED, bool PT, bool KCH = false>
 __global__ void __launch_bounds__(NW * 64)
@@ -433,8 +453,13 @@ quant_split_lds_kernel(SplitParams prm) {
   using QP = QOperandsPT<D, KNB, GS>;
   QOperands<D, KNB, GS> qo;
   QP qpt;
+  // Per-channel keys multiply q by the chunk's channel scales in fp16 (q * s
+  // as hi/lo pairs), so their q keeps eh = 0: a larger prescale could
+  // overflow there.
   if constexpr (PT) load_q_operands_pt<D, KNB, GS>(prm, b, h0, r, nh, j, qpt);
-  else load_q_operands<D, KNB, GS>(prm, b, h0, n, nh, j, qo);
+  else load_q_operands<D, KNB, GS, KCH ? 0 : (KL::P - 1) * KNB>(prm, b, h0, n, nh, j, qo);
+  const int eh = PT ? qpt.eh : qo.eh;
+  const float zsc = __builtin_ldexpf(1.0f, eh - 24);  // code-dot units per score unit
   const u4* qf = qo.qf;
   const u2 qzb = qo.qzb;
 
@@ -534,7 +559,7 @@ quant_split_lds_kernel(SplitParams prm) {
   for (int mv = 0; mv < NVM; ++mv) accv[mv] = f4{0.f, 0.f, 0.f, 0.f};
   f4 oz = f4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.0f;
-  const float lscale = prm.qk_scale * kTwo24;
+  const float lscale = prm.qk_scale * __builtin_ldexpf(1.0f, 24 - eh);  // per lane (its head)
 
   // In the tail chunk, rows past the sequence hold whatever the cache holds
   // there (possibly NaN/Inf bit patterns in scale/zero): their V scale and
@@ -552,9 +577,11 @@ quant_split_lds_kernel(SplitParams prm) {
 
   // Chunk k of the wave uses stage k % NSTAGE; the loop below is unrolled by
   // NSTAGE so every stage offset is a compile-time constant.
-  auto step = [&](int cb, auto tail, auto stage) __attribute__((always_inline)) {
+  auto step = [&](int cb, auto tail, auto stage, auto hilo) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail)::value;
     constexpr int SK = decltype(stage)::value;
+    // hi/lo probabilities in the PV products (see kHiLoMaxLen)
+    constexpr bool HILO = decltype(hilo)::value;
     // refill the stage consumed by the previous chunk, NSTAGE-1 chunks ahead
     {
       const int cn = cb + (NSTAGE - 1) * cstride;
@@ -595,6 +622,7 @@ quant_split_lds_kernel(SplitParams prm) {
     const uint8_t* mvz = mvs + SG::MB;
 
     u4 pb;  // P^T in the PV MFMA's B layout: lane (j, c) holds tokens slot_token(j, .) of head c
+    u4 pbl = u4{0u, 0u, 0u, 0u};  // HILO: the fp16 remainders P - pb, same layout
     if constexpr (PT) {
       // ---- scores: both tiles in one set of MFMAs (paired tiles) ----------
       float x[4];  // tokens 16 * tile + 4j + i of head c & 7, tile = c >> 3
@@ -636,7 +664,7 @@ quant_split_lds_kernel(SplitParams prm) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int t = tile_pt + 4 * j + i;
-          float sc = yz[i] * kTwoM24;
+          float sc = yz[i] * zsc;
 #pragma unroll
           for (int g = 0; g < NG; ++g) {
             const float sv =
@@ -654,14 +682,20 @@ quant_split_lds_kernel(SplitParams prm) {
       // ---- online softmax ---------------------------------------------------
       float alpha;
       uint32_t ph[2];
-      if (softmax_chunk_pt(x, lscale, m_run, alpha, ph)) {
+      float pf[4];
+      if (softmax_chunk_pt(x, lscale, m_run, alpha, ph, pf)) {
 #pragma unroll
         for (int mv = 0; mv < NVM; ++mv) accv[mv] *= alpha;
         oz *= alpha;
+
       }
       // tile 0 of head c is this lane's (c < 8), tile 1 is lane c + 8's
       pb = u4{ph[0], ph[1], (uint32_t)__shfl_xor((int)ph[0], 8, 64),
               (uint32_t)__shfl_xor((int)ph[1], 8, 64)};
+      if constexpr (HILO) {
+        const uint32_t l0 = pack_h2_rem(pf[0], pf[1], ph[0]), l1 = pack_h2_rem(pf[2], pf[3], ph[1]);
+        pbl = u4{l0, l1, (uint32_t)__shfl_xor((int)l0, 8, 64), (uint32_t)__shfl_xor((int)l1, 8, 64)};
+      }
     } else {
       // ---- scores S^T for the two 16-token tiles ---------------------------
       float x[8];
@@ -705,7 +739,7 @@ quant_split_lds_kernel(SplitParams prm) {
           if constexpr (KL::CB == 8) cz = mfma_k32(zn, qo.qn[m], cz);
           else cz = mfma_k16(u2{zn[0], zn[1]}, u2{qo.qn[m][0], qo.qn[m][1]}, cz);
         }
-        const float bias24 = cz[0] * kTwoM24;
+        const float bias24 = cz[0] * zsc;
   #pragma unroll
         for (int a = 0; a < 2; ++a) {
           f4 c = f4{0.f, 0.f, 0.f, 0.f};
@@ -774,7 +808,7 @@ quant_split_lds_kernel(SplitParams prm) {
   #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int t = 16 * a + 4 * j + i;
-          float sc = yz[i] * kTwoM24;
+          float sc = yz[i] * zsc;
   #pragma unroll
           for (int g = 0; g < NG; ++g) {
             const float sv = (float)__builtin_bit_cast(_Float16, (uint16_t)half_at(mks, t * SG::MROW + g));
@@ -799,8 +833,13 @@ quant_split_lds_kernel(SplitParams prm) {
   #pragma unroll
         for (int mv = 0; mv < NVM; ++mv) accv[mv] *= alpha;
         oz *= alpha;
+
       }
       pb = u4{pr.ph[0], pr.ph[1], pr.ph[2], pr.ph[3]};
+      if constexpr (HILO) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pbl[i] = pack_h2_rem(pr.p[2 * i], pr.p[2 * i + 1], pr.ph[i]);
+      }
     }
 
     // ---- V zero point: oz += Z^T P (A rows = groups, k = the lane's 8 tokens)
@@ -814,9 +853,11 @@ quant_split_lds_kernel(SplitParams prm) {
         zp[q] |= zones;
       }
       oz = mfma_k32(u4{zp[0], zp[1], zp[2], zp[3]}, pb, oz);
+      if constexpr (HILO) oz = mfma_k32(u4{zp[0], zp[1], zp[2], zp[3]}, pbl, oz);
     }
     // ---- P'_g = P * s_g ------------------------------------------------------
     u4 pg[NG];
+    u4 pgl[HILO ? NG : 1];
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       uint32_t sp[4];
@@ -827,6 +868,13 @@ quant_split_lds_kernel(SplitParams prm) {
         if constexpr (TAIL) sp[q] &= tail_pair_mask(cb + t0, cb + t1);
       }
       pg[g] = u4{pk_mul(pb[0], sp[0]), pk_mul(pb[1], sp[1]), pk_mul(pb[2], sp[2]), pk_mul(pb[3], sp[3])};
+      if constexpr (HILO) {
+        // P * s = pg + (pb * s - pg) + pbl * s: the exact remainder of the
+        // fp16 product plus the low part's product, summed in fp16
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          pgl[g][q] = pk_add(pk_fma_rem(pb[q], sp[q], pg[g][q]), pk_mul(pbl[q], sp[q]));
+      }
     }
 
     // ---- O^T += V^T P'^T ---------------------------------------------------
@@ -845,17 +893,25 @@ quant_split_lds_kernel(SplitParams prm) {
         for (int i = 0; i < 4; ++i) pm[i] = perm(vx[2 * i + 1], vx[2 * i], vsel[e]);
         // With one group per row (NG == 1) every slice of a byte shares the
         // same P', so slice p's MFMA may take the byte with only the slices
-        // below p cleared (p = 0: the raw byte): its accumulator holds the
-        // codes of slices >= p at their bit positions, and slice p alone is
-        // recovered after the loop as acc[p] - acc[p + 1] -- one AND fewer
-        // per byte pair.  Otherwise each slice is isolated by its own mask.
+        // above p cleared (the top slice: the raw byte): its accumulator holds
+        // the codes of slices <= p at their bit positions, and slice p alone
+        // is recovered after the loop as acc[p] - acc[p - 1] -- one AND fewer
+        // per byte pair.  Slices below p weigh less than slice p's own code
+        // (c * 2^(p*VNB) against at most 2^(p*VNB) - 1), so that difference
+        // loses at most about one bit of the accumulators' precision.  (The
+        // other direction, clearing the slices below p and subtracting
+        // acc[p + 1], leaves slice 0 as the small difference of two sums of
+        // whole bytes: up to ~85x the rounding at 2 bits, measured 2.8e-3
+        // max-abs on the Llama-3-8B shape with outlier channels.)  Otherwise
+        // each slice is isolated by its own mask.
 #pragma unroll
         for (int p = 0; p < VL::P; ++p) {
           const int mv = VL::mfma_index(p, wi, e);
-          const uint32_t msk = kVChain ? hi_slices_mask<VNB>(p) : slice_mask<VNB>(p);
-          const u4 av = (kVChain && p == 0) ? u4{pm[0], pm[1], pm[2], pm[3]}
-                                            : u4{pm[0] & msk, pm[1] & msk, pm[2] & msk, pm[3] & msk};
+          const uint32_t msk = kVChain ? lo_slices_mask<VNB>(p) : slice_mask<VNB>(p);
+          const u4 av = (kVChain && p == VL::P - 1) ? u4{pm[0], pm[1], pm[2], pm[3]}
+                                                    : u4{pm[0] & msk, pm[1] & msk, pm[2] & msk, pm[3] & msk};
           accv[mv] = mfma_k32(av, pg[VL::group_of(mv)], accv[mv]);
+          if constexpr (HILO) accv[mv] = mfma_k32(av, pgl[VL::group_of(mv)], accv[mv]);
         }
       }
     }
@@ -866,24 +922,29 @@ quant_split_lds_kernel(SplitParams prm) {
   // chunk holding the last token, which always runs as the TAIL step (even
   // when it is full).  A single loop exit keeps the accumulators in place
   // across the unrolled copies.
-  int cb = cb0;
-  for (; cb + (NSTAGE - 1) * cstride + kChunk < hi; cb += NSTAGE * cstride) {
-    static_for<NSTAGE>([&](auto s) __attribute__((always_inline)) {
-      step(cb + decltype(s)::value * cstride, std::false_type{}, s);
-    });
-  }
-  bool more = true;
-  static_for<NSTAGE>([&](auto s) __attribute__((always_inline)) {
-    if (more) {
-      if (cb + kChunk < hi) {
-        step(cb, std::false_type{}, s);
-        cb += cstride;
-      } else {
-        if (cb < hi) step(cb, std::true_type{}, s);
-        more = false;
-      }
+  auto stream = [&](auto hilo) __attribute__((always_inline)) {
+    int cb = cb0;
+    for (; cb + (NSTAGE - 1) * cstride + kChunk < hi; cb += NSTAGE * cstride) {
+      static_for<NSTAGE>([&](auto s) __attribute__((always_inline)) {
+        step(cb + decltype(s)::value * cstride, std::false_type{}, s, hilo);
+      });
     }
-  });
+    bool more = true;
+    static_for<NSTAGE>([&](auto s) __attribute__((always_inline)) {
+      if (more) {
+        if (cb + kChunk < hi) {
+          step(cb, std::false_type{}, s, hilo);
+          cb += cstride;
+        } else {
+          if (cb < hi) step(cb, std::true_type{}, s, hilo);
+          more = false;
+        }
+      }
+    });
+  };
+  // Short rows take hi/lo probabilities in every chunk (see kHiLoMaxLen).
+  if (L <= kHiLoMaxLen) stream(std::true_type{});
+  else stream(std::false_type{});
   wait_vmcnt<0>();  // retire the trailing (out-of-range) prefetches
   wave_lds_fence();
 
@@ -900,7 +961,7 @@ quant_split_lds_kernel(SplitParams prm) {
       const float fac = kTwo24 * __builtin_ldexpf(1.0f, -p * VNB);
       const float zv = ozg[VL::group_of(mv)];
       f4 a = accv[mv];
-      if (kVChain && p + 1 < VL::P) a -= accv[VL::mfma_index(p + 1, VL::window_of(mv), VL::e_of(mv))];
+      if (kVChain && p > 0) a -= accv[VL::mfma_index(p - 1, VL::window_of(mv), VL::e_of(mv))];
 #pragma unroll
       for (int i = 0; i < 4; ++i) wp.o[n][VL::dim_of(mv, 4 * j + i)] = fmaf(a[i], fac, zv);
     }
@@ -941,6 +1002,60 @@ void launch_quant_pt(const SplitParams& p, dim3 grid, int waves, hipStream_t st)
 // they pay only over many chunks per wave: measured 4-6% faster at 32768 tokens
 // per workgroup (2-bit, K4/V2), equal at 4096, 5-10% slower at 512-1024.
 constexpr int kPairedTilesMinSplit = 8192;
+
+// ===========================================================================
+// Read-ceiling probe: what the split kernel's access pattern streams with no
+// arithmetic behind it.  Same grid, waves, 32-token chunk order, two-stage
+// per-wave ring and direct-to-LDS instructions (issue_chunk) over the same
+// contiguous caches; each chunk is consumed by one LDS read per lane, so the
+// loads stay live.  The measurement counterpart, for this kernel's read
+// pattern, of a device-copy bandwidth probe.
+// ===========================================================================
+template <int D, int KNB, int VNB, int GS, int NW>
+__global__ void __launch_bounds__(NW * 64) read_probe_kernel(SplitParams prm) {
+  using SG = StageGeom<D, KNB, VNB, GS>;
+  constexpr int NG = SG::NG;
+  constexpr int NI = SG::NINSTR;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[NW * 2 * SG::BYTES];
+  const int unit = blockIdx.x, split = blockIdx.y;
+  const int b = unit / prm.HKV;
+  const int L = prm.seq_lens ? min(prm.seq_lens[b], prm.S) : prm.S;
+  const int lo = split * prm.split_size;
+  const int hi = min(lo + prm.split_size, L);
+  const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int64_t slab = unit;
+  const uint32_t rows = (uint32_t)prm.S;
+  const rsrc_t rk = make_rsrc(prm.k + slab * rows * SG::KL::DP, rows * SG::KL::DP);
+  const rsrc_t rv = make_rsrc(prm.v + slab * rows * SG::VL::DP, rows * SG::VL::DP);
+  const rsrc_t rm[4] = {make_rsrc(prm.ks + slab * rows * NG, rows * NG * 2),
+                        make_rsrc(prm.kz + slab * rows * NG, rows * NG * 2),
+                        make_rsrc(prm.vs + slab * rows * NG, rows * NG * 2),
+                        make_rsrc(prm.vz + slab * rows * NG, rows * NG * 2)};
+  uint8_t* ring = smem + w * 2 * SG::BYTES;
+  const int cstride = kChunk * NW;
+  const int cb0 = lo + kChunk * w;
+  issue_chunk<D, KNB, VNB, GS>(ring, rk, rv, rm, cb0, cb0 < hi, lane);
+  float acc = 0.0f;
+  int s = 0;
+  for (int cb = cb0; cb < hi; cb += cstride) {
+    wait_lgkmcnt0();  // the previous read of the stage refilled next is done
+    asm volatile("" ::: "memory");
+    const int cn = cb + cstride;
+    issue_chunk<D, KNB, VNB, GS>(ring + (s ^ 1) * SG::BYTES, rk, rv, rm, cn, cn < hi, lane);
+    wait_vmcnt<NI>();
+    asm volatile("" ::: "memory");
+    acc += reinterpret_cast<const float*>(ring + s * SG::BYTES)[lane];
+    s ^= 1;
+  }
+  wait_vmcnt<0>();
+  if (acc == 1.2345678e-30f) prm.out[blockIdx.x] = acc;  // data-dependent: the loads cannot be dropped
+}
+
+template <int D, int KNB, int VNB, int GS>
+void launch_read_probe(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
+  if (waves == 8) read_probe_kernel<D, KNB, VNB, GS, 8><<<grid, dim3(8 * 64), 0, st>>>(p);
+  else read_probe_kernel<D, KNB, VNB, GS, 4><<<grid, dim3(4 * 64), 0, st>>>(p);
+}
 
 template <int D, int KNB, int VNB, int GS>
 void launch_quant(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {

@@ -1,4 +1,4 @@
-// quant_split_lds_kernel instantiations for 2-bit K and 2-bit V codes.
+// quant_split_lds_kernel (and read-probe) instantiations for 2-bit K and 2-bit V codes.
 #include "quant_split.h"
 
 namespace tkv {
@@ -10,5 +10,13 @@ template void launch_quant<128, 2, 2, 128>(const SplitParams&, dim3, int, hipStr
 template void launch_quant<64, 2, 2, 16>(const SplitParams&, dim3, int, hipStream_t);
 template void launch_quant<64, 2, 2, 32>(const SplitParams&, dim3, int, hipStream_t);
 template void launch_quant<64, 2, 2, 64>(const SplitParams&, dim3, int, hipStream_t);
+
+template void launch_read_probe<128, 2, 2, 16>(const SplitParams&, dim3, int, hipStream_t);
+template void launch_read_probe<128, 2, 2, 32>(const SplitParams&, dim3, int, hipStream_t);
+template void launch_read_probe<128, 2, 2, 64>(const SplitParams&, dim3, int, hipStream_t);
+template void launch_read_probe<128, 2, 2, 128>(const SplitParams&, dim3, int, hipStream_t);
+template void launch_read_probe<64, 2, 2, 16>(const SplitParams&, dim3, int, hipStream_t);
+template void launch_read_probe<64, 2, 2, 32>(const SplitParams&, dim3, int, hipStream_t);
+template void launch_read_probe<64, 2, 2, 64>(const SplitParams&, dim3, int, hipStream_t);
 
 }  // namespace tkv

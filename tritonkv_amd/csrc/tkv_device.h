@@ -55,10 +55,10 @@ __device__ __forceinline__ constexpr uint32_t slice_mask(int p) {
   return ((((1u << NBITS) - 1u) << (p * NBITS)) * 0x00010001u);
 }
 
-// Bits of slices p.. of every byte held in the low byte of each fp16 half.
+// Bits of slices 0..p of every byte held in the low byte of each fp16 half.
 template <int NBITS>
-__device__ __forceinline__ constexpr uint32_t hi_slices_mask(int p) {
-  return ((0xFFu << (p * NBITS)) & 0xFFu) * 0x00010001u;
+__device__ __forceinline__ constexpr uint32_t lo_slices_mask(int p) {
+  return (((1u << ((p + 1) * NBITS)) - 1u) & 0xFFu) * 0x00010001u;
 }
 
 // Slot order of the four bytes of a dword after extraction: slots 0,1 come
@@ -106,6 +106,17 @@ __device__ __forceinline__ uint32_t pk_fma_rem(uint32_t a, uint32_t b, uint32_t 
 __device__ __forceinline__ uint32_t pk_mul(uint32_t a, uint32_t b) {
   h2 r = __builtin_bit_cast(h2, a) * __builtin_bit_cast(h2, b);
   return __builtin_bit_cast(uint32_t, r);
+}
+__device__ __forceinline__ uint32_t pk_add(uint32_t a, uint32_t b) {
+  h2 r = __builtin_bit_cast(h2, a) + __builtin_bit_cast(h2, b);
+  return __builtin_bit_cast(uint32_t, r);
+}
+// fp16 pair of the remainders p - fp16(p): with ph = pack_h2(p0, p1), the
+// low parts of a hi/lo split (p0 - half_lo(ph) is exact in fp32).
+__device__ __forceinline__ uint32_t pack_h2_rem(float p0, float p1, uint32_t ph) {
+  h2 v = {(_Float16)(p0 - (float)__builtin_bit_cast(h2, ph)[0]),
+          (_Float16)(p1 - (float)__builtin_bit_cast(h2, ph)[1])};
+  return __builtin_bit_cast(uint32_t, v);
 }
 __device__ __forceinline__ uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint32_t sel) {
   return __builtin_amdgcn_perm(hi_src, lo_src, sel);
