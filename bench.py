@@ -54,19 +54,22 @@ def _args():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=1000,
                     help="untimed steps (graph replays) right before the timed ones")
+    ap.add_argument("--min-warmup-s", type=float, default=None,
+                    help="seconds of warm-up replays at least (default: timing.MIN_WARMUP_S; "
+                         "0 for counter runs, where every dispatch is serialised)")
     ap.add_argument("--quick", action="store_true",
                     help="headline workload only (no 2-bit / control / Qwen table / CPU baseline)")
     ap.add_argument("--num-splits", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--rocprof-summary", metavar="TRACE_DIR", default=None,
                     help="no GPU work: summarise a rocprofv3 --kernel-trace --stats "
                          "--output-format csv directory (plus --pmc-fetch/--pmc-write "
                          "counter directories) as the text kept under profiles/")
     ap.add_argument("--pmc-fetch", default=None)
     ap.add_argument("--pmc-write", default=None)
-    ap.add_argument("--kernel", default="quant_split_kernel<128, 4, 4, 32",
-                    help="kernel-name substring the summary and traffic figures are for")
+    ap.add_argument("--kernel", default=None,
+                    help="full kernel name the summary and traffic figures are for (default: "
+                         "the headline's split kernel instantiation)")
     ap.add_argument("--command", default="", help="command line recorded in the summary")
     ap.add_argument("--title", default="", help="first line of the summary (default: the headline)")
     ap.add_argument("--rows", type=int, default=8, help="kernels listed in the summary")
@@ -93,41 +96,34 @@ def algorithmic_bytes(B, HQ, HKV, S, D, kbits, vbits, gs):
     return cache, cache + B * HQ * D * (2 + 4)
 
 
-def llama_inputs(seed, B=32, HQ=32, HKV=8, S=32768, D=128, n_out=4, scale=8.0):
-    import torch
+def llama_inputs(seed, B=32, HQ=32, HKV=8, S=32768, D=128):
+    """BASELINE.json config 4's inputs: fp16 N(0,1) q/K/V with 4 seeded x8
+    outlier channels per KV head (``tritonkv_amd.synthetic``, the generator
+    the full-size GPU parity tests check the kernels on)."""
+    from tritonkv_amd import synthetic
 
-    g = torch.Generator(device="cuda").manual_seed(seed)
-    q = torch.randn(B, HQ, D, device="cuda", generator=g, dtype=torch.float16)
-    chans = torch.stack([torch.randperm(D, device="cuda", generator=g)[:n_out] for _ in range(HKV)])
-    mult = torch.ones(HKV, D, device="cuda", dtype=torch.float16)
-    mult.scatter_(1, chans, scale)
-    k = torch.randn(B, HKV, S, D, device="cuda", generator=g, dtype=torch.float16)
-    k.mul_(mult[None, :, None, :])
-    v = torch.randn(B, HKV, S, D, device="cuda", generator=g, dtype=torch.float16)
-    v.mul_(mult[None, :, None, :])
+    q, k, v, _ = synthetic.outlier_channel_kv(B, HQ, HKV, S, D, seed=seed)
     return q, k, v
+
+
+# The split kernel's paired-tile form runs for GQA groups of at most 8 heads
+# and splits of at least this many tokens (kPairedTilesMinSplit in
+# tritonkv_amd/csrc/quant_split.h).
+PAIRED_TILES_MIN_SPLIT = 8192
+
+
+def split_kernel_name(D, kbits, vbits, gs, waves, G, split_size, paged=False, kch=False):
+    """The demangled name (as rocprofv3 prints it) of the quantized split
+    kernel instantiation that a launch with these arguments runs."""
+    pt = not kch and G <= 8 and split_size >= PAIRED_TILES_MIN_SPLIT
+    b = lambda x: "true" if x else "false"  # noqa: E731
+    return (f"void tkv::quant_split_lds_kernel<{D}, {kbits}, {vbits}, {gs}, {waves}, 2, "
+            f"{b(paged)}, {b(pt)}, {b(kch)}>(tkv::SplitParams)")
 
 
 # ---------------------------------------------------------------------------
 # timing
 # ---------------------------------------------------------------------------
-
-
-def capture(calls):
-    import torch
-
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        calls[0]()
-    torch.cuda.current_stream().wait_stream(side)
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        for f in calls:
-            f()
-    torch.cuda.synchronize()
-    return g
 
 
 _CLOCKS = None          # the running clocks.ClockMonitor, if any
@@ -152,60 +148,36 @@ def clock_record(timings, full=False):
     return {**win, **gate}
 
 
+_LAST_WARMUP = None      # (replays, seconds) of the last timed_steps' warm-up
+MIN_WARMUP_S = None      # --min-warmup-s
+
+
 def timed_steps(copies, steps, warmup, reps=3):
-    """µs per step of ``steps`` rotating calls in one graph: the mean over
-    ``reps`` timed replays (every timed launch counts, as in a profiler's
-    average), plus the wall-clock ms per step of the first timed replay and the
-    per-replay figures.
+    """µs per step of ``steps`` rotating calls in one graph (``timing.timed_steps``:
+    the mean over ``reps`` timed replays, after at least ``warmup`` steps and
+    ``timing.MIN_WARMUP_S`` seconds of warm-up replays of the same graph), plus
+    the wall-clock ms per step of the first timed replay and the per-replay
+    figures.  Records the clock window and the warm-up of the call."""
+    from tritonkv_amd import timing
 
-    The ``warmup`` untimed steps are replays of the same graph issued right
-    before the timed ones: on MI355X the first ~100-250 ms of streaming after
-    an idle gap (such as the graph capture) run up to 10% below the sustained
-    rate, so warming up eagerly before the capture does not carry over.
-    """
-    import torch
-
-    global _LAST_WINDOW
-    g = capture([copies[i % len(copies)] for i in range(steps)])
-    t_start = time.time()
-    for _ in range(max(1, math.ceil(warmup / steps))):
-        g.replay()
-    torch.cuda.synchronize()
-    t_timed = time.time()
-    us, walls = [], []
-    for _ in range(reps):
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        s.record()
-        g.replay()
-        e.record()
-        torch.cuda.synchronize()
-        walls.append((time.perf_counter() - t0) * 1e3 / steps)
-        us.append(s.elapsed_time(e) * 1e3 / steps)
-    _LAST_WINDOW = (max(t_start, t_timed - CLOCK_LEAD_IN_S), time.time())
-    del g
-    return statistics.mean(us), walls[0], us
+    global _LAST_WINDOW, _LAST_WARMUP
+    floor = timing.MIN_WARMUP_S if MIN_WARMUP_S is None else MIN_WARMUP_S
+    t = timing.timed_steps(copies, steps, warmup, reps=reps, min_warmup_s=floor)
+    _LAST_WINDOW = (t.timed_start - CLOCK_LEAD_IN_S, t.timed_end)
+    _LAST_WARMUP = (t.warmup_replays, t.warmup_s)
+    return t.us, t.wall_ms, t.per_replay_us
 
 
 def per_call_us(calls, reps=5):
-    """Median µs per call of a graph that makes each call once (rotating caches)."""
-    import torch
+    from tritonkv_amd import timing
 
-    g = capture(list(calls))
-    for _ in range(2):
-        g.replay()
-    torch.cuda.synchronize()
-    out = []
-    for _ in range(reps):
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        g.replay()
-        e.record()
-        torch.cuda.synchronize()
-        out.append(s.elapsed_time(e) * 1e3 / len(calls))
-    del g
-    return statistics.median(out)
+    return timing.per_call_us(calls, reps=reps)
+
+
+def capture(calls):
+    from tritonkv_amd import timing
+
+    return timing.capture(calls)
 
 
 # ---------------------------------------------------------------------------
@@ -213,7 +185,10 @@ def per_call_us(calls, reps=5):
 # ---------------------------------------------------------------------------
 
 
-def fused_call(q, kq, vq, num_splits=None, split_only=False, waves=None, fused_combine=False):
+def fused_call(q, kq, vq, num_splits=None, split_only=False, waves=None, fused_combine=False,
+               probe=False):
+    """One decode step as a callable (``probe``: the read-ceiling probe of the
+    split kernel's access pattern instead, ``tkv_read_probe``)."""
     import torch
 
     from tritonkv_amd import _lib
@@ -234,13 +209,14 @@ def fused_call(q, kq, vq, num_splits=None, split_only=False, waves=None, fused_c
         counters=_lib.ptr(cnt) if (fused_combine and not split_only) else None, waves=wv)
     lib = _lib.load()
     fn = lib.tkv_fused_decode_split if split_only else lib.tkv_fused_decode_attention
+    if probe:
+        fn = lib.tkv_read_probe
 
     def call():
         _lib.check(fn(args, torch.cuda.current_stream().cuda_stream), "fused")
     call.keep = (out, acc, mx, sm, cnt, q, kq, vq)
     call.num_splits = ns
-    pt = "true" if HQ // HKV <= 8 and size >= 8192 else "false"
-    call.kernel = (f"quant_split_lds_kernel<{D}, {kq.nbits}, {vq.nbits}, {kq.group_size}, {wv}, 2, false, {pt}>")
+    call.kernel = split_kernel_name(D, kq.nbits, vq.nbits, kq.group_size, wv, HQ // HKV, size)
     return call
 
 
@@ -395,7 +371,7 @@ def _counter_per_dispatch(directory, kernel):
     by = {}
     for r in rows:
         by.setdefault((r["Kernel_Name"], int(r["Grid_Size"])), []).append(float(r["Counter_Value"]))
-    mine = [(g, n, v) for (n, g), v in by.items() if kernel in n]
+    mine = [(g, n, v) for (n, g), v in by.items() if n == kernel]
     if not mine:
         raise ValueError(f"no dispatch of {kernel!r} in {directory}")
     g, name, vals = max(mine)
@@ -405,6 +381,8 @@ def _counter_per_dispatch(directory, kernel):
 
 
 def rocprof_summary(a) -> int:
+    if a.kernel is None:
+        a.kernel = split_kernel_name(128, 4, 4, 32, 8, 4, 32768)
     out = []
     out.append(a.title or f"# rocprofv3 summary -- kernel {a.kernel}..., Llama-3-8B decode step "
                f"(B=32 HQ=32 HKV=8 D=128 ctx=32768, 4-bit gs32), bench.py --quick")
@@ -461,7 +439,7 @@ def measured_traffic(kernel_name):
     kern = [ln.split(":", 1)[1].strip() for ln in text.splitlines() if ln.startswith("kernel: ")]
     vals = [ln.split(":", 1)[1].strip() for ln in text.splitlines()
             if ln.startswith("traffic_bytes_per_launch:")]
-    if not kern or not vals or kernel_name not in kern[-1]:
+    if not kern or not vals or kern[-1] != kernel_name:
         return None
     return int(vals[-1])
 
@@ -471,7 +449,17 @@ def measured_traffic(kernel_name):
 # ---------------------------------------------------------------------------
 
 
-def cpu_baseline(q, kq, vq, budget_s):
+def cpu_baseline(q, kq, vq, got, threads=None, one_thread_units=16):
+    """The oracle's scalar C restatement (``oracle/tkv_oracle.c``: dequantise K
+    and V to fp32, then fp32 attention) timed over the whole decode step on the
+    host's cores, one (batch row, kv head) unit per task (ctypes releases the
+    GIL for the C call), plus a one-thread figure on a few units.
+
+    Doubles as the benchmark's correctness snapshot: every unit's oracle
+    output is compared with ``got``, the GPU output of the timed step on the
+    same cache, against the 2e-3 max-abs / 1e-3 mean-abs tolerance."""
+    import concurrent.futures as cf
+
     import numpy as np
 
     from oracle import c_oracle
@@ -479,30 +467,51 @@ def cpu_baseline(q, kq, vq, budget_s):
     B, HQ, D = q.shape
     _, HKV, S, _ = kq.packed.shape
     G = HQ // HKV
-    units_total = B * HKV
-    done, t_spent = 0, 0.0
-    b = 0
-    while b < B and t_spent < budget_s:
-        qb = q[b:b + 1].float().cpu().numpy()
-        host = [t[b:b + 1].cpu().numpy() for t in (kq.packed, kq.scale, kq.zero,
-                                                   vq.packed, vq.scale, vq.zero)]
-        for h in range(HKV):
-            sub = [a[:, h:h + 1] for a in host]
-            qh = np.ascontiguousarray(qb[:, h * G:(h + 1) * G])
-            t0 = time.perf_counter()
-            c_oracle.quantized_decode_attention(
-                qh, (sub[0], sub[1], sub[2], kq.nbits, kq.group_size),
-                (sub[3], sub[4], sub[5], vq.nbits, vq.group_size), D ** -0.5)
-            t_spent += time.perf_counter() - t0
-            done += 1
-            if t_spent >= budget_s:
-                break
-        b += 1
-    us_step = t_spent / done * units_total * 1e6
-    return {"value": round(us_step, 1), "unit": "us/decode step", "cores": 1, "kind": "port",
-            "sample": (f"oracle/tkv_oracle.c (scalar C, 1 thread): dequantize K,V to fp32 + fp32 "
-                       f"attention for {done} of the {units_total} (batch row, kv head) units of "
-                       f"one decode step ({t_spent:.1f} s), extrapolated x{units_total / done:.1f}")}
+    host = [t.cpu().numpy() for t in (kq.packed, kq.scale, kq.zero, vq.packed, vq.scale, vq.zero)]
+    qf = q.float().cpu().numpy()
+    units = [(b, h) for b in range(B) for h in range(HKV)]
+
+    def run(u):
+        b, h = u
+        sub = [a[b:b + 1, h:h + 1] for a in host]
+        return c_oracle.quantized_decode_attention(
+            qf[b:b + 1, h * G:(h + 1) * G], (sub[0], sub[1], sub[2], kq.nbits, kq.group_size),
+            (sub[3], sub[4], sub[5], vq.nbits, vq.group_size), D ** -0.5)
+
+    run(units[0])  # load the library, touch the pages
+    n = threads or min(16, len(os.sched_getaffinity(0)))
+    t0 = time.perf_counter()
+    with cf.ThreadPoolExecutor(max_workers=n) as ex:
+        refs = list(ex.map(run, units))
+    t_all = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    for u in units[:one_thread_units]:
+        run(u)
+    t_one = (time.perf_counter() - t0) / one_thread_units
+    max_abs, sum_abs, count, worst = 0.0, 0.0, 0, None
+    for (b, h), ref in zip(units, refs):
+        d = np.abs(got[b, h * G:(h + 1) * G].astype(np.float64) - ref[0])
+        if d.max() > max_abs:
+            max_abs, worst = float(d.max()), [b, h]
+        sum_abs += float(d.sum())
+        count += d.size
+    check = {"units": len(units), "max_abs_err": max_abs, "mean_abs_err": sum_abs / count,
+             "worst_unit": worst, "tolerance": {"max_abs": 2e-3, "mean_abs": 1e-3},
+             "ok": bool(max_abs <= 2e-3 and sum_abs / count <= 1e-3),
+             "reference": "oracle/tkv_oracle.c fp32 dequantise-then-attend on the timed cache"}
+    try:
+        cpu = next(ln.split(":", 1)[1].strip() for ln in open("/proc/cpuinfo")
+                   if ln.startswith("model name"))
+    except (OSError, StopIteration):
+        cpu = "unknown"
+    base = {"value": round(t_all * 1e6, 1), "unit": "us/decode step", "cores": n, "kind": "port",
+            "sample": (f"the whole decode step: all {len(units)} (batch row, kv head) units, "
+                       f"oracle/tkv_oracle.c (scalar C: dequantize K,V to fp32 + fp32 attention), "
+                       f"one unit per task on {n} threads ({t_all:.2f} s)"),
+            "one_thread_us_per_step": round(t_one * len(units) * 1e6, 1),
+            "one_thread_sample": f"{one_thread_units} units on 1 thread, x{len(units) / one_thread_units:.0f}",
+            "cpu": cpu}
+    return base, check
 
 
 def cpu_config1(reps=50):
@@ -561,30 +570,20 @@ def cpu_config1(reps=50):
 
 def ragged_70b(steps, warmup, seed=2024):
     """B=64, HQ=64, HKV=8, D=128; per-sequence length S_b ~ U[1024, 131072]
-    (seeded); K 4-bit / V 2-bit, group 32.  One step appends one new token per
-    sequence (GPU quantize + pack of K and V at position S_b) and then decodes
-    over S_b + 1 tokens.  Storage is padded to 131072 + 64 tokens; only the
-    sum of S_b + 1 counts as cache bytes."""
+    (seeded); K 4-bit / V 2-bit, group 32; inputs from
+    ``tritonkv_amd.synthetic.ragged_batch`` (the full-size GPU parity test's).
+    One step appends one new token per sequence (GPU quantize + pack of K and
+    V at position S_b) and then decodes over S_b + 1 tokens.  Storage is padded
+    to 131072 + 64 tokens; only the sum of S_b + 1 counts as cache bytes."""
     import torch
 
+    from tritonkv_amd import synthetic
     from tritonkv_amd.kernels import fused_decode_attention
-    from tritonkv_amd.quantize import QuantizedTensor, append_kv, cache_row_bytes, empty_cache
+    from tritonkv_amd.quantize import append_kv, cache_row_bytes
 
     B, HQ, HKV, D, gs, cap = 64, 64, 8, 128, 32, 131072 + 64
-    g = torch.Generator().manual_seed(seed)
-    lens = torch.randint(1024, 131072 + 1, (B,), generator=g, dtype=torch.int32)
-    kc = empty_cache(B, HKV, cap, D, 4, gs, "cuda")
-    vc = empty_cache(B, HKV, cap, D, 2, gs, "cuda")
-    gd = torch.Generator(device="cuda").manual_seed(seed + 1)
-    for b in range(B):
-        for cache in (kc, vc):
-            x = torch.randn(1, HKV, int(lens[b]), D, device="cuda", generator=gd, dtype=torch.float16)
-            append_kv(QuantizedTensor(cache.packed[b:b + 1], cache.scale[b:b + 1], cache.zero[b:b + 1],
-                                      cache.nbits, gs, D), x)
-            del x
-    q = torch.randn(B, HQ, D, device="cuda", generator=gd, dtype=torch.float16)
-    k_new = torch.randn(B, HKV, 1, D, device="cuda", generator=gd, dtype=torch.float16)
-    v_new = torch.randn(B, HKV, 1, D, device="cuda", generator=gd, dtype=torch.float16)
+    lens = synthetic.ragged_lengths(B, 1024, 131072, seed=seed)
+    q, kc, vc, k_new, v_new = synthetic.ragged_batch(B, HQ, HKV, D, lens, cap, 4, 2, gs, seed=seed)
     pos = lens.to("cuda")
     lens1 = (lens + 1).to("cuda")
     out = torch.empty(B, HQ, D, device="cuda")
@@ -727,7 +726,9 @@ def qwen_table(ctxs=(512, 2048, 8192, 16384)):
     for S in ctxs:
         g = torch.Generator(device="cuda").manual_seed(1000 + S)
         q = torch.randn(B, HQ, D, device="cuda", generator=g, dtype=torch.float16)
-        for method in ("fused4", "fused2", "fp16", "fp16_nosplit", "torch_fp16"):
+        ns_fused4 = None
+        for method in ("fused4", "fused2", "fp16", "fp16_fused_split", "fp16_nosplit",
+                       "torch_fp16"):
             nbits = {"fused4": 4, "fused2": 2}.get(method, 16)
             cache, step_bytes = algorithmic_bytes(B, HQ, HKV, S, D, nbits, nbits, gs)
             R = replicas_for(cache)
@@ -736,6 +737,9 @@ def qwen_table(ctxs=(512, 2048, 8192, 16384)):
             if method == "fp16":
                 for i in range(R):
                     calls.append(fp16_call(q, kv[0, i], kv[1, i]))
+            elif method == "fp16_fused_split":  # the fused 4-bit kernel's split count
+                for i in range(R):
+                    calls.append(fp16_call(q, kv[0, i], kv[1, i], num_splits=ns_fused4))
             elif method == "fp16_nosplit":
                 for i in range(R):
                     calls.append(fp16_call(q, kv[0, i], kv[1, i], num_splits=1))
@@ -750,6 +754,8 @@ def qwen_table(ctxs=(512, 2048, 8192, 16384)):
                     ki = QuantizedTensor(kq.packed[i], kq.scale[i], kq.zero[i], nbits, gs, D)
                     vi = QuantizedTensor(vq.packed[i], vq.scale[i], vq.zero[i], nbits, gs, D)
                     calls.append(fused_call(q, ki, vi))
+            if method == "fused4":
+                ns_fused4 = calls[0].num_splits
             hot = per_call_us([calls[0]] * 50)
             cold = per_call_us(calls)
             rows.append({"ctx": S, "method": method, "cache_bytes": cache, "replicas": R,
@@ -768,6 +774,10 @@ def qwen_table(ctxs=(512, 2048, 8192, 16384)):
         return round(by[(S, num)][col] / by[(S, den)][col], 3)
 
     effects = {str(S): {"quant_effect_cold_4b": ratio(S, "fp16", "fused4", "cold_us"),
+                        "quant_effect_cold_4b_same_split": ratio(S, "fp16_fused_split", "fused4",
+                                                                 "cold_us"),
+                        "quant_effect_hot_4b_same_split": ratio(S, "fp16_fused_split", "fused4",
+                                                                "hot_us"),
                         "quant_effect_cold_2b": ratio(S, "fp16", "fused2", "cold_us"),
                         "quant_effect_hot_4b": ratio(S, "fp16", "fused4", "hot_us"),
                         "flash_decode_effect_cold_vs_torch": ratio(S, "torch_fp16", "fp16", "cold_us"),
@@ -951,6 +961,8 @@ def main() -> int:
         return regime_probe(a.regime_probe)
     if a.compare:
         return compare(a.compare)
+    global MIN_WARMUP_S
+    MIN_WARMUP_S = a.min_warmup_s
     if a.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU per box; the decode step shards "
                           "by (batch, kv head) with no communication, and no figure at "
@@ -994,12 +1006,19 @@ def main() -> int:
     cache4, bytes4 = algorithmic_bytes(B, HQ, HKV, S, D, 4, 4, gs)
     steps4 = [fused_call(*c, num_splits=a.num_splits) for c in copies4]
     us4, wall4, samples4 = timed_steps(steps4, a.steps, a.warmup)
+    warm4 = _LAST_WARMUP
     clocks4 = clock_record(samples4, full=True)
     split4 = [fused_call(*c, num_splits=a.num_splits, split_only=True) for c in copies4]
     split_us4, _, split_samples4 = timed_steps(split4, a.steps, a.warmup)
     clocks_split4 = clock_record(split_samples4)
     kernel4 = split4[0].kernel
     achieved = bytes4 / split_us4 / 1e3
+    probe4 = [fused_call(*c, num_splits=a.num_splits, probe=True) for c in copies4]
+    probe_us4, _, _ = timed_steps(probe4, a.steps, a.warmup)
+    ceiling4 = cache4 / probe_us4 / 1e3
+    print(f"# llama 4-bit read-ceiling probe: {probe_us4:.2f} us = {ceiling4:.0f} GB/s; split "
+          f"kernel at {probe_us4 / split_us4:.1%} of it", file=sys.stderr, flush=True)
+    del probe4
     print(f"# llama 4-bit: step {us4:.2f} us, split kernel {split_us4:.2f} us, "
           f"{achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%} of 8 TB/s), "
           f"splits={steps4[0].num_splits}", file=sys.stderr, flush=True)
@@ -1013,11 +1032,20 @@ def main() -> int:
                         "num_splits": steps4[0].num_splits,
                         "step_us_per_replay": [round(x, 2) for x in samples4],
                         "split_kernel_us_per_replay": [round(x, 2) for x in split_samples4],
+                        "read_ceiling": {"probe_us": round(probe_us4, 2),
+                                         "gbps": round(ceiling4, 1),
+                                         "frac_of_hbm_peak": round(ceiling4 / HBM_PEAK_GBS, 4),
+                                         "kernel_frac_of_ceiling": round(probe_us4 / split_us4, 4)},
                         "clocks": clocks_split4}
-    cpu = None
+    cpu, check = None, None
     if not a.quick and not a.no_cpu_baseline:
         q0, kq0, vq0 = copies4[0]
-        cpu = cpu_baseline(q0, kq0, vq0, a.cpu_seconds)
+        got0 = steps4[0].keep[0].cpu().numpy()  # copy 0's output of the last timed replay
+        cpu, check = cpu_baseline(q0, kq0, vq0, got0)
+        print(f"# cpu baseline {cpu['value'] / 1e3:.0f} ms/step on {cpu['cores']} threads; "
+              f"check vs oracle: max abs {check['max_abs_err']:.2e}, mean abs "
+              f"{check['mean_abs_err']:.2e} over {check['units']} units", file=sys.stderr,
+              flush=True)
         cpu["config1_reference_cpu_step"] = cpu_config1()
     del steps4, split4
     torch.cuda.empty_cache()
@@ -1057,12 +1085,17 @@ def main() -> int:
                             "gbps_split_kernel": round(nbytes / sp / 1e3, 1),
                             "frac_of_hbm_peak": round(nbytes / sp / 1e3 / HBM_PEAK_GBS, 4),
                             "clocks": clock_record(sps)}
+            if nbits != 16:
+                pu, _, _ = timed_steps([mk(*c, probe=True) for c in cps], a.steps, a.warmup)
+                detail[name]["read_ceiling"] = {
+                    "probe_us": round(pu, 2), "gbps": round(cache / pu / 1e3, 1),
+                    "kernel_frac_of_ceiling": round(pu / sp, 4)}
             print(f"# llama {name}: step {us:.2f} us, split {sp:.2f} us", file=sys.stderr, flush=True)
             del cps
             torch.cuda.empty_cache()
         detail["quant_effect_4b"] = round(detail["fp16"]["us_per_step"] / us4, 3)
         detail["quant_effect_2b"] = round(detail["fp16"]["us_per_step"] / detail["fused2"]["us_per_step"], 3)
-        detail["empty_graph_node_us"] = round(empty_kernel_floor() * 1e3, 2)
+        detail["empty_graph_node_us"] = round(empty_kernel_floor(), 2)
         detail["qwen2.5-1.5b"] = qwen_table()
         detail["qwen2.5-1.5b_serving_step"] = qwen_serving_steps()
         detail["qwen2.5-1.5b_e2e_decode"] = qwen_e2e()
@@ -1093,8 +1126,13 @@ def main() -> int:
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(kernel4),
                      "kernel": kernel4, "kernel_us": round(split_us4, 2),
-                     "algorithmic_bytes": bytes4},
+                     "algorithmic_bytes": bytes4,
+                     "read_ceiling_gbps": round(ceiling4, 1),
+                     "frac_of_read_ceiling": round(probe_us4 / split_us4, 4)},
         "cpu_baseline": cpu,
+        "check": check,
+        "warmup_replays": warm4[0],
+        "warmup_s": round(warm4[1], 3),
         "clocks": clocks4,
         "detail": detail,
     }

@@ -159,6 +159,10 @@ def test_c_entry_points_reject_bad_arguments_without_a_gpu():
     assert lib.tkv_paged_quantize_pack(dummy, 0, 1, 1, 1, 128, 4, 32, dummy, dummy, 1, 48, 1,
                                        dummy, dummy, dummy, None) == _lib.TKV_EINVAL
     assert _lib.status_string(_lib.TKV_EINVAL) == "invalid argument"
+    # the read-ceiling probe takes the split kernel's contiguous form only
+    assert lib.tkv_read_probe(None, None) == _lib.TKV_EINVAL
+    a.k_new = a.v_new = dummy
+    assert lib.tkv_read_probe(ctypes.byref(a), None) == _lib.TKV_EUNSUPPORTED
 
 
 def test_noalloc_entry_point_rejects_before_touching_the_gpu():
@@ -224,6 +228,19 @@ def test_python_validation_precedes_backend_check():
     # every tensor on one device: a host pointer handed to a kernel would fault the GPU
     with pytest.raises(ValueError, match="same device"):
         fused_decode_attention(q, _fake_qt(), _fake_qt(device="meta"))
+    # the fused append writes into the caches: a non-contiguous one (the token
+    # would land in a temporary copy) or a misaligned one is refused, never copied
+    kq = _fake_qt(S=64)
+    view = type(kq)(kq.packed[:, :, :48], kq.scale[:, :, :48], kq.zero[:, :, :48], 4, 32, 128)
+    assert not view.packed.is_contiguous()
+    tok = torch.zeros(1, 2, 128, dtype=torch.float16)
+    with pytest.raises(ValueError, match="contiguous"):
+        fused_decode_attention(q, view, _fake_qt(S=48), k_new=tok, v_new=tok)
+    flat = torch.zeros(1 + 2 * 48 * 64, dtype=torch.uint8)
+    shifted = type(kq)(flat[1:].view(1, 2, 48, 64), view.scale.contiguous(),
+                       view.zero.contiguous(), 4, 32, 128)
+    with pytest.raises(ValueError, match="16-byte boundary"):
+        fused_decode_attention(q, shifted, _fake_qt(S=48))
     from tritonkv_amd.kernels import fp16_decode_attention
     from tritonkv_amd.kernels.fused_decode_attn import _check_out
 
@@ -321,12 +338,20 @@ def test_ragged_batches_of_a_unit_per_cu_split_long_histories_in_two(monkeypatch
         fda.plan_splits(32768, 64, None, 4, 8, 4)
 
 
-def test_timing_stats_match_reference_definition():
-    from tritonkv_amd.timing import replicas_for, stats
+def test_timing_replicas_and_warmup_floor():
+    """Rotating-set sizing (>= 768 MB of distinct caches) and the warm-up rule:
+    at least W steps and at least MIN_WARMUP_S of replays, whatever the step count."""
+    from tritonkv_amd.timing import MIN_WARMUP_S, replicas_for, warmup_replays_needed
 
-    s = stats([4.0, 1.0, 3.0, 2.0])
-    assert s["median_ms"] == 2.5 and s["p25_ms"] == 1.75 and s["p75_ms"] == 3.25
-    assert s["iqr_frac_of_median"] == pytest.approx(0.6)
     assert replicas_for(163_840, 768_000_000) == 4688
     assert replicas_for(16_777_216, 768_000_000) == 46
+    assert replicas_for(768_000_000, 768_000_000) == 1
     assert replicas_for(0, 768_000_000) == 1
+    assert replicas_for(1, max_replicas=8) == 8
+    assert MIN_WARMUP_S >= 0.3
+    # the driver's --steps 20 --warmup 5 on a 4.5 ms replay: the time floor rules
+    assert warmup_replays_needed(20, 5, 0.0045, 0.5) == 112
+    # many warm-up steps: the step count rules
+    assert warmup_replays_needed(20, 10_000, 0.0045, 0.5) == 500
+    # a replay longer than the floor still runs once
+    assert warmup_replays_needed(20, 0, 2.0, 0.5) == 1
