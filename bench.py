@@ -77,6 +77,12 @@ def _args():
                     help="do not sample clocks/power/temperature during the timed legs")
     ap.add_argument("--compare", nargs="+", metavar="RUN_JSON", default=None,
                     help="no timing: compare the bench JSON lines of complete runs row by row")
+    ap.add_argument("--kernel-probe", choices=sorted(KERNEL_PROBES), default=None,
+                    help="no timing: a few eager launches of one split kernel at its benchmark "
+                         "shape, for rocprofv3 --pmc counter runs")
+    ap.add_argument("--counter-summary", nargs="+", metavar="PMC_DIR", default=None,
+                    help="no GPU work: per-kernel table of the SQ/GRBM counters of rocprofv3 "
+                         "--pmc output directories (one per pass)")
     ap.add_argument("--regime-probe", choices=("hot", "cold"), default=None,
                     help="no timing: 60 eager Qwen2.5-1.5B ctx-16384 4-bit decode calls on one "
                          "cache (hot) or rotating copies >= 768 MB (cold), for rocprofv3 --pmc")
@@ -924,6 +930,97 @@ def qwen_e2e(ctxs=(8192, 32768), B=16, steps=8, seed=11):
 # ---------------------------------------------------------------------------
 
 
+# name -> (K bits, V bits, group size, per-channel keys): the Llama-3-8B-shape
+# split kernels of the benchmark's legs.
+KERNEL_PROBES = {"k4v4g32": (4, 4, 32, False), "k4v4g128": (4, 4, 128, False),
+                 "k2v2g32": (2, 2, 32, False), "k2v2g128": (2, 2, 128, False),
+                 "ch2": (2, 2, 32, True), "ch4": (4, 4, 32, True)}
+
+
+def kernel_probe(name, launches=6):
+    """``launches`` eager split-kernel launches (no combine) of one format at the
+    Llama-3-8B shape on the benchmark's first cache copy, plus the read probe of
+    the same access pattern (not for per-channel keys)."""
+    import torch
+
+    from tritonkv_amd import _lib
+    from tritonkv_amd.channel import BLOCK, quantize_keys_per_channel
+    from tritonkv_amd.kernels.fused_decode_attn import choose_waves, plan_splits
+    from tritonkv_amd.quantize import quantize_groupwise, quantize_kv
+
+    kb, vb, gs, ch = KERNEL_PROBES[name]
+    q, k, v = llama_inputs(seed=10)
+    calls = []
+    if ch:
+        ck = quantize_keys_per_channel(k, kb)
+        vq = quantize_groupwise(v, vb, gs)
+        del k, v
+        B, HQ, D = q.shape
+        _, HKV, S, _ = vq.packed.shape
+        _, ns, size = plan_splits(S, 64, None, B, HKV, HQ // HKV)
+        out = torch.empty(B, HQ, D, device="cuda")
+        acc = torch.empty(B, HQ, ns + 1, D, device="cuda")
+        ml = torch.empty(2, B, HQ, ns + 1, device="cuda")
+        args = _lib.DecodeArgs(
+            q=q.data_ptr(), k=ck.packed.data_ptr(), k_scale=ck.scale.data_ptr(),
+            k_zero=ck.zero.data_ptr(), v=vq.packed.data_ptr(), v_scale=vq.scale.data_ptr(),
+            v_zero=vq.zero.data_ptr(), acc=acc.data_ptr(), maxs=ml[0].data_ptr(),
+            sums=ml[1].data_ptr(), out=out.data_ptr(), B=B, HQ=HQ, HKV=HKV, S=S, D=D,
+            k_nbits=kb, v_nbits=vb, group_size=gs, sm_scale=D ** -0.5, split_size=size,
+            num_splits=ns, waves=choose_waves(B, HKV, HQ // HKV, size, ns), key_block=BLOCK,
+            split_base=0, num_splits_total=ns + 1)
+        lib = _lib.load()
+
+        def call():
+            _lib.check(lib.tkv_fused_decode_split(args, torch.cuda.current_stream().cuda_stream),
+                       "per-channel split")
+        call.keep = (q, ck, vq, out, acc, ml)
+        calls.append(call)
+    else:
+        kq, vq = quantize_kv(k, v, kb, gs)
+        del k, v
+        calls.append(fused_call(q, kq, vq, split_only=True))
+        calls.append(fused_call(q, kq, vq, probe=True))
+    for f in calls:
+        for _ in range(launches):
+            f()
+    torch.cuda.synchronize()
+    print(json.dumps({"kernel_probe": name, "launches": launches, "kernels": len(calls)}))
+    return 0
+
+
+def counter_summary(dirs) -> int:
+    """Mean value per dispatch of every counter in the --pmc directories, per
+    kernel (largest grid of each kernel name), with per-wave instruction counts."""
+    rows = {}
+    for d in dirs:
+        for r in _csv_rows(d, "counter_collection.csv"):
+            key = r["Kernel_Name"]
+            grid = int(r["Grid_Size"])
+            ent = rows.setdefault(key, {})
+            ent.setdefault((grid, r["Counter_Name"]), []).append(float(r["Counter_Value"]))
+    out = []
+    for name, ent in rows.items():
+        if "tkv::" not in name:
+            continue
+        gmax = max(g for g, _ in ent)
+        vals = {c: statistics.mean(v) for (g, c), v in ent.items() if g == gmax}
+        out.append(f"kernel: {name}  (grid {gmax} work-items)")
+        for c in sorted(vals):
+            out.append(f"  {c:28s} {vals[c]:18.1f}")
+        waves = vals.get("SQ_WAVES")
+        if waves:
+            per = ", ".join(f"{c[len('SQ_INSTS_'):]} {vals[c] / waves:.0f}"
+                            for c in sorted(vals) if c.startswith("SQ_INSTS_"))
+            out.append(f"  per wave: {per}")
+        if vals.get("SQ_BUSY_CYCLES") and vals.get("SQ_ACTIVE_INST_VALU") and vals.get("SQ_WAVE_CYCLES"):
+            out.append(f"  SQ_ACTIVE_INST_VALU / SQ_WAVE_CYCLES = "
+                       f"{vals['SQ_ACTIVE_INST_VALU'] / vals['SQ_WAVE_CYCLES']:.3f}")
+        out.append("")
+    print("\n".join(out))
+    return 0
+
+
 def regime_probe(mode):
     """Eager decode calls at the Qwen2.5-1.5B shape, ctx 16384, 4-bit gs32, on one
     cache ('hot') or on rotating copies totalling >= 768 MB ('cold')."""
@@ -957,6 +1054,10 @@ def main() -> int:
     a = _args()
     if a.rocprof_summary:
         return rocprof_summary(a)
+    if a.counter_summary:
+        return counter_summary(a.counter_summary)
+    if a.kernel_probe:
+        return kernel_probe(a.kernel_probe)
     if a.regime_probe:
         return regime_probe(a.regime_probe)
     if a.compare:

@@ -259,7 +259,7 @@ __device__ __forceinline__ void load_q_operands_pt(const SplitParams& prm, int b
   for (int bi = 0; bi < QO::NB; ++bi)
 #pragma unroll
     for (int e = 0; e < 8; ++e) amax = fmaxf(amax, hv ? fabsf(qv[bi][e]) : 0.0f);
-  qo.eh = q_prescale_exp(fmaxf(amax, __shfl_xor(amax, 16, 64)), (QO::P - 1) * KNB);
+  qo.eh = q_prescale_exp(max_xor16(amax), (QO::P - 1) * KNB);
 #pragma unroll
   for (int p = 0; p < QO::P; ++p)
 #pragma unroll
@@ -278,7 +278,7 @@ __device__ __forceinline__ void load_q_operands_pt(const SplitParams& prm, int b
     }
   // lanes j and j ^ 1 hold the two halves of every 16-dim block (j ^ 2 repeats them)
 #pragma unroll
-  for (int g = 0; g < NG; ++g) qz[g] += __shfl_xor(qz[g], 16, 64);
+  for (int g = 0; g < NG; ++g) qz[g] = sum_xor16(qz[g]);
   float hl[8];
 #pragma unroll
   for (int g = 0; g < 8; ++g) {
@@ -299,7 +299,7 @@ __device__ __forceinline__ void load_q_operands_pt(const SplitParams& prm, int b
 __device__ __forceinline__ bool softmax_chunk_pt(const float (&x)[4], float lscale, float& m,
                                                  float& alpha, uint32_t (&ph)[2], float (&p)[4]) {
   float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-  mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
+  mx = fmaxf(mx, lane_xor8(mx));
   mx = xor_max16_32(mx) * lscale;
   const bool moved = mx > m;
   const bool any_moved = __builtin_amdgcn_ballot_w64(moved) != 0;
@@ -690,11 +690,10 @@ quant_split_lds_kernel(SplitParams prm) {
 
       }
       // tile 0 of head c is this lane's (c < 8), tile 1 is lane c + 8's
-      pb = u4{ph[0], ph[1], (uint32_t)__shfl_xor((int)ph[0], 8, 64),
-              (uint32_t)__shfl_xor((int)ph[1], 8, 64)};
+      pb = u4{ph[0], ph[1], lane_xor8(ph[0]), lane_xor8(ph[1])};
       if constexpr (HILO) {
         const uint32_t l0 = pack_h2_rem(pf[0], pf[1], ph[0]), l1 = pack_h2_rem(pf[2], pf[3], ph[1]);
-        pbl = u4{l0, l1, (uint32_t)__shfl_xor((int)l0, 8, 64), (uint32_t)__shfl_xor((int)l1, 8, 64)};
+        pbl = u4{l0, l1, lane_xor8(l0), lane_xor8(l1)};
       }
     } else {
       // ---- scores S^T for the two 16-token tiles ---------------------------

@@ -75,15 +75,56 @@ __device__ __forceinline__ uint32_t code_of_half(uint32_t half_bits, int shift) 
 // ---------------------------------------------------------------------------
 // Wave-level helpers.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float xor_max16_32(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  v = fmaxf(v, __shfl_xor(v, 32, 64));
+// The value unchanged, but opaque to the optimizer (no instruction).
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm volatile("" : "+v"(v));
   return v;
 }
+
+// Cross-lane combines on the VALU (no LDS round trip as with ds_bpermute).
+// v_permlane16_swap exchanges lanes i and i ^ 16, v_permlane32_swap lanes i
+// and i ^ 32: given the same value twice, one output holds the lane's own
+// value and the other its partner's (which is which depends on the lane), so
+// a commutative combine of the two outputs is the pair's in every lane.  The
+// outputs pass through opaque(): this compiler folds fminf/fmaxf of the two
+// outputs of the swap builtin to its first output.
+template <bool SWAP32>
+__device__ __forceinline__ void swap_pair(float v, float& a, float& b) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto s = SWAP32 ? __builtin_amdgcn_permlane32_swap(u, u, false, false)
+                        : __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  a = __builtin_bit_cast(float, opaque(s[0]));
+  b = __builtin_bit_cast(float, opaque(s[1]));
+}
+__device__ __forceinline__ float max_xor16(float v) {
+  float a, b;
+  swap_pair<false>(v, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float sum_xor16(float v) {
+  float a, b;
+  swap_pair<false>(v, a, b);
+  return a + b;
+}
+__device__ __forceinline__ float xor_max16_32(float v) {
+  float a, b;
+  swap_pair<false>(v, a, b);
+  swap_pair<true>(fmaxf(a, b), a, b);
+  return fmaxf(a, b);
+}
 __device__ __forceinline__ float xor_sum16_32(float v) {
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
+  float a, b;
+  swap_pair<false>(v, a, b);
+  swap_pair<true>(a + b, a, b);
+  return a + b;
+}
+// The value of lane i ^ 8 (the other half of the lane's 16-lane row): DPP
+// row_ror:8.
+__device__ __forceinline__ uint32_t lane_xor8(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float lane_xor8(float v) {
+  return __builtin_bit_cast(float, lane_xor8(__builtin_bit_cast(uint32_t, v)));
 }
 
 __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {

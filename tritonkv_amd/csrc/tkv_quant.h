@@ -50,11 +50,6 @@ __device__ __forceinline__ void minmax_dpp(float& mn, float& mx) {
   mx = fmaxf(mx, b);
 }
 
-// The value unchanged, but opaque to the optimizer (no instruction).
-__device__ __forceinline__ uint32_t opaque(uint32_t v) {
-  asm volatile("" : "+v"(v));
-  return v;
-}
 
 // Combine min/max across the lane pairs a permlane swap exchanges (rows 2k and
 // 2k+1 for SWAP32 = false, the two 32-lane halves for true).  Given the same
