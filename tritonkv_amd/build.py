@@ -3,7 +3,8 @@
     python -m tritonkv_amd.build          # or: __graft_entry__.build()
 
 Each ``.hip`` source is compiled to an object in parallel (the quantized split
-kernel's instantiations are spread over one file per K/V bit-width pair), then
+kernel's instantiations are spread over one file per K/V bit-width pair and
+head-column width), then
 linked into ``tritonkv_amd/libtkv_hip.so``.  Flags:
 
 * ``--offload-arch=gfx950`` only -- no other targets, no host fallback;
@@ -37,8 +38,8 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 OBJ = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libtkv_hip.so")
-SOURCES = ["decode_attention.hip", "quant_split_k4v4.hip", "quant_split_k2v2.hip",
-           "quant_split_k4v2.hip", "quant_split_k2v4.hip", "quant_pack.hip", "runtime.hip"]
+SOURCES = ["decode_attention.hip", "quant_pack.hip", "runtime.hip"] + [
+    f"quant_split_{bits}{hc}.hip" for bits in ("k4v4", "k2v2", "k4v2", "k2v4") for hc in ("", "_h4", "_h8")]
 ARCH = "gfx950"
 
 

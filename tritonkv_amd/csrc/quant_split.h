@@ -216,12 +216,15 @@ struct QOperandsPT {
   int eh;  // this lane's head's prescale exponent (as QOperands::eh)
 };
 
-template <int D, int KNB, int GS>
+// Column col carries head (col & 7) % HC of tile col >> 3 (HC = 8, or 4 when
+// the PV products give every head several columns).
+template <int D, int KNB, int GS, int HC>
 __device__ __forceinline__ void load_q_operands_pt(const SplitParams& prm, int b, int h0, int col,
                                                    int nh, int j, QOperandsPT<D, KNB, GS>& qo) {
   using QO = QOperandsPT<D, KNB, GS>;
   constexpr int NG = D / GS;
-  const int h = col & 7;
+  static_assert(HC == 8 || HC == 4, "head columns per tile");
+  const int h = col & (HC - 1);
   const bool hv = h < nh;
   const bool own = (col >> 3) == (j >> 1);  // these k-slots belong to this column's tile
   const int64_t qrow = ((int64_t)b * prm.HQ + h0 + (hv ? h : 0)) * D;
@@ -343,7 +346,7 @@ struct LdsKernelSmem {
 constexpr int kHiLoMaxLen = 256;
 
 
-template <int D, int KNB, int VNB, int GS, int NW, int NSTAGE, bool PAGED, bool PT, bool KCH = false>
+template <int D, int KNB, int VNB, int GS, int NW, int NSTAGE, bool PAGED, bool PT, bool KCH, int HS>
 __global__ void __launch_bounds__(NW * 64)
 quant_split_lds_kernel(SplitParams prm) {
   using SG = StageGeom<D, KNB, VNB, GS>;
@@ -357,6 +360,18 @@ quant_split_lds_kernel(SplitParams prm) {
   static_assert(2 * NG <= 16, "zero-point MFMA holds hi/lo of at most 8 groups");
   static_assert((NSTAGE - 1) * NI < 64, "vmcnt range");
   static_assert(!KCH || (!PAGED && !PT && GS <= 32), "per-channel keys: contiguous, one-tile path");
+  // Head columns of the PV products.  Column c of every PV MFMA carries query
+  // head c % HS.  With HS < 16 (GQA groups of at most HS heads) the 16 / HS
+  // copies of a head take different V groups: column c holds P * s_g for
+  // group g = v * S + c / HS in the v-th of NPG P' operands, so one packed
+  // multiply per token pair serves S groups where it used to serve one (the
+  // other columns carried padding heads).  A V MFMA over dims of group g then
+  // accumulates the true products in the columns of slot g % S only, and
+  // those are the ones written out.
+  static_assert(HS == 16 || (HS == 8 || HS == 4), "head columns");
+  static_assert(HS == 16 || NG >= 2, "one V group: nothing to share");
+  constexpr int S = 16 / HS;             // V-group slots per head
+  constexpr int NPG = (NG + S - 1) / S;  // P' operands per chunk
 
   __shared__ __attribute__((aligned(16))) uint8_t smem[NW * SM::WAVE + SM::PATCH];
 
@@ -374,6 +389,7 @@ quant_split_lds_kernel(SplitParams prm) {
   const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int r = lane & 15, j = lane >> 4;
   const int n = r;
+  const int slot = r / HS;  // V-group slot of this lane's column
   // Where a chunk's rows live.  Contiguous caches: one buffer resource per
   // tensor over this (b, kv head) block, chunk rows at token index cb.  Paged
   // caches: resources over the (pool page, kv head) slab holding the chunk
@@ -456,8 +472,8 @@ quant_split_lds_kernel(SplitParams prm) {
   // Per-channel keys multiply q by the chunk's channel scales in fp16 (q * s
   // as hi/lo pairs), so their q keeps eh = 0: a larger prescale could
   // overflow there.
-  if constexpr (PT) load_q_operands_pt<D, KNB, GS>(prm, b, h0, r, nh, j, qpt);
-  else load_q_operands<D, KNB, GS, KCH ? 0 : (KL::P - 1) * KNB>(prm, b, h0, n, nh, j, qo);
+  if constexpr (PT) load_q_operands_pt<D, KNB, GS, HS < 8 ? HS : 8>(prm, b, h0, r, nh, j, qpt);
+  else load_q_operands<D, KNB, GS, KCH ? 0 : (KL::P - 1) * KNB>(prm, b, h0, n % HS, nh, j, qo);
   const int eh = PT ? qpt.eh : qo.eh;
   const float zsc = __builtin_ldexpf(1.0f, eh - 24);  // code-dot units per score unit
   const u4* qf = qo.qf;
@@ -520,7 +536,7 @@ quant_split_lds_kernel(SplitParams prm) {
 #pragma unroll
   for (int m = 0; m < NKM; ++m) kmask[m] = slice_mask<KNB>(KL::slice_of(m, j));
 
-  constexpr bool kVChain = NG == 1;  // all slices of a V byte in one group
+  constexpr bool kVChain = NPG == 1;  // every V MFMA takes the same P' operand
 
   // Per-lane LDS byte offsets inside a stage.
   // K operand of tile a, load Lh: row 16a + r, byte load_offset(Lh, j).
@@ -550,6 +566,16 @@ quant_split_lds_kernel(SplitParams prm) {
   // Row NG of that operand is all ones (fp16 1.0 pairs), so the same MFMA also
   // accumulates sum_t p_t, the softmax denominator, from the very fp16
   // probabilities the PV products use.
+  // P' operand v of this lane: the V scales of group v * S + slot (clamped:
+  // a slot past the last group computes a copy nobody reads); dword offset of
+  // its fp16 pair in a staged [t][MROW] row and the v_perm selector of its half.
+  uint32_t soff[NPG], ssel[NPG];
+#pragma unroll
+  for (int v = 0; v < NPG; ++v) {
+    const int g = min(v * S + slot, NG - 1);
+    soff[v] = 2 * (g & ~1);
+    ssel[v] = (g & 1) ? 0x07060302u : 0x05040100u;
+  }
   const int zr = r < NG ? r : 0;
   const uint32_t zsel = r < NG ? ((r & 1) ? 0x07060302u : 0x05040100u) : 0x0C0C0C0Cu;
   const uint32_t zones = r == NG ? 0x3C003C00u : 0u;
@@ -689,12 +715,17 @@ quant_split_lds_kernel(SplitParams prm) {
         oz *= alpha;
 
       }
-      // tile 0 of head c is this lane's (c < 8), tile 1 is lane c + 8's
-      pb = u4{ph[0], ph[1], lane_xor8(ph[0]), lane_xor8(ph[1])};
-      if constexpr (HILO) {
-        const uint32_t l0 = pack_h2_rem(pf[0], pf[1], ph[0]), l1 = pack_h2_rem(pf[2], pf[3], ph[1]);
-        pbl = u4{l0, l1, lane_xor8(l0), lane_xor8(l1)};
-      }
+      // The PV operand of column c needs tile 0 then tile 1 of head c % HS:
+      // lane c holds tile c >> 3 of it and lane c ^ 8 the other tile.  (With
+      // HS = 16 the columns c >= 8 are padding heads and take any order.)
+      const bool swap = HS < 16 && r >= 8;
+      auto tiles = [&](uint32_t a0, uint32_t a1) -> u4 {
+        const uint32_t o0 = lane_xor8(a0), o1 = lane_xor8(a1);
+        return swap ? u4{o0, o1, a0, a1} : u4{a0, a1, o0, o1};
+      };
+      pb = tiles(ph[0], ph[1]);
+      if constexpr (HILO)
+        pbl = tiles(pack_h2_rem(pf[0], pf[1], ph[0]), pack_h2_rem(pf[2], pf[3], ph[1]));
     } else {
       // ---- scores S^T for the two 16-token tiles ---------------------------
       float x[8];
@@ -854,25 +885,27 @@ quant_split_lds_kernel(SplitParams prm) {
       oz = mfma_k32(u4{zp[0], zp[1], zp[2], zp[3]}, pb, oz);
       if constexpr (HILO) oz = mfma_k32(u4{zp[0], zp[1], zp[2], zp[3]}, pbl, oz);
     }
-    // ---- P'_g = P * s_g ------------------------------------------------------
-    u4 pg[NG];
-    u4 pgl[HILO ? NG : 1];
+    // ---- P' = P * s_g, g = v * S + slot ----------------------------------------
+    u4 pg[NPG];
+    u4 pgl[HILO ? NPG : 1];
 #pragma unroll
-    for (int g = 0; g < NG; ++g) {
+    for (int v = 0; v < NPG; ++v) {
       uint32_t sp[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int t0 = slot_token(j, 2 * q), t1 = slot_token(j, 2 * q + 1);
-        sp[q] = perm(dword_at(mvs, t1, g), dword_at(mvs, t0, g), (g & 1) ? 0x07060302u : 0x05040100u);
+        const uint32_t d0 = *reinterpret_cast<const uint32_t*>(mvs + 2 * t0 * SG::MROW + soff[v]);
+        const uint32_t d1 = *reinterpret_cast<const uint32_t*>(mvs + 2 * t1 * SG::MROW + soff[v]);
+        sp[q] = perm(d1, d0, ssel[v]);
         if constexpr (TAIL) sp[q] &= tail_pair_mask(cb + t0, cb + t1);
       }
-      pg[g] = u4{pk_mul(pb[0], sp[0]), pk_mul(pb[1], sp[1]), pk_mul(pb[2], sp[2]), pk_mul(pb[3], sp[3])};
+      pg[v] = u4{pk_mul(pb[0], sp[0]), pk_mul(pb[1], sp[1]), pk_mul(pb[2], sp[2]), pk_mul(pb[3], sp[3])};
       if constexpr (HILO) {
         // P * s = pg + (pb * s - pg) + pbl * s: the exact remainder of the
         // fp16 product plus the low part's product, summed in fp16
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          pgl[g][q] = pk_add(pk_fma_rem(pb[q], sp[q], pg[g][q]), pk_mul(pbl[q], sp[q]));
+          pgl[v][q] = pk_add(pk_fma_rem(pb[q], sp[q], pg[v][q]), pk_mul(pbl[q], sp[q]));
       }
     }
 
@@ -890,12 +923,13 @@ quant_split_lds_kernel(SplitParams prm) {
         uint32_t pm[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) pm[i] = perm(vx[2 * i + 1], vx[2 * i], vsel[e]);
-        // With one group per row (NG == 1) every slice of a byte shares the
-        // same P', so slice p's MFMA may take the byte with only the slices
-        // above p cleared (the top slice: the raw byte): its accumulator holds
-        // the codes of slices <= p at their bit positions, and slice p alone
-        // is recovered after the loop as acc[p] - acc[p - 1] -- one AND fewer
-        // per byte pair.  Slices below p weigh less than slice p's own code
+        // When every V MFMA takes the same P' operand (one V group, or head
+        // columns that give each group columns of its own: NPG == 1), every
+        // slice of a byte meets the same P' in each column, so slice p's MFMA
+        // may take the byte with only the slices above p cleared (the top
+        // slice: the raw byte): its accumulator holds the codes of slices
+        // <= p at their bit positions, and slice p alone is recovered after
+        // the loop as acc[p] - acc[p - 1] -- one AND fewer per byte pair.  Slices below p weigh less than slice p's own code
         // (c * 2^(p*VNB) against at most 2^(p*VNB) - 1), so that difference
         // loses at most about one bit of the accumulators' precision.  (The
         // other direction, clearing the slices below p and subtracting
@@ -909,8 +943,8 @@ quant_split_lds_kernel(SplitParams prm) {
           const uint32_t msk = kVChain ? lo_slices_mask<VNB>(p) : slice_mask<VNB>(p);
           const u4 av = (kVChain && p == VL::P - 1) ? u4{pm[0], pm[1], pm[2], pm[3]}
                                                     : u4{pm[0] & msk, pm[1] & msk, pm[2] & msk, pm[3] & msk};
-          accv[mv] = mfma_k32(av, pg[VL::group_of(mv)], accv[mv]);
-          if constexpr (HILO) accv[mv] = mfma_k32(av, pgl[VL::group_of(mv)], accv[mv]);
+          accv[mv] = mfma_k32(av, pg[VL::group_of(mv) / S], accv[mv]);
+          if constexpr (HILO) accv[mv] = mfma_k32(av, pgl[VL::group_of(mv) / S], accv[mv]);
         }
       }
     }
@@ -961,8 +995,10 @@ quant_split_lds_kernel(SplitParams prm) {
       const float zv = ozg[VL::group_of(mv)];
       f4 a = accv[mv];
       if (kVChain && p > 0) a -= accv[VL::mfma_index(p - 1, VL::window_of(mv), VL::e_of(mv))];
+      if (S == 1 || VL::group_of(mv) % S == slot) {  // this column's products are group mv's
 #pragma unroll
-      for (int i = 0; i < 4; ++i) wp.o[n][VL::dim_of(mv, 4 * j + i)] = fmaf(a[i], fac, zv);
+        for (int i = 0; i < 4; ++i) wp.o[n % HS][VL::dim_of(mv, 4 * j + i)] = fmaf(a[i], fac, zv);
+      }
     }
     if (j == 0) {
       wp.m[n] = m_run;
@@ -983,15 +1019,19 @@ quant_split_lds_kernel(SplitParams prm) {
 constexpr int kStages8 = 2;
 constexpr int kStages4 = 2;
 
-template <int D, int KNB, int VNB, int GS, bool PT>
+template <int D, int KNB, int VNB, int GS, bool PT, int HS>
 void launch_quant_pt(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
   const bool paged = p.page_size > 0;
   if (waves == 8) {
-    if (paged) quant_split_lds_kernel<D, KNB, VNB, GS, 8, 2, true, PT><<<grid, dim3(8 * 64), 0, st>>>(p);
-    else quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, PT><<<grid, dim3(8 * 64), 0, st>>>(p);
+    if (paged)
+      quant_split_lds_kernel<D, KNB, VNB, GS, 8, 2, true, PT, false, HS><<<grid, dim3(8 * 64), 0, st>>>(p);
+    else
+      quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, PT, false, HS><<<grid, dim3(8 * 64), 0, st>>>(p);
   } else {
-    if (paged) quant_split_lds_kernel<D, KNB, VNB, GS, 4, 2, true, PT><<<grid, dim3(4 * 64), 0, st>>>(p);
-    else quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false, PT><<<grid, dim3(4 * 64), 0, st>>>(p);
+    if (paged)
+      quant_split_lds_kernel<D, KNB, VNB, GS, 4, 2, true, PT, false, HS><<<grid, dim3(4 * 64), 0, st>>>(p);
+    else
+      quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false, PT, false, HS><<<grid, dim3(4 * 64), 0, st>>>(p);
   }
 }
 
@@ -1056,20 +1096,38 @@ void launch_read_probe(const SplitParams& p, dim3 grid, int waves, hipStream_t s
   else read_probe_kernel<D, KNB, VNB, GS, 4><<<grid, dim3(4 * 64), 0, st>>>(p);
 }
 
-template <int D, int KNB, int VNB, int GS>
-void launch_quant(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
+// One head-column width HS (the kernels of one width are instantiated in a
+// translation unit of their own, quant_split_k*v*[_h*].hip).
+template <int D, int KNB, int VNB, int GS, int HS>
+void launch_quant_hs(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
   if constexpr (GS <= 32) {
     if (p.key_block) {  // per-channel keys (the host checked: contiguous, no fused append)
       if (waves == 8)
-        quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, false, true><<<grid, dim3(8 * 64), 0, st>>>(p);
+        quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, false, true, HS>
+            <<<grid, dim3(8 * 64), 0, st>>>(p);
       else
-        quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false, false, true><<<grid, dim3(4 * 64), 0, st>>>(p);
+        quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false, false, true, HS>
+            <<<grid, dim3(4 * 64), 0, st>>>(p);
       return;
     }
   }
   if (p.G <= 8 && p.split_size >= kPairedTilesMinSplit)
-    launch_quant_pt<D, KNB, VNB, GS, true>(p, grid, waves, st);
-  else launch_quant_pt<D, KNB, VNB, GS, false>(p, grid, waves, st);
+    launch_quant_pt<D, KNB, VNB, GS, true, HS>(p, grid, waves, st);
+  else launch_quant_pt<D, KNB, VNB, GS, false, HS>(p, grid, waves, st);
+}
+
+// Head-column width of a launch: the narrowest of 4, 8, 16 that holds the GQA
+// group, when there are V groups to share the columns (D / GS >= 2).
+template <int D, int GS>
+constexpr bool kHeadColumns = D / GS >= 2;
+
+template <int D, int KNB, int VNB, int GS>
+void launch_quant(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
+  if constexpr (kHeadColumns<D, GS>) {
+    if (p.G <= 4) return launch_quant_hs<D, KNB, VNB, GS, 4>(p, grid, waves, st);
+    if (p.G <= 8) return launch_quant_hs<D, KNB, VNB, GS, 8>(p, grid, waves, st);
+  }
+  launch_quant_hs<D, KNB, VNB, GS, 16>(p, grid, waves, st);
 }
 
 }  // namespace tkv

@@ -1,7 +1,20 @@
-// quant_split_lds_kernel (and read-probe) instantiations for 2-bit K and 2-bit V codes.
+// quant_split_lds_kernel (and read-probe) instantiations for 2-bit K and 2-bit V codes:
+// the launch dispatcher and the kernels with 16 head columns.  The 4- and 8-column
+// kernels are instantiated in quant_split_k2v2_h4.hip and quant_split_k2v2_h8.hip.
 #include "quant_split.h"
 
 namespace tkv {
+
+extern template void launch_quant_hs<128, 2, 2, 16, 4>(const SplitParams&, dim3, int, hipStream_t);
+extern template void launch_quant_hs<128, 2, 2, 32, 4>(const SplitParams&, dim3, int, hipStream_t);
+extern template void launch_quant_hs<128, 2, 2, 64, 4>(const SplitParams&, dim3, int, hipStream_t);
+extern template void launch_quant_hs<64, 2, 2, 16, 4>(const SplitParams&, dim3, int, hipStream_t);
+extern template void launch_quant_hs<64, 2, 2, 32, 4>(const SplitParams&, dim3, int, hipStream_t);
+extern template void launch_quant_hs<128, 2, 2, 16, 8>(const SplitParams&, dim3, int, hipStream_t);
+extern template void launch_quant_hs<128, 2, 2, 32, 8>(const SplitParams&, dim3, int, hipStream_t);
+extern template void launch_quant_hs<128, 2, 2, 64, 8>(const SplitParams&, dim3, int, hipStream_t);
+extern template void launch_quant_hs<64, 2, 2, 16, 8>(const SplitParams&, dim3, int, hipStream_t);
+extern template void launch_quant_hs<64, 2, 2, 32, 8>(const SplitParams&, dim3, int, hipStream_t);
 
 template void launch_quant<128, 2, 2, 16>(const SplitParams&, dim3, int, hipStream_t);
 template void launch_quant<128, 2, 2, 32>(const SplitParams&, dim3, int, hipStream_t);
@@ -10,6 +23,13 @@ template void launch_quant<128, 2, 2, 128>(const SplitParams&, dim3, int, hipStr
 template void launch_quant<64, 2, 2, 16>(const SplitParams&, dim3, int, hipStream_t);
 template void launch_quant<64, 2, 2, 32>(const SplitParams&, dim3, int, hipStream_t);
 template void launch_quant<64, 2, 2, 64>(const SplitParams&, dim3, int, hipStream_t);
+template void launch_quant_hs<128, 2, 2, 16, 16>(const SplitParams&, dim3, int, hipStream_t);
+template void launch_quant_hs<128, 2, 2, 32, 16>(const SplitParams&, dim3, int, hipStream_t);
+template void launch_quant_hs<128, 2, 2, 64, 16>(const SplitParams&, dim3, int, hipStream_t);
+template void launch_quant_hs<128, 2, 2, 128, 16>(const SplitParams&, dim3, int, hipStream_t);
+template void launch_quant_hs<64, 2, 2, 16, 16>(const SplitParams&, dim3, int, hipStream_t);
+template void launch_quant_hs<64, 2, 2, 32, 16>(const SplitParams&, dim3, int, hipStream_t);
+template void launch_quant_hs<64, 2, 2, 64, 16>(const SplitParams&, dim3, int, hipStream_t);
 
 template void launch_read_probe<128, 2, 2, 16>(const SplitParams&, dim3, int, hipStream_t);
 template void launch_read_probe<128, 2, 2, 32>(const SplitParams&, dim3, int, hipStream_t);
