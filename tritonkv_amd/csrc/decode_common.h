@@ -81,7 +81,7 @@ __device__ __forceinline__ bool softmax_chunk(const float (&x)[8], float lscale,
   const bool any_moved = __builtin_amdgcn_ballot_w64(moved) != 0;
   alpha = 1.0f;
   if (any_moved) {
-    const float mn = fmaxf(m, mx);
+    const float mn = vmax(m, mx);
     alpha = safe_exp2_diff(m, mn);
     m = mn;
     if constexpr (TRACK_L) l *= alpha;

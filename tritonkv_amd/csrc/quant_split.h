@@ -40,7 +40,11 @@ struct StageGeom {
   static constexpr int K_OFF = 0;
   static constexpr int V_OFF = K_OFF + KB;
   static constexpr int M_OFF = V_OFF + VB;    // ks, kz, vs, vz at M_OFF + t * MB
-  static constexpr int BYTES = M_OFF + 4 * MB;
+  // MB bytes of fp16 1.0 pairs behind vz: the ones row of the V zero-point
+  // MFMA reads them through the same offsets as the zero points (written
+  // once per launch; no DMA touches them).
+  static constexpr int ONES_OFF = M_OFF + 4 * MB;
+  static constexpr int BYTES = ONES_OFF + MB;
   static constexpr int NKI = (KB + 1023) / 1024;  // 16-byte-lane DMA instructions for K
   static constexpr int NVI = (VB + 1023) / 1024;
   static constexpr int NMI = (MB + 255) / 256;    // dword-lane DMA instructions per tensor
@@ -302,13 +306,13 @@ __device__ __forceinline__ void load_q_operands_pt(const SplitParams& prm, int b
 __device__ __forceinline__ bool softmax_chunk_pt(const float (&x)[4], float lscale, float& m,
                                                  float& alpha, uint32_t (&ph)[2], float (&p)[4]) {
   float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-  mx = fmaxf(mx, lane_xor8(mx));
+  mx = vmax(mx, lane_xor8(mx));
   mx = xor_max16_32(mx) * lscale;
   const bool moved = mx > m;
   const bool any_moved = __builtin_amdgcn_ballot_w64(moved) != 0;
   alpha = 1.0f;
   if (any_moved) {
-    const float mn = fmaxf(m, mx);
+    const float mn = vmax(m, mx);
     alpha = safe_exp2_diff(m, mn);
     m = mn;
   }
@@ -437,6 +441,10 @@ quant_split_lds_kernel(SplitParams prm) {
     return min(max((int)__builtin_amdgcn_readfirstlane(e), 0), prm.num_pages - 1);
   };
   uint8_t* ring = smem + w * SM::WAVE;
+#pragma unroll
+  for (int s = 0; s < NSTAGE; ++s)
+    for (int i = lane; i < SG::MB / 4; i += 64)
+      reinterpret_cast<uint32_t*>(ring + s * SG::BYTES + SG::ONES_OFF)[i] = 0x3C003C00u;
 
   // Chunk k of this wave starts at token lo + 32 * (w + NW * k).
   const int cb0 = lo + kChunk * w;
@@ -559,13 +567,6 @@ quant_split_lds_kernel(SplitParams prm) {
     const int ob = VL::dword_offset(wi, r);
     voff[wi] = SG::V_OFF + SG::template pos_of<VL::DP>(4 * j, ob >> 4) * 16 + (ob & 15);
   }
-  // V zero point rows r < NG of the zero MFMA's A operand, zeros for r >= NG.
-  // Lane r < NG gathers group r's zero points of two tokens into one fp16
-  // pair with a single v_perm (low or high half of each token's dword); the
-  // selector of lanes r >= NG yields constant zero bytes.
-  // Row NG of that operand is all ones (fp16 1.0 pairs), so the same MFMA also
-  // accumulates sum_t p_t, the softmax denominator, from the very fp16
-  // probabilities the PV products use.
   // P' operand v of this lane: the V scales of group v * S + slot (clamped:
   // a slot past the last group computes a copy nobody reads); dword offset of
   // its fp16 pair in a staged [t][MROW] row and the v_perm selector of its half.
@@ -576,9 +577,16 @@ quant_split_lds_kernel(SplitParams prm) {
     soff[v] = 2 * (g & ~1);
     ssel[v] = (g & 1) ? 0x07060302u : 0x05040100u;
   }
-  const int zr = r < NG ? r : 0;
-  const uint32_t zsel = r < NG ? ((r & 1) ? 0x07060302u : 0x05040100u) : 0x0C0C0C0Cu;
-  const uint32_t zones = r == NG ? 0x3C003C00u : 0u;
+  // A operand of the V zero-point MFMA: row r < NG holds group r's zero
+  // points, gathered for two tokens into one fp16 pair with a single v_perm
+  // (low or high half of each token's dword); row NG is all ones (fp16 1.0
+  // pairs, read from the stage's ones area through the same offsets), so the
+  // same MFMA also accumulates sum_t p_t, the softmax denominator, from the
+  // very fp16 probabilities the PV products use; rows r > NG are zero (their
+  // selector yields constant zero bytes).
+  const int zoff = r < NG ? 2 * (r & ~1) : SG::MB;
+  const uint32_t zsel = r < NG ? ((r & 1) ? 0x07060302u : 0x05040100u)
+                               : (r == NG ? 0x05040100u : 0x0C0C0C0Cu);
 
   f4 accv[NVM];
 #pragma unroll
@@ -878,9 +886,9 @@ quant_split_lds_kernel(SplitParams prm) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int t0 = slot_token(j, 2 * q), t1 = slot_token(j, 2 * q + 1);
-        zp[q] = perm(dword_at(mvz, t1, zr), dword_at(mvz, t0, zr), zsel);
+        zp[q] = perm(*reinterpret_cast<const uint32_t*>(mvz + zoff + 2 * t1 * SG::MROW),
+                     *reinterpret_cast<const uint32_t*>(mvz + zoff + 2 * t0 * SG::MROW), zsel);
         if constexpr (TAIL) zp[q] &= tail_pair_mask(cb + t0, cb + t1);
-        zp[q] |= zones;
       }
       oz = mfma_k32(u4{zp[0], zp[1], zp[2], zp[3]}, pb, oz);
       if constexpr (HILO) oz = mfma_k32(u4{zp[0], zp[1], zp[2], zp[3]}, pbl, oz);

@@ -96,10 +96,19 @@ __device__ __forceinline__ void swap_pair(float v, float& a, float& b) {
   a = __builtin_bit_cast(float, opaque(s[0]));
   b = __builtin_bit_cast(float, opaque(s[1]));
 }
+// max(a, b) as one v_max_f32.  fmaxf first quiets each operand the compiler
+// cannot prove canonical -- every value that comes out of a DPP move or a lane
+// swap -- at one more instruction per operand; the operands here are scores
+// and running maxima, never signalling NaNs.
+__device__ __forceinline__ float vmax(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
 __device__ __forceinline__ float max_xor16(float v) {
   float a, b;
   swap_pair<false>(v, a, b);
-  return fmaxf(a, b);
+  return vmax(a, b);
 }
 __device__ __forceinline__ float sum_xor16(float v) {
   float a, b;
@@ -109,8 +118,8 @@ __device__ __forceinline__ float sum_xor16(float v) {
 __device__ __forceinline__ float xor_max16_32(float v) {
   float a, b;
   swap_pair<false>(v, a, b);
-  swap_pair<true>(fmaxf(a, b), a, b);
-  return fmaxf(a, b);
+  swap_pair<true>(vmax(a, b), a, b);
+  return vmax(a, b);
 }
 __device__ __forceinline__ float xor_sum16_32(float v) {
   float a, b;
@@ -121,7 +130,7 @@ __device__ __forceinline__ float xor_sum16_32(float v) {
 // The value of lane i ^ 8 (the other half of the lane's 16-lane row): DPP
 // row_ror:8.
 __device__ __forceinline__ uint32_t lane_xor8(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, true);
 }
 __device__ __forceinline__ float lane_xor8(float v) {
   return __builtin_bit_cast(float, lane_xor8(__builtin_bit_cast(uint32_t, v)));
