@@ -247,87 +247,104 @@ __device__ __forceinline__ void load_q_operands(const SplitParams& prm, int b, i
   using KL = KLayout<D, KNB, GS>;
   constexpr int NG = D / GS;
   constexpr int NKM = KL::NKM;
-  u4* qf = qo.qf;
-  u2& qzb = qo.qzb;
-  float qz[NG];
-#pragma unroll
-  for (int g = 0; g < NG; ++g) qz[g] = 0.0f;
-  {
-    const bool hv = n < nh;
-    const int64_t qrow = ((int64_t)b * prm.HQ + h0 + (hv ? n : 0)) * D;
-    float qv[NKM][KL::CB];
-    if (prm.q_fp32) {
-      const float* qp = static_cast<const float*>(prm.q) + qrow;
-#pragma unroll
-      for (int m = 0; m < NKM; ++m)
-#pragma unroll
-        for (int c = 0; c < KL::CB; c += 4) {
-          const f4 v = *reinterpret_cast<const f4*>(qp + m * KL::KSTEP + KL::CB * j + c);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) qv[m][c + e] = (float)(_Float16)v[e];
-        }
-    } else {
-      const _Float16* qp = static_cast<const _Float16*>(prm.q) + qrow;
-#pragma unroll
-      for (int m = 0; m < NKM; ++m) {
-        if constexpr (KL::CB == 8) {
-          const h8 v = *reinterpret_cast<const h8*>(qp + m * KL::KSTEP + KL::CB * j);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) qv[m][e] = (float)v[e];
-        } else {
-          const h4 v = *reinterpret_cast<const h4*>(qp + m * KL::KSTEP + KL::CB * j);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) qv[m][e] = (float)v[e];
-        }
-      }
-    }
-    float amax = 0.0f;
+  constexpr int NP = KL::CB / 2;  // fp16 pairs per step and lane
+  // q stays in fp16 pairs throughout (an fp32 q is rounded to fp16 first, as
+  // the reference's fp16 MFMA operand does): the max |q| is an integer max of
+  // the magnitude bits, the prescale one packed multiply by a power of two
+  // (the same rounding as scaling in fp32 and rounding once), and a head past
+  // nh is cleared with one AND per operand dword.
+  const bool hv = n < nh;
+  const uint32_t hvm = hv ? 0xFFFFFFFFu : 0u;
+  const int64_t qrow = ((int64_t)b * prm.HQ + h0 + (hv ? n : 0)) * D;
+  uint32_t qh[NKM][NP];  // natural-order pairs of the lane's CB dims of step m
+  if (prm.q_fp32) {
+    const float* qp = static_cast<const float*>(prm.q) + qrow;
 #pragma unroll
     for (int m = 0; m < NKM; ++m)
 #pragma unroll
-      for (int c = 0; c < KL::CB; ++c) amax = fmaxf(amax, hv ? fabsf(qv[m][c]) : 0.0f);
-    qo.eh = q_prescale_exp(xor_max16_32(amax), EMAX);
+      for (int c = 0; c < KL::CB; c += 4) {
+        const f4 v = *reinterpret_cast<const f4*>(qp + m * KL::KSTEP + KL::CB * j + c);
+        qh[m][c / 2] = pack_h2(v[0], v[1]);
+        qh[m][c / 2 + 1] = pack_h2(v[2], v[3]);
+      }
+  } else {
+    const _Float16* qp = static_cast<const _Float16*>(prm.q) + qrow;
 #pragma unroll
     for (int m = 0; m < NKM; ++m) {
-      const int p = KL::slice_of(m, j);
-      const float pre = __builtin_ldexpf(1.0f, qo.eh - p * KNB);
-      uint32_t wv[4] = {0, 0, 0, 0};
+      if constexpr (KL::CB == 8) {
+        const u4 v = *reinterpret_cast<const u4*>(qp + m * KL::KSTEP + KL::CB * j);
 #pragma unroll
-      for (int s2 = 0; s2 < KL::CB; s2 += 2) {
-        const float q0 = hv ? qv[m][slot_byte(s2)] : 0.0f;
-        const float q1 = hv ? qv[m][slot_byte(s2 + 1)] : 0.0f;
-        qz[KL::group_of_step(m)] += q0 + q1;
-        wv[s2 / 2] = pack_h2(q0 * pre, q1 * pre);
+        for (int e = 0; e < 4; ++e) qh[m][e] = v[e];
+      } else {
+        const u2 v = *reinterpret_cast<const u2*>(qp + m * KL::KSTEP + KL::CB * j);
+        qh[m][0] = v[0];
+        qh[m][1] = v[1];
       }
-      qf[m] = u4{wv[0], wv[1], wv[2], wv[3]};
-      uint32_t nv[4] = {0, 0, 0, 0};
+    }
+  }
+  typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+  us2 mag = us2{0, 0};
 #pragma unroll
-      for (int s2 = 0; s2 < KL::CB; s2 += 2)
-        nv[s2 / 2] = hv ? pack_h2(qv[m][s2], qv[m][s2 + 1]) : 0u;
-      qo.qn[m] = u4{nv[0], nv[1], nv[2], nv[3]};
+  for (int m = 0; m < NKM; ++m)
+#pragma unroll
+    for (int e = 0; e < NP; ++e)
+      mag = __builtin_elementwise_max(mag, __builtin_bit_cast(us2, qh[m][e] & 0x7FFF7FFFu));
+  const uint32_t mbits = mag[0] > mag[1] ? mag[0] : mag[1];
+  const float amax = hv ? (float)__builtin_bit_cast(_Float16, (unsigned short)mbits) : 0.0f;
+  qo.eh = q_prescale_exp(xor_max16_32(amax), EMAX);
+  float qz[NG];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) qz[g] = 0.0f;
+  const h2 ones = h2{(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+  for (int m = 0; m < NKM; ++m) {
+    // 2^(eh - p * KNB) as an fp16 pair: eh >= -1 and p * KNB <= 6, so the
+    // exponent stays in the normal range
+    const int p = KL::slice_of(m, j);
+    const uint32_t pe = (uint32_t)(qo.eh - p * KNB + 15) << 10;
+    const uint32_t pre = pe | (pe << 16);
+    // slot order: pairs of dims (0,2) (1,3) (4,6) (5,7) of the step
+    uint32_t sl[NP];
+#pragma unroll
+    for (int e = 0; e < NP; e += 2) {
+      sl[e] = perm(qh[m][e + 1], qh[m][e], 0x05040100u);
+      sl[e + 1] = perm(qh[m][e + 1], qh[m][e], 0x07060302u);
     }
 #pragma unroll
-    for (int g = 0; g < NG; ++g) qz[g] = xor_sum16_32(qz[g]);
+    for (int e = 0; e < 4; ++e) {
+      qo.qf[m][e] = e < NP ? pk_mul(sl[e], pre) & hvm : 0u;
+      qo.qn[m][e] = e < NP ? qh[m][e] & hvm : 0u;
+    }
+    float zs = 0.0f;
+#pragma unroll
+    for (int e = 0; e < NP; ++e)
+      zs = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, qh[m][e]), ones, zs, false);
+    qz[KL::group_of_step(m)] += zs;
   }
+#pragma unroll
+  for (int g = 0; g < NG; ++g) qz[g] = xor_sum16_32(hv ? qz[g] : 0.0f);
   // B operand of the K zero-point MFMA: k-slot k < NG holds fp16(Qz_k),
   // NG <= k < 2NG the fp16 remainder Qz - fp16(Qz), so the product with the
-  // exact fp16 zero points keeps fp32 precision.
-  {
-    float hl[4];
+  // exact fp16 zero points keeps fp32 precision.  Lane group j holds k-slots
+  // 4j .. 4j + 3.
+  float hiv[NG], lov[NG];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int k = 4 * j + i;
-      float v = 0.0f;
-#pragma unroll
-      for (int g = 0; g < NG; ++g) {
-        const float hi16 = (float)(_Float16)qz[g];
-        if (k == g) v = hi16;
-        if (k == NG + g) v = qz[g] - hi16;
-      }
-      hl[i] = v;
-    }
-    qzb = u2{pack_h2(hl[0], hl[1]), pack_h2(hl[2], hl[3])};
+  for (int g = 0; g < NG; ++g) {
+    hiv[g] = (float)(_Float16)qz[g];
+    lov[g] = qz[g] - hiv[g];
   }
+  float hl[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float v = 0.0f;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int k = 4 * jj + i;
+      if (k < 2 * NG && j == jj) v = k < NG ? hiv[k < NG ? k : 0] : lov[k >= NG && k < 2 * NG ? k - NG : 0];
+    }
+    hl[i] = v;
+  }
+  qo.qzb = u2{pack_h2(hl[0], hl[1]), pack_h2(hl[2], hl[3])};
 }
 
 }  // namespace tkv
