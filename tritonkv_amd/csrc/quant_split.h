@@ -228,15 +228,18 @@ __device__ __forceinline__ void load_q_operands_pt(const SplitParams& prm, int b
   using QO = QOperandsPT<D, KNB, GS>;
   constexpr int NG = D / GS;
   static_assert(HC == 8 || HC == 4, "head columns per tile");
+  // q stays in fp16 pairs, as in load_q_operands: integer max of the
+  // magnitude bits, one packed prescale multiply per operand dword, and the
+  // other tile's k-slots (and heads past nh) cleared with one AND.
   const int h = col & (HC - 1);
   const bool hv = h < nh;
   const bool own = (col >> 3) == (j >> 1);  // these k-slots belong to this column's tile
+  const uint32_t hvm = hv ? 0xFFFFFFFFu : 0u;
+  const uint32_t opm = (hv && own) ? 0xFFFFFFFFu : 0u;
   const int64_t qrow = ((int64_t)b * prm.HQ + h0 + (hv ? h : 0)) * D;
-  float qz[NG];
-#pragma unroll
-  for (int g = 0; g < NG; ++g) qz[g] = 0.0f;
-  // All loads first, in one branch, so they are in flight together.
-  float qv[QO::NB][8];
+  // natural-order pairs of the lane's 8 dims of block bi: dims
+  // (bi / NU) * DP + 16 * (bi % NU) + 8 * (j & 1) .. + 7
+  uint32_t qh[QO::NB][4];
   if (prm.q_fp32) {
     const float* qp = static_cast<const float*>(prm.q) + qrow + 8 * (j & 1);
 #pragma unroll
@@ -244,45 +247,57 @@ __device__ __forceinline__ void load_q_operands_pt(const SplitParams& prm, int b
       const int d0 = (bi / QO::NU) * QO::DP + 16 * (bi % QO::NU);
       const f4 a = *reinterpret_cast<const f4*>(qp + d0);
       const f4 c = *reinterpret_cast<const f4*>(qp + d0 + 4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        qv[bi][e] = (float)(_Float16)a[e];
-        qv[bi][4 + e] = (float)(_Float16)c[e];
-      }
+      qh[bi][0] = pack_h2(a[0], a[1]);
+      qh[bi][1] = pack_h2(a[2], a[3]);
+      qh[bi][2] = pack_h2(c[0], c[1]);
+      qh[bi][3] = pack_h2(c[2], c[3]);
     }
   } else {
     const _Float16* qp = static_cast<const _Float16*>(prm.q) + qrow + 8 * (j & 1);
 #pragma unroll
     for (int bi = 0; bi < QO::NB; ++bi) {
       const int d0 = (bi / QO::NU) * QO::DP + 16 * (bi % QO::NU);
-      const h8 v = *reinterpret_cast<const h8*>(qp + d0);
+      const u4 v = *reinterpret_cast<const u4*>(qp + d0);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) qv[bi][e] = (float)v[e];
+      for (int e = 0; e < 4; ++e) qh[bi][e] = v[e];
     }
   }
-  // lanes j and j ^ 1 hold the two halves of each 16-dim block of the head
-  float amax = 0.0f;
+  typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+  us2 mag = us2{0, 0};
 #pragma unroll
   for (int bi = 0; bi < QO::NB; ++bi)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, hv ? fabsf(qv[bi][e]) : 0.0f);
+    for (int e = 0; e < 4; ++e)
+      mag = __builtin_elementwise_max(mag, __builtin_bit_cast(us2, qh[bi][e] & 0x7FFF7FFFu));
+  const uint32_t mbits = mag[0] > mag[1] ? mag[0] : mag[1];
+  const float amax = hv ? (float)__builtin_bit_cast(_Float16, (unsigned short)mbits) : 0.0f;
+  // lanes j and j ^ 1 hold the two halves of each 16-dim block of the head
   qo.eh = q_prescale_exp(max_xor16(amax), (QO::P - 1) * KNB);
+  float qz[NG];
 #pragma unroll
-  for (int p = 0; p < QO::P; ++p)
+  for (int g = 0; g < NG; ++g) qz[g] = 0.0f;
+  const h2 ones = h2{(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+  for (int p = 0; p < QO::P; ++p) {
+    // 2^(eh - p * KNB) as an fp16 pair (a normal number: eh >= -1, p * KNB <= 6)
+    const uint32_t pe = (uint32_t)(qo.eh - p * KNB + 15) << 10;
+    const uint32_t pre = pe | (pe << 16);
 #pragma unroll
     for (int u = 0; u < QO::NU; ++u) {
+      const int bi = p * QO::NU + u;
       const int g = (p * QO::DP + 16 * u) / GS;
-      const float pre = __builtin_ldexpf(1.0f, qo.eh - p * KNB);
-      uint32_t wv[4];
+      // slot order: pairs of dims (0,2) (1,3) (4,6) (5,7)
+      const uint32_t sl[4] = {perm(qh[bi][1], qh[bi][0], 0x05040100u), perm(qh[bi][1], qh[bi][0], 0x07060302u),
+                              perm(qh[bi][3], qh[bi][2], 0x05040100u), perm(qh[bi][3], qh[bi][2], 0x07060302u)};
+      qo.qb[bi] = u4{pk_mul(sl[0], pre) & opm, pk_mul(sl[1], pre) & opm, pk_mul(sl[2], pre) & opm,
+                     pk_mul(sl[3], pre) & opm};
+      float zs = 0.0f;
 #pragma unroll
-      for (int s2 = 0; s2 < 8; s2 += 2) {
-        const float q0 = hv ? qv[p * QO::NU + u][slot_byte(s2)] : 0.0f;
-        const float q1 = hv ? qv[p * QO::NU + u][slot_byte(s2 + 1)] : 0.0f;
-        qz[g] += q0 + q1;
-        wv[s2 / 2] = own ? pack_h2(q0 * pre, q1 * pre) : 0u;
-      }
-      qo.qb[p * QO::NU + u] = u4{wv[0], wv[1], wv[2], wv[3]};
+      for (int e = 0; e < 4; ++e)
+        zs = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, qh[bi][e] & hvm), ones, zs, false);
+      qz[g] += zs;
     }
+  }
   // lanes j and j ^ 1 hold the two halves of every 16-dim block (j ^ 2 repeats them)
 #pragma unroll
   for (int g = 0; g < NG; ++g) qz[g] = sum_xor16(qz[g]);
