@@ -10,7 +10,8 @@
  *   pack_codes / unpack_codes quantize.py:149-183
  *   quantize_groupwise        quantize.py:186-236
  *   dequantize_groupwise      quantize.py:239-246
- *   reference attention       reference.py:61-88 (fp32 scores, softmax, weighted sum)
+ *   reference attention       reference.py:61-88 (scores, softmax, weighted sum; fp32
+ *                             inputs, sums accumulated in binary64, see attend_head)
  *
  * Built with plain IEEE binary32 arithmetic (no -ffast-math): division is
  * correctly rounded, rintf() rounds half to even in the default rounding mode,
@@ -150,26 +151,34 @@ void tkvo_dequantize(const uint8_t *packed, const uint16_t *scale16, const uint1
 
 /* ---- fp32 decode attention ------------------------------------------- */
 
+/* Scores, softmax and the weighted sum accumulate in binary64 and the result
+ * is rounded to binary32 once.  The reference computes in fp32 on the GPU,
+ * where every reduction is a tree; a scalar loop summing tens of thousands of
+ * fp32 terms in order (an fp32 accumulator of ~19 taking addends of 1e-5)
+ * drifts by up to ~2e-4 relative, more than the kernel's own error, so the
+ * checker keeps the sums exact to well below fp32 resolution instead.  The
+ * inputs (dequantized K and V, q) are the fp32 values the reference sees. */
 static void attend_head(const float *q, const float *krows, const float *vrows, int n, int D,
-                        float sm_scale, float *scores, float *out) {
-    float m = -INFINITY;
+                        float sm_scale, double *scores, double *acc, float *out) {
+    double m = -INFINITY;
     for (int t = 0; t < n; ++t) {
-        float s = 0.0f;
-        for (int d = 0; d < D; ++d) s += q[d] * krows[(int64_t)t * D + d];
-        s *= sm_scale;
+        double s = 0.0;
+        for (int d = 0; d < D; ++d) s += (double)q[d] * (double)krows[(int64_t)t * D + d];
+        s *= (double)sm_scale;
         scores[t] = s;
         if (s > m) m = s;
     }
-    float l = 0.0f;
+    double l = 0.0;
     for (int t = 0; t < n; ++t) {
-        scores[t] = expf(scores[t] - m);
+        scores[t] = exp(scores[t] - m);
         l += scores[t];
     }
-    for (int d = 0; d < D; ++d) out[d] = 0.0f;
+    for (int d = 0; d < D; ++d) acc[d] = 0.0;
     for (int t = 0; t < n; ++t) {
-        float p = scores[t] / l;
-        for (int d = 0; d < D; ++d) out[d] += p * vrows[(int64_t)t * D + d];
+        const double p = scores[t];
+        for (int d = 0; d < D; ++d) acc[d] += p * (double)vrows[(int64_t)t * D + d];
     }
+    for (int d = 0; d < D; ++d) out[d] = (float)(acc[d] / l);
 }
 
 /* q (B,HQ,D), k/v (B,HKV,S,D) fp32, seq_lens NULL or B lengths <= S. */
@@ -177,17 +186,18 @@ int tkvo_decode_attention(const float *q, const float *k, const float *v, int B,
                           int S, int D, float sm_scale, const int64_t *seq_lens, float *out) {
     if (HQ % HKV) return -1;
     int G = HQ / HKV;
-    float *scores = (float *)malloc(sizeof(float) * (size_t)(S > 0 ? S : 1));
-    if (!scores) return -1;
+    double *scores = (double *)malloc(sizeof(double) * (size_t)(S > 0 ? S : 1));
+    double *acc = (double *)malloc(sizeof(double) * (size_t)D);
+    if (!scores || !acc) { free(scores); free(acc); return -1; }
     for (int b = 0; b < B; ++b) {
         int n = seq_lens ? (int)seq_lens[b] : S;
         for (int h = 0; h < HQ; ++h) {
             int64_t kv = (int64_t)b * HKV + h / G;
             attend_head(q + ((int64_t)b * HQ + h) * D, k + kv * S * D, v + kv * S * D, n, D,
-                        sm_scale, scores, out + ((int64_t)b * HQ + h) * D);
+                        sm_scale, scores, acc, out + ((int64_t)b * HQ + h) * D);
         }
     }
-    free(scores);
+    free(scores); free(acc);
     return 0;
 }
 
@@ -201,8 +211,9 @@ int tkvo_quantized_decode_attention(const float *q, const uint8_t *kp, const uin
     int G = HQ / HKV, NG = D / gs, DP = D / (8 / nbits);
     float *kf = (float *)malloc(sizeof(float) * (size_t)S * D);
     float *vf = (float *)malloc(sizeof(float) * (size_t)S * D);
-    float *scores = (float *)malloc(sizeof(float) * (size_t)(S > 0 ? S : 1));
-    if (!kf || !vf || !scores) { free(kf); free(vf); free(scores); return -1; }
+    double *scores = (double *)malloc(sizeof(double) * (size_t)(S > 0 ? S : 1));
+    double *acc = (double *)malloc(sizeof(double) * (size_t)D);
+    if (!kf || !vf || !scores || !acc) { free(kf); free(vf); free(scores); free(acc); return -1; }
     for (int b = 0; b < B; ++b)
         for (int hk = 0; hk < HKV; ++hk) {
             int64_t row0 = ((int64_t)b * HKV + hk) * S;
@@ -210,10 +221,10 @@ int tkvo_quantized_decode_attention(const float *q, const uint8_t *kp, const uin
             tkvo_dequantize(vp + row0 * DP, vs + row0 * NG, vz + row0 * NG, S, D, nbits, gs, vf);
             for (int j = 0; j < G; ++j) {
                 int h = hk * G + j;
-                attend_head(q + ((int64_t)b * HQ + h) * D, kf, vf, S, D, sm_scale, scores,
+                attend_head(q + ((int64_t)b * HQ + h) * D, kf, vf, S, D, sm_scale, scores, acc,
                             out + ((int64_t)b * HQ + h) * D);
             }
         }
-    free(kf); free(vf); free(scores);
+    free(kf); free(vf); free(scores); free(acc);
     return 0;
 }

@@ -8,9 +8,12 @@
   append fused into the split kernel.
 
 The inputs are ``tritonkv_amd.synthetic``'s, at the benchmark's seeds, so these
-tests check the very workloads ``bench.py`` times.  Whole-batch oracle
-evaluation at these sizes would take minutes, so the checks are:
+tests check the very workloads ``bench.py`` times.  The checks are:
 
+* Llama: every (batch row, kv head) unit of the batch, for both split plans,
+  against the C oracle (``oracle/tkv_oracle.c``: dequantise to fp32, attend
+  with binary64 sums) on the GPU cache's own codes, within 2e-3 max-abs /
+  1e-3 mean-abs;
 * size-independent properties over the whole batch: the split count does not
   change the answer (Llama); the fused append is bitwise equal to
   append-then-decode, in the output and in every cache byte (70B-style);
@@ -45,6 +48,40 @@ X70B_CAPACITY = 131072 + 64
 
 def _say(msg):
     print(msg, flush=True)
+
+
+def _whole_batch_vs_c_oracle(q, kq, vq, outs, what):
+    """Every (b, kv head) unit of each output in ``outs`` against the C oracle on
+    the cache's codes (one unit per task; ctypes releases the GIL)."""
+    import concurrent.futures as cf
+    import os
+
+    from oracle import c_oracle
+
+    B, HQ, D = q.shape
+    HKV = kq.packed.shape[1]
+    G = HQ // HKV
+    host = [t.cpu().numpy() for t in (kq.packed, kq.scale, kq.zero, vq.packed, vq.scale, vq.zero)]
+    qf = q.float().cpu().numpy()
+    units = [(b, h) for b in range(B) for h in range(HKV)]
+
+    def run(u):
+        b, h = u
+        sub = [a[b:b + 1, h:h + 1] for a in host]
+        return c_oracle.quantized_decode_attention(
+            qf[b:b + 1, h * G:(h + 1) * G], (sub[0], sub[1], sub[2], kq.nbits, kq.group_size),
+            (sub[3], sub[4], sub[5], vq.nbits, vq.group_size), D ** -0.5)[0]
+
+    with cf.ThreadPoolExecutor(max_workers=min(16, len(os.sched_getaffinity(0)))) as ex:
+        refs = list(ex.map(run, units))
+    for plan, out in outs:
+        o = out.cpu().numpy().astype(np.float64)
+        err = np.stack([np.abs(o[b, h * G:(h + 1) * G] - r) for (b, h), r in zip(units, refs)])
+        worst = units[int(err.reshape(len(units), -1).max(axis=1).argmax())]
+        _say(f"  whole batch {plan}: max-abs {err.max():.3e} mean-abs {err.mean():.3e} "
+             f"(worst unit b={worst[0]} h={worst[1]})")
+        assert err.max() <= MAX_ABS_TOL, f"{what} {plan}: max-abs {err.max()} at unit {worst}"
+        assert err.mean() <= 1e-3, f"{what} {plan}: mean-abs {err.mean()}"
 
 
 def _assert_unit_codes(kq_gpu, x_unit, b, h, L, what):
@@ -102,6 +139,8 @@ def test_llama3_8b_outlier_channels_full_shape(llama_kv, nbits, gs):
     # size-independent: both split plans approximate one answer within the
     # tolerance each is held to below, over the whole batch
     assert (got - split).abs().max().item() <= 2 * MAX_ABS_TOL
+    _whole_batch_vs_c_oracle(q, kq, vq, (("default", got), ("8 splits", split)),
+                             f"llama nbits={nbits} gs={gs}")
     got_np, split_np = got.cpu().numpy(), split.cpu().numpy()
     for b, h in LLAMA_UNITS:
         _say(f"  unit b={b} h={h}")

@@ -221,6 +221,32 @@ def test_attention_matches_float64_brute_force(shape):
     assert np.max(np.abs(c - want)) < 2e-6
 
 
+def test_c_oracle_long_history_matches_float64():
+    """The C oracle at a benchmark-sized history: 32768 tokens with x8 outlier
+    channels and one dominant token, where the output sits near |v| ~ 20 and a
+    scalar fp32 running sum of the weighted rows drifts by ~1e-3 (the checker
+    accumulates in binary64 for exactly this reason)."""
+    rng = np.random.default_rng(11)
+    B, HQ, HKV, S, D = 1, 4, 1, 32768, 128
+    mult = np.ones(D, np.float32)
+    mult[[3, 40, 77, 101]] = 8.0
+    q = rng.standard_normal((B, HQ, D)).astype(np.float32)
+    k = (rng.standard_normal((B, HKV, S, D)) * mult).astype(np.float32)
+    v = (rng.standard_normal((B, HKV, S, D)) * mult).astype(np.float32)
+    # one token that takes ~90% of head 0's weight, with a large V row
+    s_others = np.log(np.exp(q[0, 0].astype(np.float64) @ k[0, 0].T.astype(np.float64)
+                             / math.sqrt(D)).sum())
+    k[0, 0, 1234] = q[0, 0] * np.float32((s_others + 2.2) * math.sqrt(D) / float(q[0, 0] @ q[0, 0]))
+    v[0, 0, 1234] = 20.0
+    got = c_oracle.decode_attention(q, k, v, 1 / math.sqrt(D))
+    qd, kd, vd = q.astype(np.float64), k.astype(np.float64), v.astype(np.float64)
+    s = np.einsum("hd,td->ht", qd[0], kd[0, 0]) / math.sqrt(D)
+    w = np.exp(s - s.max(axis=1, keepdims=True))
+    want = (w @ vd[0, 0]) / w.sum(axis=1, keepdims=True)
+    assert np.abs(want).max() > 5.0
+    assert np.max(np.abs(got[0] - want)) < 2e-6
+
+
 def test_attention_closed_forms():
     rng = np.random.default_rng(7)
     q = rng.standard_normal((1, 6, 16)).astype(np.float32)

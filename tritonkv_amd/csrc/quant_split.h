@@ -364,6 +364,18 @@ struct LdsKernelSmem {
 // step and 9-18% at the DRAM-bound Llama-3-8B shape.
 constexpr int kHiLoMaxLen = 256;
 
+// Longer rows keep fp16 P, but the products P * s_g can be carried with their
+// exact remainders (one pk_fma per pair and one more MFMA per V product).
+// The rounding of an fp16 P * s reaches the output as up to 2^-12 * |c * s|
+// per token, and |c * s| spans the V group's whole range: with 2-bit codes
+// and 128-dim groups (one group per row, so every group holds a key's
+// outlier channels) that range is largest.  Measured on the Llama-3-8B shape
+// with x8 outlier channels, whole batch against the binary64-sum oracle:
+// 2.07e-3 max-abs with fp16 P * s, 1.42e-3 with the remainders (for 7% more
+// time: 118.6 -> 126.9 us); 2-bit gs32 is 0.98e-3 without them.
+template <int VNB, int NG>
+constexpr bool kPsRemainder = VNB == 2 && NG == 1;
+
 
 template <int D, int KNB, int VNB, int GS, int NW, int NSTAGE, bool PAGED, bool PT, bool KCH, int HS>
 __global__ void __launch_bounds__(NW * 64)
@@ -626,11 +638,16 @@ quant_split_lds_kernel(SplitParams prm) {
 
   // Chunk k of the wave uses stage k % NSTAGE; the loop below is unrolled by
   // NSTAGE so every stage offset is a compile-time constant.
-  auto step = [&](int cb, auto tail, auto stage, auto hilo) __attribute__((always_inline)) {
+  auto step = [&](int cb, auto tail, auto stage, auto pmode) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail)::value;
     constexpr int SK = decltype(stage)::value;
     // hi/lo probabilities in the PV products (see kHiLoMaxLen)
-    constexpr bool HILO = decltype(hilo)::value;
+    // Precision of the PV products (see kHiLoMaxLen and kPsRemainder): 0 fp16
+    // P and P * s; 1 adds the exact remainder of each fp16 product P * s;
+    // 2 (HILO) also carries P itself as hi/lo fp16 pairs.
+    constexpr int PMODE = decltype(pmode)::value;
+    constexpr bool HILO = PMODE == 2;
+    constexpr bool PSREM = PMODE >= 1;
     // refill the stage consumed by the previous chunk, NSTAGE-1 chunks ahead
     {
       const int cn = cb + (NSTAGE - 1) * cstride;
@@ -910,7 +927,7 @@ quant_split_lds_kernel(SplitParams prm) {
     }
     // ---- P' = P * s_g, g = v * S + slot ----------------------------------------
     u4 pg[NPG];
-    u4 pgl[HILO ? NPG : 1];
+    u4 pgl[PSREM ? NPG : 1];
 #pragma unroll
     for (int v = 0; v < NPG; ++v) {
       uint32_t sp[4];
@@ -929,6 +946,9 @@ quant_split_lds_kernel(SplitParams prm) {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
           pgl[v][q] = pk_add(pk_fma_rem(pb[q], sp[q], pg[v][q]), pk_mul(pbl[q], sp[q]));
+      } else if constexpr (PSREM) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) pgl[v][q] = pk_fma_rem(pb[q], sp[q], pg[v][q]);
       }
     }
 
@@ -967,7 +987,7 @@ quant_split_lds_kernel(SplitParams prm) {
           const u4 av = (kVChain && p == VL::P - 1) ? u4{pm[0], pm[1], pm[2], pm[3]}
                                                     : u4{pm[0] & msk, pm[1] & msk, pm[2] & msk, pm[3] & msk};
           accv[mv] = mfma_k32(av, pg[VL::group_of(mv) / S], accv[mv]);
-          if constexpr (HILO) accv[mv] = mfma_k32(av, pgl[VL::group_of(mv) / S], accv[mv]);
+          if constexpr (PSREM) accv[mv] = mfma_k32(av, pgl[VL::group_of(mv) / S], accv[mv]);
         }
       }
     }
@@ -978,29 +998,30 @@ quant_split_lds_kernel(SplitParams prm) {
   // chunk holding the last token, which always runs as the TAIL step (even
   // when it is full).  A single loop exit keeps the accumulators in place
   // across the unrolled copies.
-  auto stream = [&](auto hilo) __attribute__((always_inline)) {
+  auto stream = [&](auto pmode) __attribute__((always_inline)) {
     int cb = cb0;
     for (; cb + (NSTAGE - 1) * cstride + kChunk < hi; cb += NSTAGE * cstride) {
       static_for<NSTAGE>([&](auto s) __attribute__((always_inline)) {
-        step(cb + decltype(s)::value * cstride, std::false_type{}, s, hilo);
+        step(cb + decltype(s)::value * cstride, std::false_type{}, s, pmode);
       });
     }
     bool more = true;
     static_for<NSTAGE>([&](auto s) __attribute__((always_inline)) {
       if (more) {
         if (cb + kChunk < hi) {
-          step(cb, std::false_type{}, s, hilo);
+          step(cb, std::false_type{}, s, pmode);
           cb += cstride;
         } else {
-          if (cb < hi) step(cb, std::true_type{}, s, hilo);
+          if (cb < hi) step(cb, std::true_type{}, s, pmode);
           more = false;
         }
       }
     });
   };
-  // Short rows take hi/lo probabilities in every chunk (see kHiLoMaxLen).
-  if (L <= kHiLoMaxLen) stream(std::true_type{});
-  else stream(std::false_type{});
+  // Short rows take hi/lo probabilities in every chunk (see kHiLoMaxLen);
+  // longer ones the remainders of P * s where kPsRemainder asks for them.
+  if (L <= kHiLoMaxLen) stream(std::integral_constant<int, 2>{});
+  else stream(std::integral_constant<int, kPsRemainder<VNB, NG> ? 1 : 0>{});
   wait_vmcnt<0>();  // retire the trailing (out-of-range) prefetches
   wave_lds_fence();
 
