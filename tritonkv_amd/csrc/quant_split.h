@@ -350,6 +350,9 @@ struct LdsKernelSmem {
   // the fp16 scale/zero of K and V, NG each), behind the waves' rings.
   static constexpr int PATCH_META = SG::KL::DP + SG::VL::DP;
   static constexpr int PATCH = (PATCH_META + 4 * SG::NG * 2 + 15) / 16 * 16;
+  // Unpaired tiles: the q operands one wave builds for the workgroup (qf, qn,
+  // qzb, eh: 8 * NKM + 3 dwords per lane), behind the patch.
+  static constexpr int QOP = (8 * SG::KL::NKM + 3) * 4 * 64;
 };
 
 // Probabilities enter the PV products as fp16 (B operands of the MFMAs), as
@@ -404,7 +407,7 @@ quant_split_lds_kernel(SplitParams prm) {
   constexpr int S = 16 / HS;             // V-group slots per head
   constexpr int NPG = (NG + S - 1) / S;  // P' operands per chunk
 
-  __shared__ __attribute__((aligned(16))) uint8_t smem[NW * SM::WAVE + SM::PATCH];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[NW * SM::WAVE + SM::PATCH + (PT ? 0 : SM::QOP)];
 
   const int unit = blockIdx.x;   // fastest: consecutive workgroups (which the
   const int split = blockIdx.y;  // dispatcher deals to the 8 XCDs in turn) take other units
@@ -507,8 +510,41 @@ quant_split_lds_kernel(SplitParams prm) {
   // Per-channel keys multiply q by the chunk's channel scales in fp16 (q * s
   // as hi/lo pairs), so their q keeps eh = 0: a larger prescale could
   // overflow there.
-  if constexpr (PT) load_q_operands_pt<D, KNB, GS, HS < 8 ? HS : 8>(prm, b, h0, r, nh, j, qpt);
-  else load_q_operands<D, KNB, GS, KCH ? 0 : (KL::P - 1) * KNB>(prm, b, h0, n % HS, nh, j, qo);
+  if constexpr (PT) {
+    load_q_operands_pt<D, KNB, GS, HS < 8 ? HS : 8>(prm, b, h0, r, nh, j, qpt);
+  } else {
+    // Every wave of the workgroup serves the same query heads, so wave 0
+    // alone builds the q operands and the others read them from LDS: on a
+    // short row the build (q loads, then ~300 VALU) would otherwise be
+    // repeated by the second wave of every SIMD ahead of its first chunk.
+    uint32_t* const qop = reinterpret_cast<uint32_t*>(smem + NW * SM::WAVE + SM::PATCH) + lane;
+    constexpr int QN = 4 * NKM;  // dword slots of qn (used by per-channel keys)
+    if (w == 0) {
+      load_q_operands<D, KNB, GS, KCH ? 0 : (KL::P - 1) * KNB>(prm, b, h0, n % HS, nh, j, qo);
+#pragma unroll
+      for (int m = 0; m < NKM; ++m)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          qop[64 * (4 * m + e)] = qo.qf[m][e];
+          if constexpr (KCH) qop[64 * (QN + 4 * m + e)] = qo.qn[m][e];
+        }
+      qop[64 * (2 * QN)] = qo.qzb[0];
+      qop[64 * (2 * QN + 1)] = qo.qzb[1];
+      qop[64 * (2 * QN + 2)] = (uint32_t)qo.eh;
+    }
+    __syncthreads();
+    if (w != 0) {
+#pragma unroll
+      for (int m = 0; m < NKM; ++m)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          qo.qf[m][e] = qop[64 * (4 * m + e)];
+          if constexpr (KCH) qo.qn[m][e] = qop[64 * (QN + 4 * m + e)];
+        }
+      qo.qzb = u2{qop[64 * (2 * QN)], qop[64 * (2 * QN + 1)]};
+      qo.eh = (int)qop[64 * (2 * QN + 2)];
+    }
+  }
   const int eh = PT ? qpt.eh : qo.eh;
   const float zsc = __builtin_ldexpf(1.0f, eh - 24);  // code-dot units per score unit
   const u4* qf = qo.qf;
