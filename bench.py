@@ -86,6 +86,11 @@ def _args():
     ap.add_argument("--regime-probe", choices=("hot", "cold"), default=None,
                     help="no timing: 60 eager Qwen2.5-1.5B ctx-16384 4-bit decode calls on one "
                          "cache (hot) or rotating copies >= 768 MB (cold), for rocprofv3 --pmc")
+    ap.add_argument("--qwen-trace", type=int, metavar="CTX", default=None,
+                    help="no timing: 200 eager hot decode calls each of the fused 4-bit, fused "
+                         "2-bit and fp16 control paths at the Qwen2.5-1.5B shape and context "
+                         "CTX (default splits, combine launch included), for a rocprofv3 "
+                         "kernel trace")
     return ap.parse_args()
 
 
@@ -206,7 +211,8 @@ def fused_call(q, kq, vq, num_splits=None, split_only=False, waves=None, fused_c
     _, ns, size = plan_splits(S, 64, num_splits, B, HKV, HQ // HKV)
     out = torch.empty(B, HQ, D, device=q.device)
     acc, mx, sm, cnt = _workspace_for({}, B, HQ, ns, D, q.device, HKV)
-    wv = choose_waves(B, HKV, HQ // HKV, size, ns) if waves is None else waves
+    wv = choose_waves(B, HKV, HQ // HKV, size, ns, D=D, k_nbits=kq.nbits, v_nbits=vq.nbits,
+                      group_size=kq.group_size) if waves is None else waves
     args = _lib.DecodeArgs(
         q=q.data_ptr(), k=kq.packed.data_ptr(), k_scale=kq.scale.data_ptr(),
         k_zero=kq.zero.data_ptr(), v=vq.packed.data_ptr(), v_scale=vq.scale.data_ptr(),
@@ -262,7 +268,7 @@ def paged_call(q, kp, vp, table, split_only=False):
         v_zero=vp.zero.data_ptr(), acc=_lib.ptr(acc), maxs=_lib.ptr(mx), sums=_lib.ptr(sm),
         out=out.data_ptr(), B=B, HQ=HQ, HKV=HKV, S=S, D=D, k_nbits=kp.nbits, v_nbits=vp.nbits,
         group_size=kp.group_size, sm_scale=D ** -0.5, split_size=size, num_splits=ns,
-        waves=choose_waves(B, HKV, HQ // HKV, size, ns), block_table=table.data_ptr(),
+        waves=choose_waves(B, HKV, HQ // HKV, size, ns, paged=True), block_table=table.data_ptr(),
         block_table_stride=table.shape[1], page_size=page, num_pages=num_pages)
     lib = _lib.load()
     fn = lib.tkv_fused_decode_split if split_only else lib.tkv_fused_decode_attention
@@ -968,7 +974,8 @@ def kernel_probe(name, launches=6):
             v_zero=vq.zero.data_ptr(), acc=acc.data_ptr(), maxs=ml[0].data_ptr(),
             sums=ml[1].data_ptr(), out=out.data_ptr(), B=B, HQ=HQ, HKV=HKV, S=S, D=D,
             k_nbits=kb, v_nbits=vb, group_size=gs, sm_scale=D ** -0.5, split_size=size,
-            num_splits=ns, waves=choose_waves(B, HKV, HQ // HKV, size, ns), key_block=BLOCK,
+            num_splits=ns, waves=choose_waves(B, HKV, HQ // HKV, size, ns, D=D, k_nbits=kb,
+                                              v_nbits=vb, group_size=gs), key_block=BLOCK,
             split_base=0, num_splits_total=ns + 1)
         lib = _lib.load()
 
@@ -1051,6 +1058,30 @@ def regime_probe(mode):
     return 0
 
 
+def qwen_trace(S, calls_each=200):
+    """Eager hot decode calls at the Qwen2.5-1.5B shape (B=1, HQ=12, HKV=2,
+    D=128, gs32): fp16 control, fused 4-bit, fused 2-bit, in that order."""
+    import torch
+
+    from tritonkv_amd.quantize import quantize_groupwise
+
+    B, HQ, HKV, D, gs = 1, 12, 2, 128, 32
+    g = torch.Generator(device="cuda").manual_seed(7)
+    q = torch.randn(B, HQ, D, device="cuda", generator=g, dtype=torch.float16)
+    k = torch.randn(B, HKV, S, D, device="cuda", generator=g, dtype=torch.float16)
+    v = torch.randn(B, HKV, S, D, device="cuda", generator=g, dtype=torch.float16)
+    calls = [fp16_call(q, k, v)] + [
+        fused_call(q, quantize_groupwise(k, nb, gs), quantize_groupwise(v, nb, gs))
+        for nb in (4, 2)]
+    for c in calls:
+        for _ in range(calls_each):
+            c()
+        torch.cuda.synchronize()
+    print(json.dumps({"qwen_trace": S, "calls_each": calls_each,
+                      "splits": [c.num_splits for c in calls]}))
+    return 0
+
+
 def main() -> int:
     a = _args()
     if a.rocprof_summary:
@@ -1061,6 +1092,8 @@ def main() -> int:
         return kernel_probe(a.kernel_probe)
     if a.regime_probe:
         return regime_probe(a.regime_probe)
+    if a.qwen_trace:
+        return qwen_trace(a.qwen_trace)
     if a.compare:
         return compare(a.compare)
     global MIN_WARMUP_S

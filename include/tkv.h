@@ -61,7 +61,10 @@ enum {
  *                      The caller zero-fills the B*HKV*ceil(G/16) int32 counters
  *                      once; every call leaves them zero again.  Calls that
  *                      share a counters buffer must not overlap in time.
- * waves: workgroup size in 64-lane waves, 4 or 8 (0 = 4). */
+ * waves: workgroup size in 64-lane waves, 4, 8 or 12 (0 = 4).  12 runs
+ *        12 waves where the library has such a kernel (quantized, head_dim
+ *        128, contiguous caches, 2-bit gs32 with at most 4 query heads per
+ *        KV head, or gs128 with equal K/V bits) and 8 otherwise. */
 typedef struct tkv_decode_args {
   const void *q;
   int32_t q_is_fp32;

@@ -236,6 +236,68 @@ def test_ragged_sequence_lengths():
         assert_close_to_reference(got, ref, f"ragged ns={ns}")
 
 
+def _launch(q, kq, vq, out, num_splits, waves, seq_lens):
+    """One fused call through the C ABI with an explicit wave count (one split:
+    no partials)."""
+    from tritonkv_amd import _lib
+
+    assert num_splits == 1
+    B, HQ, D = q.shape
+    _, HKV, S, _ = kq.packed.shape
+    a = _lib.DecodeArgs(q=q.data_ptr(), k=kq.packed.data_ptr(), k_scale=kq.scale.data_ptr(),
+                        k_zero=kq.zero.data_ptr(), v=vq.packed.data_ptr(),
+                        v_scale=vq.scale.data_ptr(), v_zero=vq.zero.data_ptr(),
+                        seq_lens=seq_lens.data_ptr(), out=out.data_ptr(), B=B, HQ=HQ, HKV=HKV,
+                        S=S, D=D, k_nbits=kq.nbits, v_nbits=vq.nbits, group_size=kq.group_size,
+                        sm_scale=D ** -0.5, split_size=S, num_splits=1, waves=waves)
+    _lib.check(_lib.load().tkv_fused_decode_attention(a, _lib.stream_handle(q.device)), "fused")
+    torch.cuda.synchronize()
+
+
+TWELVE_WAVE_CASES = [
+    # (K bits, V bits, group size, HQ, HKV): formats with a 12-wave kernel, and
+    # one without (4-bit gs32), whose 12-wave request runs 8 waves
+    (2, 2, 32, 8, 2),
+    (2, 2, 128, 12, 2),
+    (4, 4, 128, 12, 2),
+    (4, 4, 32, 8, 2),
+]
+
+
+@pytest.mark.parametrize("case", TWELVE_WAVE_CASES, ids=lambda c: "K{}V{}-gs{}-G{}".format(
+    c[0], c[1], c[2], c[3] // c[4]))
+def test_twelve_wave_workgroups(case):
+    """12-wave workgroups (one split of 9000 tokens, rows of 9000, 100 and 5000
+    tokens: a short row leaves most waves without a chunk) against the oracle
+    and against 8 waves; the default wave count of a long split is 12 exactly
+    for the listed formats."""
+    from tritonkv_amd.kernels.fused_decode_attn import choose_waves, twelve_wave_format
+    from tritonkv_amd.quantize import quantize_groupwise
+
+    kb, vb, gs, HQ, HKV = case
+    B, S, D = 3, 9000, 128
+    print(f"twelve waves {case}", flush=True)
+    q, k, v = oinp.make_random_kv(B, HQ, HKV, S, D, seed=29 + kb + gs)
+    q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
+    kq, vq = quantize_groupwise(k, kb, gs), quantize_groupwise(v, vb, gs)
+    lens = torch.tensor([9000, 100, 5000], dtype=torch.int32)
+    listed = twelve_wave_format(D, HQ // HKV, kb, vb, gs)
+    assert listed == (case != (4, 4, 32, 8, 2))
+    assert choose_waves(B, HKV, HQ // HKV, S, 1, D=D, k_nbits=kb, v_nbits=vb,
+                        group_size=gs) == (12 if listed else 8)
+    ref = oracle_attention_on_quant(q, kq, vq, seq_lens=lens.numpy())
+    outs = {}
+    for waves in (12, 8):
+        got = torch.empty(B, HQ, D, device=DEV)
+        _launch(q, kq, vq, got, num_splits=1, waves=waves, seq_lens=lens.to(DEV))
+        assert_close_to_reference(got, ref, f"{case} waves={waves}")
+        outs[waves] = got
+    if not listed:  # the request ran the 8-wave kernel
+        assert torch.equal(outs[12], outs[8])
+    got = _fused(q, kq, vq, seq_lens=lens.to(DEV), num_splits=1)  # the Python API's default
+    assert_close_to_reference(got, ref, f"{case} default waves")
+
+
 def test_append_then_decode_ragged_batch():
     """The 70B-style decode step at reduced size: per-row lengths, K 4-bit /
     V 2-bit, one new token appended by the GPU quantizer at position S_b, then

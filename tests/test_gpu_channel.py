@@ -136,6 +136,23 @@ def test_channel_decode_matches_oracle(case, ns, lens):
     assert_close_to_reference(got, ref, f"channel decode {case} ns={ns}")
 
 
+def test_channel_decode_twelve_waves():
+    """Per-channel 2-bit keys, 2-bit V gs32, GQA group of 4, one split of 8704
+    tokens: the path's default is a 12-wave workgroup."""
+    from tritonkv_amd.channel import channel_decode_attention
+    from tritonkv_amd.kernels.fused_decode_attn import choose_waves
+
+    B, HQ, HKV, D, S = 2, 8, 2, 128, 8704
+    assert choose_waves(B, HKV, 4, S, 1, D=D, k_nbits=2, v_nbits=2, group_size=32) == 12
+    q, ck, vq, kres, vres, ql, rl = _window_case(B, HQ, HKV, D, S, 2, 2, 32, [8704, 8200],
+                                                 [5, 32], seed=77)
+    got = channel_decode_attention(q.to(DEV), ck, vq, kres.to(DEV), vres.to(DEV),
+                                   q_lens=ql.to(DEV), res_lens=rl.to(DEV), num_splits=1)
+    torch.cuda.synchronize()
+    ref = _oracle(q, ck, vq, kres, vres, ql, rl)
+    assert_close_to_reference(got, ref, "channel decode, 12 waves")
+
+
 @pytest.mark.parametrize("R", [16, 48])
 @pytest.mark.parametrize("q_dtype", [torch.float16, torch.float32])
 def test_channel_decode_window_sizes(R, q_dtype):

@@ -85,6 +85,29 @@ def test_paged_append_requires_a_gpu_tensor():
                      torch.zeros(1, dtype=torch.int32))
 
 
+def test_wave_count_policy():
+    from tritonkv_amd.kernels.fused_decode_attn import (TWELVE_WAVES_MIN_SPLIT, choose_waves,
+                                                        twelve_wave_format)
+
+    fmt = dict(D=128, k_nbits=2, v_nbits=2, group_size=32)
+    # Llama-3-8B shape, 2-bit gs32 (G = 4): one 32768-token split per unit -> 12 waves
+    assert choose_waves(32, 8, 4, 32768, 1, **fmt) == 12
+    # the same format below the split threshold, or in a wider GQA group, or paged -> 8
+    assert choose_waves(32, 8, 4, TWELVE_WAVES_MIN_SPLIT - 64, 1, **fmt) == 8
+    assert choose_waves(1, 2, 6, 32768, 1, **fmt) == 8
+    assert choose_waves(32, 8, 4, 32768, 1, paged=True, **fmt) == 8
+    # gs128 with equal bits, any group -> 12; the 4-bit gs32 headline, mixed
+    # bits, head_dim 64 and the fp16 control (the default format) -> 8
+    assert choose_waves(32, 8, 4, 32768, 1, D=128, k_nbits=4, v_nbits=4, group_size=128) == 12
+    assert choose_waves(32, 8, 4, 32768, 1, D=128, k_nbits=4, v_nbits=4, group_size=32) == 8
+    assert choose_waves(64, 8, 8, 65536, 2, D=128, k_nbits=4, v_nbits=2, group_size=32) == 8
+    assert choose_waves(32, 8, 4, 32768, 1, D=64, k_nbits=2, v_nbits=2, group_size=32) == 8
+    assert choose_waves(32, 8, 4, 32768, 1) == 8
+    assert not twelve_wave_format(128, 4, 4, 2, 128)
+    # short splits keep the 4 / 8 rule
+    assert choose_waves(1, 2, 6, 128, 16, **fmt) == 4
+
+
 def test_split_policy_fills_the_device_at_mid_batches():
     from tritonkv_amd.kernels.fused_decode_attn import (TOKENS_PER_WORKGROUP_FP16, choose_waves,
                                                         plan_splits)

@@ -191,7 +191,8 @@ def channel_decode_attention(
         out=out.data_ptr(), B=B, HQ=HQ, HKV=HKV, S=S, D=D, k_nbits=ck.nbits,
         v_nbits=vq.nbits, group_size=vq.group_size, sm_scale=float(sm_scale),
         split_size=split_size, num_splits=num_splits, counters=None,
-        waves=choose_waves(B, HKV, group, split_size, num_splits), key_block=BLOCK)
+        waves=choose_waves(B, HKV, group, split_size, num_splits, D=D, k_nbits=ck.nbits,
+                           v_nbits=vq.nbits, group_size=vq.group_size), key_block=BLOCK)
     with torch.cuda.device(q.device):
         rc = _lib.load().tkv_channel_decode_attention(
             args, kr.data_ptr(), vr.data_ptr(), _lib.ptr(rlens), R, _lib.stream_handle(q.device))

@@ -385,7 +385,7 @@ static int validate_common(const tkv_decode_args* a) {
     return TKV_EINVAL;
   if ((uintptr_t)a->q & 15) return TKV_EINVAL;  // vector loads of q rows
   if (((uintptr_t)a->acc | (uintptr_t)a->out) & 15) return TKV_EINVAL;  // float4 rows
-  if (a->waves != 0 && a->waves != 4 && a->waves != 8) return TKV_EINVAL;
+  if (a->waves != 0 && a->waves != 4 && a->waves != 8 && a->waves != 12) return TKV_EINVAL;
   if ((uintptr_t)a->counters & 3) return TKV_EINVAL;
   if (a->page_size < 0) return TKV_EINVAL;
   if (a->page_size > 0) {
@@ -545,12 +545,12 @@ static int launch_fp16_split(const tkv_decode_args* a, hipStream_t st) {
   const dim3 grid = split_grid(a);
   (void)hipGetLastError();
   if (a->D == 128) {
-    if (a->waves == 8)
+    if (a->waves >= 8)  // 12 runs 8
       fp16_split_kernel<128, 8><<<grid, dim3(8 * 64), 0, st>>>(p);
     else
       fp16_split_kernel<128, 4><<<grid, dim3(4 * 64), 0, st>>>(p);
   } else {
-    if (a->waves == 8)
+    if (a->waves >= 8)
       fp16_split_kernel<64, 8><<<grid, dim3(8 * 64), 0, st>>>(p);
     else
       fp16_split_kernel<64, 4><<<grid, dim3(4 * 64), 0, st>>>(p);

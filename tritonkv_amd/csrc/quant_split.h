@@ -355,6 +355,22 @@ struct LdsKernelSmem {
   static constexpr int QOP = (8 * SG::KL::NKM + 3) * 4 * 64;
 };
 
+// 12-wave workgroups: three waves per SIMD (VGPRs <= 168) in one workgroup
+// per CU, for the formats whose kernel is bound by issue rather than by its
+// loads (more waves to interleave), measured at the Llama-3-8B shape (one
+// workgroup per CU, 32768 tokens each): 2-bit gs32 -7%, per-channel 2-bit
+// keys -5%, 2-bit gs128 -4%, 4-bit gs128 -3%, while 4-bit gs32 (at the read
+// pattern's ceiling) was 1% slower.  Only formats whose 12-wave kernels
+// compile without spills are listed (several others spill at 168 VGPRs); the
+// workgroup's rings, patch and shared q operands must also fit the 160 KB of
+// LDS.  A 12-wave request for any other kernel runs 8 waves.
+template <int D, int KNB, int VNB, int GS, int HS, bool PT>
+constexpr bool kTwelveWaves =
+    D == 128 &&
+    ((KNB == 2 && VNB == 2 && GS == 32 && HS == 4) || (KNB == VNB && GS == 128)) &&
+    12 * LdsKernelSmem<D, KNB, VNB, GS, 12, 2>::WAVE + LdsKernelSmem<D, KNB, VNB, GS, 12, 2>::PATCH +
+            (PT ? 0 : LdsKernelSmem<D, KNB, VNB, GS, 12, 2>::QOP) <= 160 * 1024;
+
 // Probabilities enter the PV products as fp16 (B operands of the MFMAs), as
 // they do in the reference's tl.dot.  Their rounding reaches the output as
 // about 2^-11 * |v| / sqrt(L) for a row of L tokens, whichever chunk it falls
@@ -502,9 +518,82 @@ quant_split_lds_kernel(SplitParams prm) {
   }
 
 
+  using QP = QOperandsPT<D, KNB, GS>;
+  // Per-lane set-up, ahead of the q operands: the waves that wait for wave 0
+  // to build them do it meanwhile.
+  uint32_t vsel[VL::NE];
+#pragma unroll
+  for (int e = 0; e < VL::NE; ++e) vsel[e] = VL::perm_sel(VL::byte_in_dword(e, r));
+  uint32_t kmask[NKM];
+#pragma unroll
+  for (int m = 0; m < NKM; ++m) kmask[m] = slice_mask<KNB>(KL::slice_of(m, j));
+
+  constexpr bool kVChain = NPG == 1;  // every V MFMA takes the same P' operand
+
+  // Per-lane LDS byte offsets inside a stage.
+  // K operand of tile a, load Lh: row 16a + r, byte load_offset(Lh, j).
+  uint32_t koff[KL::NLOAD];
+#pragma unroll
+  for (int Lh = 0; Lh < KL::NLOAD; ++Lh) {
+    const int ob = KL::load_offset(Lh, j);
+    koff[Lh] = SG::K_OFF + SG::template pos_of<KL::DP>(r, ob >> 4) * 16 + (ob & 15);
+  }
+  // Paired tiles: unit u of token 16 * (j >> 1) + r, bytes 8 * (j & 1) .. + 7.
+  uint32_t koffp[QP::NU];
+#pragma unroll
+  for (int u = 0; u < QP::NU; ++u)
+    koffp[u] = SG::K_OFF + SG::template pos_of<KL::DP>(16 * (j >> 1) + r, u) * 16 + 8 * (j & 1);
+  const int tile_pt = 16 * (r >> 3);  // paired tiles: the tile of this lane's scores
+  // V operand of slot i, window wi: token slot_token(j, i), dword dword_offset(wi, r).
+  uint32_t voff[VL::NWIN];
+#pragma unroll
+  for (int wi = 0; wi < VL::NWIN; ++wi) {
+    const int ob = VL::dword_offset(wi, r);
+    voff[wi] = SG::V_OFF + SG::template pos_of<VL::DP>(4 * j, ob >> 4) * 16 + (ob & 15);
+  }
+  // P' operand v of this lane: the V scales of group v * S + slot (clamped:
+  // a slot past the last group computes a copy nobody reads); dword offset of
+  // its fp16 pair in a staged [t][MROW] row and the v_perm selector of its half.
+  uint32_t soff[NPG], ssel[NPG];
+#pragma unroll
+  for (int v = 0; v < NPG; ++v) {
+    const int g = min(v * S + slot, NG - 1);
+    soff[v] = 2 * (g & ~1);
+    ssel[v] = (g & 1) ? 0x07060302u : 0x05040100u;
+  }
+  // A operand of the V zero-point MFMA: row r < NG holds group r's zero
+  // points, gathered for two tokens into one fp16 pair with a single v_perm
+  // (low or high half of each token's dword); row NG is all ones (fp16 1.0
+  // pairs, read from the stage's ones area through the same offsets), so the
+  // same MFMA also accumulates sum_t p_t, the softmax denominator, from the
+  // very fp16 probabilities the PV products use; rows r > NG are zero (their
+  // selector yields constant zero bytes).
+  int zoff = r < NG ? 2 * (r & ~1) : SG::MB;
+  uint32_t zsel = r < NG ? ((r & 1) ? 0x07060302u : 0x05040100u)
+                         : (r == NG ? 0x05040100u : 0x0C0C0C0Cu);
+  if constexpr (!PT) {
+    // Materialise them here: otherwise the compiler sinks this arithmetic
+    // past the barrier below, onto every wave's path to its first chunk.
+    auto pin = [](auto& x) __attribute__((always_inline)) { asm volatile("" : "+v"(x)); };
+#pragma unroll
+    for (int e = 0; e < VL::NE; ++e) pin(vsel[e]);
+#pragma unroll
+    for (int m = 0; m < NKM; ++m) pin(kmask[m]);
+#pragma unroll
+    for (int Lh = 0; Lh < KL::NLOAD; ++Lh) pin(koff[Lh]);
+#pragma unroll
+    for (int wi = 0; wi < VL::NWIN; ++wi) pin(voff[wi]);
+#pragma unroll
+    for (int v = 0; v < NPG; ++v) {
+      pin(soff[v]);
+      pin(ssel[v]);
+    }
+    pin(zoff);
+    pin(zsel);
+  }
+
   // q operands: one per MFMA step of a tile, or (paired tiles, G <= 8) one
   // block-diagonal operand per 16-dim block of both tiles.
-  using QP = QOperandsPT<D, KNB, GS>;
   QOperands<D, KNB, GS> qo;
   QP qpt;
   // Per-channel keys multiply q by the chunk's channel scales in fp16 (q * s
@@ -599,57 +688,6 @@ quant_split_lds_kernel(SplitParams prm) {
       }
     }
   }
-
-  uint32_t vsel[VL::NE];
-#pragma unroll
-  for (int e = 0; e < VL::NE; ++e) vsel[e] = VL::perm_sel(VL::byte_in_dword(e, r));
-  uint32_t kmask[NKM];
-#pragma unroll
-  for (int m = 0; m < NKM; ++m) kmask[m] = slice_mask<KNB>(KL::slice_of(m, j));
-
-  constexpr bool kVChain = NPG == 1;  // every V MFMA takes the same P' operand
-
-  // Per-lane LDS byte offsets inside a stage.
-  // K operand of tile a, load Lh: row 16a + r, byte load_offset(Lh, j).
-  uint32_t koff[KL::NLOAD];
-#pragma unroll
-  for (int Lh = 0; Lh < KL::NLOAD; ++Lh) {
-    const int ob = KL::load_offset(Lh, j);
-    koff[Lh] = SG::K_OFF + SG::template pos_of<KL::DP>(r, ob >> 4) * 16 + (ob & 15);
-  }
-  // Paired tiles: unit u of token 16 * (j >> 1) + r, bytes 8 * (j & 1) .. + 7.
-  uint32_t koffp[QP::NU];
-#pragma unroll
-  for (int u = 0; u < QP::NU; ++u)
-    koffp[u] = SG::K_OFF + SG::template pos_of<KL::DP>(16 * (j >> 1) + r, u) * 16 + 8 * (j & 1);
-  const int tile_pt = 16 * (r >> 3);  // paired tiles: the tile of this lane's scores
-  // V operand of slot i, window wi: token slot_token(j, i), dword dword_offset(wi, r).
-  uint32_t voff[VL::NWIN];
-#pragma unroll
-  for (int wi = 0; wi < VL::NWIN; ++wi) {
-    const int ob = VL::dword_offset(wi, r);
-    voff[wi] = SG::V_OFF + SG::template pos_of<VL::DP>(4 * j, ob >> 4) * 16 + (ob & 15);
-  }
-  // P' operand v of this lane: the V scales of group v * S + slot (clamped:
-  // a slot past the last group computes a copy nobody reads); dword offset of
-  // its fp16 pair in a staged [t][MROW] row and the v_perm selector of its half.
-  uint32_t soff[NPG], ssel[NPG];
-#pragma unroll
-  for (int v = 0; v < NPG; ++v) {
-    const int g = min(v * S + slot, NG - 1);
-    soff[v] = 2 * (g & ~1);
-    ssel[v] = (g & 1) ? 0x07060302u : 0x05040100u;
-  }
-  // A operand of the V zero-point MFMA: row r < NG holds group r's zero
-  // points, gathered for two tokens into one fp16 pair with a single v_perm
-  // (low or high half of each token's dword); row NG is all ones (fp16 1.0
-  // pairs, read from the stage's ones area through the same offsets), so the
-  // same MFMA also accumulates sum_t p_t, the softmax denominator, from the
-  // very fp16 probabilities the PV products use; rows r > NG are zero (their
-  // selector yields constant zero bytes).
-  const int zoff = r < NG ? 2 * (r & ~1) : SG::MB;
-  const uint32_t zsel = r < NG ? ((r & 1) ? 0x07060302u : 0x05040100u)
-                               : (r == NG ? 0x05040100u : 0x0C0C0C0Cu);
 
   f4 accv[NVM];
 #pragma unroll
@@ -1096,13 +1134,21 @@ quant_split_lds_kernel(SplitParams prm) {
 // measured slightly slower at the Llama-3-8B shape (208 vs 206 us): one chunk
 // in flight per wave already saturates what this access pattern streams.
 // Paged caches use two stages.
-constexpr int kStages8 = 2;
+constexpr int kStages8 = 2;  // also the ring depth of 12-wave workgroups
+static_assert(kStages8 == 2, "kFits12Waves sizes two-stage rings");
 constexpr int kStages4 = 2;
 
 template <int D, int KNB, int VNB, int GS, bool PT, int HS>
 void launch_quant_pt(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
   const bool paged = p.page_size > 0;
-  if (waves == 8) {
+  if constexpr (kTwelveWaves<D, KNB, VNB, GS, HS, PT>) {
+    if (waves == 12 && !paged) {
+      quant_split_lds_kernel<D, KNB, VNB, GS, 12, kStages8, false, PT, false, HS>
+          <<<grid, dim3(12 * 64), 0, st>>>(p);
+      return;
+    }
+  }
+  if (waves >= 8) {
     if (paged)
       quant_split_lds_kernel<D, KNB, VNB, GS, 8, 2, true, PT, false, HS><<<grid, dim3(8 * 64), 0, st>>>(p);
     else
@@ -1172,7 +1218,15 @@ __global__ void __launch_bounds__(NW * 64) read_probe_kernel(SplitParams prm) {
 
 template <int D, int KNB, int VNB, int GS>
 void launch_read_probe(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
-  if (waves == 8) read_probe_kernel<D, KNB, VNB, GS, 8><<<grid, dim3(8 * 64), 0, st>>>(p);
+  // The same workgroup size as the kernel it probes (whose 12-wave form at
+  // G <= 4 has head columns of width 4 and, at GS = 128, width 16).
+  if constexpr (kTwelveWaves<D, KNB, VNB, GS, GS == 128 ? 16 : 4, true>) {
+    if (waves == 12 && (GS == 128 || p.G <= 4)) {
+      read_probe_kernel<D, KNB, VNB, GS, 12><<<grid, dim3(12 * 64), 0, st>>>(p);
+      return;
+    }
+  }
+  if (waves >= 8) read_probe_kernel<D, KNB, VNB, GS, 8><<<grid, dim3(8 * 64), 0, st>>>(p);
   else read_probe_kernel<D, KNB, VNB, GS, 4><<<grid, dim3(4 * 64), 0, st>>>(p);
 }
 
@@ -1182,7 +1236,14 @@ template <int D, int KNB, int VNB, int GS, int HS>
 void launch_quant_hs(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
   if constexpr (GS <= 32) {
     if (p.key_block) {  // per-channel keys (the host checked: contiguous, no fused append)
-      if (waves == 8)
+      if constexpr (kTwelveWaves<D, KNB, VNB, GS, HS, false>) {
+        if (waves == 12) {
+          quant_split_lds_kernel<D, KNB, VNB, GS, 12, kStages8, false, false, true, HS>
+              <<<grid, dim3(12 * 64), 0, st>>>(p);
+          return;
+        }
+      }
+      if (waves >= 8)
         quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, false, true, HS>
             <<<grid, dim3(8 * 64), 0, st>>>(p);
       else

@@ -151,10 +151,37 @@ def default_num_splits(B: int, HKV: int, G: int, S: int, block_n: int,
     return max(1, min(want, max_splits, _cdiv(S, block_n)))
 
 
-def choose_waves(B: int, HKV: int, G: int, split_size: int, num_splits: int = 0) -> int:
-    """Waves per workgroup: 8 when a workgroup streams the whole history or at
-    least 512 tokens (two 32-token chunks per wave, so each wave overlaps a
-    load with compute), else 4."""
+# Workgroups that stream at least this many tokens run 12 waves where the
+# library has a 12-wave kernel (twelve_wave_format).
+TWELVE_WAVES_MIN_SPLIT = 8192
+
+
+def twelve_wave_format(D: int, G: int, k_nbits: int, v_nbits: int, group_size: int,
+                       paged: bool = False) -> bool:
+    """Whether the library has a 12-wave split kernel for this format (the list
+    in ``csrc/quant_split.h``, ``kTwelveWaves``): head_dim 128, contiguous
+    caches, and 2-bit K/V with groups of 32 at GQA groups of at most 4 query
+    heads (per-token or per-channel keys), or groups of 128 with equal K/V bits.
+    These kernels are bound by instruction issue, and a third wave per SIMD
+    gives it more to interleave (Llama-3-8B shape: 3-7% faster); a request of
+    12 waves for any other kernel runs 8."""
+    if D != 128 or paged:
+        return False
+    return (k_nbits == 2 and v_nbits == 2 and group_size == 32 and G <= 4) or \
+        (k_nbits == v_nbits and k_nbits in (2, 4) and group_size == 128)
+
+
+def choose_waves(B: int, HKV: int, G: int, split_size: int, num_splits: int = 0, *,
+                 D: int = 128, k_nbits: int = 16, v_nbits: int = 16, group_size: int = 0,
+                 paged: bool = False) -> int:
+    """Waves per workgroup: 12 for the formats of ``twelve_wave_format`` when a
+    workgroup streams at least ``TWELVE_WAVES_MIN_SPLIT`` tokens; else 8 when
+    it streams the whole history or at least 512 tokens (two 32-token chunks
+    per wave, so each wave overlaps a load with compute); else 4.  The default
+    format (16-bit) is the fp16 control's."""
+    if split_size >= TWELVE_WAVES_MIN_SPLIT and \
+            twelve_wave_format(D, G, k_nbits, v_nbits, group_size, paged):
+        return 12
     return 8 if num_splits == 1 or split_size >= 512 else 4
 
 
@@ -357,7 +384,8 @@ def fused_decode_attention(
         k_nbits=kq.nbits, v_nbits=vq.nbits, group_size=kq.group_size,
         sm_scale=float(sm_scale), split_size=split_size, num_splits=num_splits,
         counters=_lib.ptr(counters) if fused_combine else None,
-        waves=choose_waves(B, HKV, group, split_size, num_splits),
+        waves=choose_waves(B, HKV, group, split_size, num_splits, D=D, k_nbits=kq.nbits,
+                           v_nbits=vq.nbits, group_size=kq.group_size),
         k_new=_lib.ptr(kn), v_new=_lib.ptr(vn), new_is_fp32=new_f32)
     with torch.cuda.device(q.device):
         rc = _lib.load().tkv_fused_decode_attention(args, _lib.stream_handle(q.device))

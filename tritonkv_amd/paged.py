@@ -181,7 +181,8 @@ def paged_decode_attention(
         out=out.data_ptr(), B=B, HQ=HQ, HKV=HKV, S=S, D=D,
         k_nbits=k_pool.nbits, v_nbits=v_pool.nbits, group_size=k_pool.group_size,
         sm_scale=float(sm_scale), split_size=split_size, num_splits=num_splits, counters=None,
-        waves=choose_waves(B, HKV, group, split_size, num_splits),
+        waves=choose_waves(B, HKV, group, split_size, num_splits, D=D, k_nbits=k_pool.nbits,
+                           v_nbits=v_pool.nbits, group_size=k_pool.group_size, paged=True),
         block_table=table.data_ptr(), block_table_stride=table.shape[1], page_size=page_size,
         num_pages=num_pages, k_new=_lib.ptr(kn), v_new=_lib.ptr(vn), new_is_fp32=new_f32)
     with torch.cuda.device(q.device):
