@@ -722,6 +722,13 @@ quant_split_lds_kernel(SplitParams prm) {
     constexpr int PMODE = decltype(pmode)::value;
     constexpr bool HILO = PMODE == 2;
     constexpr bool PSREM = PMODE >= 1;
+    // Paired tiles with 16 head columns (one V group per row: no head columns)
+    // leave columns 8-15 without a head of their own (G <= 8).  With the
+    // P * s remainders those columns carry them -- column 8 + c the
+    // remainders of head c, which lane 8 + c holds anyway (both tiles, in
+    // order) -- so one V MFMA per product serves both, and the epilogue adds
+    // column 8 + c into column c.
+    constexpr bool FOLD = PMODE == 1 && PT && HS == 16;
     // refill the stage consumed by the previous chunk, NSTAGE-1 chunks ahead
     {
       const int cn = cb + (NSTAGE - 1) * cstride;
@@ -832,7 +839,7 @@ quant_split_lds_kernel(SplitParams prm) {
       // The PV operand of column c needs tile 0 then tile 1 of head c % HS:
       // lane c holds tile c >> 3 of it and lane c ^ 8 the other tile.  (With
       // HS = 16 the columns c >= 8 are padding heads and take any order.)
-      const bool swap = HS < 16 && r >= 8;
+      const bool swap = (HS < 16 || FOLD) && r >= 8;
       auto tiles = [&](uint32_t a0, uint32_t a1) -> u4 {
         const uint32_t o0 = lane_xor8(a0), o1 = lane_xor8(a1);
         return swap ? u4{o0, o1, a0, a1} : u4{a0, a1, o0, o1};
@@ -1024,6 +1031,10 @@ quant_split_lds_kernel(SplitParams prm) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) pgl[v][q] = pk_fma_rem(pb[q], sp[q], pg[v][q]);
       }
+      if constexpr (FOLD) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) pg[v][q] = r >= 8 ? pgl[v][q] : pg[v][q];
+      }
     }
 
     // ---- O^T += V^T P'^T ---------------------------------------------------
@@ -1061,7 +1072,7 @@ quant_split_lds_kernel(SplitParams prm) {
           const u4 av = (kVChain && p == VL::P - 1) ? u4{pm[0], pm[1], pm[2], pm[3]}
                                                     : u4{pm[0] & msk, pm[1] & msk, pm[2] & msk, pm[3] & msk};
           accv[mv] = mfma_k32(av, pg[VL::group_of(mv) / S], accv[mv]);
-          if constexpr (PSREM) accv[mv] = mfma_k32(av, pgl[VL::group_of(mv) / S], accv[mv]);
+          if constexpr (PSREM && !FOLD) accv[mv] = mfma_k32(av, pgl[VL::group_of(mv) / S], accv[mv]);
         }
       }
     }
@@ -1098,6 +1109,9 @@ quant_split_lds_kernel(SplitParams prm) {
   else stream(std::integral_constant<int, kPsRemainder<VNB, NG> ? 1 : 0>{});
   wait_vmcnt<0>();  // retire the trailing (out-of-range) prefetches
   wave_lds_fence();
+  // whether the V accumulators of columns 8-15 hold the P * s remainders of
+  // columns 0-7 (the stream ran with FOLD)
+  const bool folded = PT && HS == 16 && kPsRemainder<VNB, NG> && L > kHiLoMaxLen;
 
   // ---- this wave's partial into its own ring region -------------------------
   WavePartial<D>& wp = *reinterpret_cast<WavePartial<D>*>(ring);
@@ -1113,6 +1127,10 @@ quant_split_lds_kernel(SplitParams prm) {
       const float zv = ozg[VL::group_of(mv)];
       f4 a = accv[mv];
       if (kVChain && p > 0) a -= accv[VL::mfma_index(p - 1, VL::window_of(mv), VL::e_of(mv))];
+      if (folded) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] += lane_xor8(a[i]);
+      }
       if (S == 1 || VL::group_of(mv) % S == slot) {  // this column's products are group mv's
 #pragma unroll
         for (int i = 0; i < 4; ++i) wp.o[n % HS][VL::dim_of(mv, 4 * j + i)] = fmaf(a[i], fac, zv);
