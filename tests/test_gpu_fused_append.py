@@ -109,6 +109,50 @@ def test_fused_append_is_bit_identical_to_append_then_decode(case):
     assert_close_to_reference(got, ref, f"fused append {case}")
 
 
+@pytest.mark.parametrize("kbits,gs", [(2, 32), (2, 128), (4, 128)])
+def test_fused_append_in_twelve_wave_workgroups(kbits, gs):
+    """The fused append in the 12-wave kernels (one split of 9000 tokens at a
+    GQA group of 4): bit-identical to append-then-decode, and the oracle's
+    attention over the appended caches."""
+    from tritonkv_amd.kernels import fused_decode_attention
+    from tritonkv_amd.kernels.fused_decode_attn import choose_waves
+    from tritonkv_amd.quantize import append_kv
+
+    B, HQ, HKV, D, S = 3, 8, 2, 128, 9000
+    assert choose_waves(B, HKV, HQ // HKV, S, 1, D=D, k_nbits=kbits, v_nbits=kbits,
+                        group_size=gs) == 12
+    lens = torch.tensor([9000, 8193, 100], dtype=torch.int32)
+    print(f"fused append, 12 waves: K{kbits}V{kbits} gs{gs}", flush=True)
+    q, k, v = oinp.make_random_kv(B, HQ, HKV, S, D, seed=41 + gs)
+    q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
+    g = torch.Generator().manual_seed(9)
+    k_new = torch.randn(B, HKV, D, generator=g).half().to(DEV)
+    v_new = torch.randn(B, HKV, D, generator=g).half().to(DEV)
+    kc0, vc0 = _caches(k, v, kbits, kbits, gs, (lens - 1).tolist())
+    lens_d = lens.to(DEV)
+    ka, va = _clone(kc0), _clone(vc0)
+    append_kv(ka, k_new[:, :, None], lens_d - 1)
+    append_kv(va, v_new[:, :, None], lens_d - 1)
+    want = fused_decode_attention(q, ka, va, num_splits=1, seq_lens=lens_d)
+    kb, vb = _clone(kc0), _clone(vc0)
+    got = fused_decode_attention(q, kb, vb, num_splits=1, seq_lens=lens_d, k_new=k_new,
+                                 v_new=v_new)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want), (got - want).abs().max().item()
+    assert _same(ka, kb) and _same(va, vb)
+    clean = []
+    for c in (ka, va):
+        c = _clone(c)
+        for b in range(B):
+            L = int(lens[b])
+            c.packed[b, :, L:] = 0
+            c.scale[b, :, L:] = 0
+            c.zero[b, :, L:] = 0
+        clean.append(c)
+    ref = oracle_attention_on_quant(q, clean[0], clean[1], seq_lens=lens.numpy())
+    assert_close_to_reference(got, ref, f"fused append, 12 waves, K{kbits} gs{gs}")
+
+
 def test_fused_append_fp32_tokens_and_no_seq_lens():
     """fp32 new tokens; without seq_lens the token goes to the last slot S - 1."""
     from tritonkv_amd.kernels import fused_decode_attention
