@@ -493,6 +493,38 @@ def test_workgroup_size_and_combine_mode(waves, fused_combine, num_splits):
         assert int(cnt.abs().sum()) == 0
 
 
+@pytest.mark.parametrize("fused_combine", [False, True])
+def test_twelve_wave_splits_and_combine_modes(fused_combine):
+    """12-wave workgroups writing split partials (3 splits), merged by the
+    combine kernel or by the last workgroup; the tickets reset every call."""
+    from tritonkv_amd import _lib
+    from tritonkv_amd.kernels import plan_splits
+
+    B, HQ, HKV, D, S = 2, 8, 2, 128, 5000
+    q, k, v, kq, vq = make_case(B, HQ, HKV, D, S, 2, 32, 31)
+    _, ns, size = plan_splits(S, 64, 3, B, HKV, HQ // HKV)
+    acc = torch.empty(B, HQ, ns, D, device=DEV)
+    mx = torch.empty(B, HQ, ns, device=DEV)
+    sm = torch.empty(B, HQ, ns, device=DEV)
+    cnt = torch.zeros(B * HKV, dtype=torch.int32, device=DEV)
+    out = torch.empty(B, HQ, D, device=DEV)
+    a = _lib.DecodeArgs(q=q.data_ptr(), k=kq.packed.data_ptr(), k_scale=kq.scale.data_ptr(),
+                        k_zero=kq.zero.data_ptr(), v=vq.packed.data_ptr(),
+                        v_scale=vq.scale.data_ptr(), v_zero=vq.zero.data_ptr(),
+                        acc=acc.data_ptr(), maxs=mx.data_ptr(), sums=sm.data_ptr(),
+                        out=out.data_ptr(), B=B, HQ=HQ, HKV=HKV, S=S, D=D, k_nbits=2,
+                        v_nbits=2, group_size=32, sm_scale=D ** -0.5, split_size=size,
+                        num_splits=ns, counters=cnt.data_ptr() if fused_combine else None,
+                        waves=12)
+    ref = oracle_attention_on_quant(q, kq, vq)
+    for rep in range(3):
+        out.fill_(float("nan"))
+        _lib.check(_lib.load().tkv_fused_decode_attention(a, _lib.stream_handle(q.device)), "fused")
+        torch.cuda.synchronize()
+        assert_close_to_reference(out, ref, f"12 waves fused={fused_combine} ns={ns} rep={rep}")
+        assert int(cnt.abs().sum()) == 0
+
+
 @pytest.mark.parametrize("kbits,vbits,gs,waves", [(4, 4, 32, 8), (2, 2, 128, 4), (4, 2, 32, 8)])
 def test_read_probe_runs_over_the_split_kernels_reads(kbits, vbits, gs, waves):
     """tkv_read_probe (the bandwidth-ceiling probe of the split kernel's access
