@@ -1153,7 +1153,7 @@ quant_split_lds_kernel(SplitParams prm) {
 // in flight per wave already saturates what this access pattern streams.
 // Paged caches use two stages.
 constexpr int kStages8 = 2;  // also the ring depth of 12-wave workgroups
-static_assert(kStages8 == 2, "kFits12Waves sizes two-stage rings");
+static_assert(kStages8 == 2, "kTwelveWaves sizes two-stage rings");
 constexpr int kStages4 = 2;
 
 template <int D, int KNB, int VNB, int GS, bool PT, int HS>
