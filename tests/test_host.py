@@ -326,12 +326,16 @@ def test_default_split_plan_covers_history_without_empty_splits(B, HKV, G, S):
         assert ns >= 1 and size * ns >= S and size * (ns - 1) < S
 
 
-def test_ragged_batches_of_a_unit_per_cu_split_long_histories_in_two(monkeypatch):
+def test_ragged_batches_of_a_unit_per_cu_split_long_histories(monkeypatch):
     from tritonkv_amd.kernels import fused_decode_attn as fda
 
     monkeypatch.setattr(fda, "compute_units", lambda: 256)
     assert fda.plan_splits(131072, 64, None, 64, 8, 8)[1] == 1
-    assert fda.plan_splits(131072, 64, None, 64, 8, 8, ragged=True)[1] == 2
+    # pieces of at most 32768 tokens, at least two
+    assert fda.plan_splits(131072, 64, None, 64, 8, 8, ragged=True)[1] == 4
+    assert fda.plan_splits(131072 + 64, 64, None, 64, 8, 8, ragged=True)[1] == 4
+    assert fda.plan_splits(32768, 64, None, 32, 8, 4, ragged=True)[1] == 2
+    assert fda.plan_splits(16384, 64, None, 32, 8, 4, ragged=True)[1] == 2
     assert fda.plan_splits(8192, 64, None, 64, 8, 8, ragged=True)[1] == 1  # short: unsplit
     # below one unit per CU the ordinary policy applies either way
     assert fda.plan_splits(32768, 64, None, 4, 8, 4, ragged=True) == \

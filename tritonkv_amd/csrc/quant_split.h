@@ -440,6 +440,22 @@ quant_split_lds_kernel(SplitParams prm) {
   const int r = lane & 15, j = lane >> 4;
   const int n = r;
   const int slot = r / HS;  // V-group slot of this lane's column
+  // An empty split (a row of a ragged batch that ends before the split
+  // starts) writes the empty partial -- max -inf, sum 0, output 0 -- and
+  // leaves, with no q operands, DMA or merge.  With counters (the
+  // last-workgroup merge counts every split's ticket) it takes the full path.
+  if (lo >= L && prm.ns_total > 1 && prm.counters == nullptr) {
+    for (int idx = tid; idx < nh * D; idx += NW * 64) {
+      const int hn = idx / D, d = idx % D;
+      const int64_t pr = ((int64_t)b * prm.HQ + h0 + hn) * prm.ns_total + prm.split_base + split;
+      prm.acc[pr * D + d] = 0.0f;
+      if (d == 0) {
+        prm.maxs[pr] = -INFINITY;
+        prm.sums[pr] = 0.0f;
+      }
+    }
+    return;
+  }
   // Where a chunk's rows live.  Contiguous caches: one buffer resource per
   // tensor over this (b, kv head) block, chunk rows at token index cb.  Paged
   // caches: resources over the (pool page, kv head) slab holding the chunk

@@ -131,10 +131,13 @@ def default_num_splits(B: int, HKV: int, G: int, S: int, block_n: int,
 
     With per-row lengths (``ragged``: the call passes ``seq_lens``, which the
     host cannot read without a sync), a batch of at least one unit per compute
-    unit and a history of at least 16384 tokens is cut in two: rows of very
-    different lengths make one workgroup per unit finish unevenly, and halves
-    even that out (B=64, HKV=8, lengths U[1k, 128k]: 789 vs 875 us) at no cost
-    when the lengths are equal (Llama-3-8B shape: 208.7 vs 209.2 us).
+    unit and a history of at least 16384 tokens is cut into pieces of at most
+    32768 tokens, and at least two: rows of very different lengths make one
+    workgroup per unit finish unevenly, and shorter pieces even that out.
+    B=64, HKV=8, lengths U[1k, 128k], K4/V2: 875 us unsplit, 736 us at 2
+    splits, 718 us at 4 (a split past a row's end leaves at once), 725 us at
+    8.  Two splits cost nothing when the lengths are equal (Llama-3-8B shape:
+    208.7 vs 209.2 us).
 
     Returned in units of ``block_n`` blocks so the reference's tightening
     applies unchanged.
@@ -144,7 +147,9 @@ def default_num_splits(B: int, HKV: int, G: int, S: int, block_n: int,
     if S <= tokens_per_workgroup:
         return 1
     if units >= cu:
-        return min(2, _cdiv(S, block_n)) if ragged and S >= 16384 else 1
+        if not ragged or S < 16384:
+            return 1
+        return min(max(2, S // 32768), _cdiv(S, block_n))
     workgroups = min(cu, max(32, units * S // tokens_per_workgroup))
     want = max(1, workgroups // units)
     max_splits = max(1, S // max(tokens_per_workgroup // 4, block_n))
