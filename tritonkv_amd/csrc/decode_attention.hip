@@ -350,6 +350,68 @@ __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ 
   combine_row<D, false>(acc, maxs, sums, out, ns, ns, WindowArgs{});
 }
 
+// Few splits (ns <= MAXS <= 32, no window): one wave per row and no LDS.
+// Lane (g, dq) merges splits g, g + NGRP, ... of float4 column dq, all its
+// loads issued before the first is used; the NGRP groups then meet through
+// lane exchanges.  At the Qwen2.5-1.5B shape (12 rows, 16-32 splits) the
+// combine is pure latency, and this drops its barrier and LDS round trips.
+constexpr int kSmallCombineMaxSplits = 32;
+
+template <int D, int MAXS>
+__global__ void __launch_bounds__(64) combine_small_kernel(const float* __restrict__ acc,
+                                                           const float* __restrict__ maxs,
+                                                           const float* __restrict__ sums,
+                                                           float* __restrict__ out, int ns) {
+  constexpr int DQ = D / 4;          // float4 columns of a row
+  constexpr int NGRP = 64 / DQ;      // split groups
+  constexpr int PER = MAXS / NGRP;   // splits per lane at most
+  const int64_t row = blockIdx.x;
+  const int lane = threadIdx.x, dq = lane % DQ, g = lane / DQ;
+  float ms[PER], ls[PER];
+  f4 as[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int64_t ps = row * ns + min(g + NGRP * i, ns - 1);  // past ns: clamped, skipped
+    ms[i] = maxs[ps];
+    ls[i] = sums[ps];
+    as[i] = reinterpret_cast<const f4*>(acc + ps * D)[dq];
+  }
+  float m = -INFINITY, l = 0.0f;
+  f4 a = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    if (g + NGRP * i >= ns || ms[i] == -INFINITY) continue;
+    const float mn = fmaxf(m, ms[i]);
+    const float al = safe_exp2_diff(m, mn);
+    const float be = __builtin_amdgcn_exp2f(ms[i] - mn);
+    a = a * al + as[i] * be;
+    l = l * al + ls[i] * be;
+    m = mn;
+  }
+#pragma unroll
+  for (int off = DQ; off < 64; off *= 2) {
+    const float mo = __shfl_xor(m, off, 64), lo = __shfl_xor(l, off, 64);
+    f4 ao;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ao[e] = __shfl_xor(a[e], off, 64);
+    const float mn = fmaxf(m, mo);
+    const float al = safe_exp2_diff(m, mn), be = safe_exp2_diff(mo, mn);
+    a = a * al + ao * be;
+    l = l * al + lo * be;
+    m = mn;
+  }
+  if (g == 0) reinterpret_cast<f4*>(out + row * D)[dq] = a / l;
+}
+
+template <int D>
+static void launch_combine_small(const float* acc, const float* maxs, const float* sums,
+                                 float* out, dim3 grid, int ns, hipStream_t st) {
+  if (ns <= kSmallCombineMaxSplits / 2)
+    combine_small_kernel<D, kSmallCombineMaxSplits / 2><<<grid, dim3(64), 0, st>>>(acc, maxs, sums, out, ns);
+  else
+    combine_small_kernel<D, kSmallCombineMaxSplits><<<grid, dim3(64), 0, st>>>(acc, maxs, sums, out, ns);
+}
+
 template <int D>
 __global__ void __launch_bounds__(256) combine_window_kernel(const float* __restrict__ acc,
                                                              const float* __restrict__ maxs,
@@ -496,11 +558,14 @@ static int launch_combine(const float* acc, const float* maxs, const float* sums
                           const WindowArgs* win = nullptr) {
   const dim3 grid((unsigned)(B * HQ));
   const int sd = stride ? stride : ns;
+  const bool small = !win && ns <= kSmallCombineMaxSplits;
   if (D == 128) {
     if (win) combine_window_kernel<128><<<grid, dim3(256), 0, st>>>(acc, maxs, sums, out, ns, sd, *win);
+    else if (small) launch_combine_small<128>(acc, maxs, sums, out, grid, ns, st);
     else combine_kernel<128><<<grid, dim3(256), 0, st>>>(acc, maxs, sums, out, ns);
   } else if (D == 64) {
     if (win) combine_window_kernel<64><<<grid, dim3(256), 0, st>>>(acc, maxs, sums, out, ns, sd, *win);
+    else if (small) launch_combine_small<64>(acc, maxs, sums, out, grid, ns, st);
     else combine_kernel<64><<<grid, dim3(256), 0, st>>>(acc, maxs, sums, out, ns);
   } else {
     return TKV_EUNSUPPORTED;
