@@ -350,12 +350,12 @@ __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ 
   combine_row<D, false>(acc, maxs, sums, out, ns, ns, WindowArgs{});
 }
 
-// Few splits (ns <= MAXS <= 32, no window): one wave per row and no LDS.
+// Few splits (ns <= MAXS <= 64, no window): one wave per row and no LDS.
 // Lane (g, dq) merges splits g, g + NGRP, ... of float4 column dq, all its
 // loads issued before the first is used; the NGRP groups then meet through
-// lane exchanges.  At the Qwen2.5-1.5B shape (12 rows, 16-32 splits) the
+// lane exchanges.  At the Qwen2.5-1.5B shape (12 rows, 16-64 splits) the
 // combine is pure latency, and this drops its barrier and LDS round trips.
-constexpr int kSmallCombineMaxSplits = 32;
+constexpr int kSmallCombineMaxSplits = 64;
 
 template <int D, int MAXS>
 __global__ void __launch_bounds__(64) combine_small_kernel(const float* __restrict__ acc,
@@ -406,10 +406,12 @@ __global__ void __launch_bounds__(64) combine_small_kernel(const float* __restri
 template <int D>
 static void launch_combine_small(const float* acc, const float* maxs, const float* sums,
                                  float* out, dim3 grid, int ns, hipStream_t st) {
-  if (ns <= kSmallCombineMaxSplits / 2)
-    combine_small_kernel<D, kSmallCombineMaxSplits / 2><<<grid, dim3(64), 0, st>>>(acc, maxs, sums, out, ns);
+  if (ns <= 16)
+    combine_small_kernel<D, 16><<<grid, dim3(64), 0, st>>>(acc, maxs, sums, out, ns);
+  else if (ns <= 32)
+    combine_small_kernel<D, 32><<<grid, dim3(64), 0, st>>>(acc, maxs, sums, out, ns);
   else
-    combine_small_kernel<D, kSmallCombineMaxSplits><<<grid, dim3(64), 0, st>>>(acc, maxs, sums, out, ns);
+    combine_small_kernel<D, 64><<<grid, dim3(64), 0, st>>>(acc, maxs, sums, out, ns);
 }
 
 template <int D>
