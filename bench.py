@@ -614,6 +614,10 @@ def ragged_70b(steps, warmup, seed=2024):
         fused_decode_attention(q, kc, vc, seq_lens=lens1, allow_mixed_bits=True, out=out,
                                _workspace=ws, k_new=k_new, v_new=v_new)
 
+    def decode_natural():  # split workgroups in grid order, no longest-first order
+        fused_decode_attention(q, kc, vc, seq_lens=lens1, allow_mixed_bits=True, out=out,
+                               _workspace=ws, dispatch_order=False)
+
     torch.cuda.synchronize()
     row = cache_row_bytes(D, 4, gs) + cache_row_bytes(D, 2, gs)
     tokens = int(lens1.sum())
@@ -622,17 +626,20 @@ def ragged_70b(steps, warmup, seed=2024):
     us, _, _ = timed_steps([step], steps, warmup)
     dus, _, _ = timed_steps([decode], steps, warmup)
     fus, _, _ = timed_steps([fused_step], steps, warmup)
+    nus, _, _ = timed_steps([decode_natural], steps, warmup)
     total = decode_bytes + append_bytes
     res = {"us_per_step": round(us, 2), "decode_us": round(dus, 2),
            "append_us": round(us - dus, 2), "fused_append_step_us": round(fus, 2),
+           "decode_us_natural_order": round(nus, 2),
            "sum_tokens": tokens,
            "algorithmic_bytes": total,
            "gbps_step": round(total / us / 1e3, 1),
            "frac_of_hbm_peak_step": round(total / us / 1e3 / HBM_PEAK_GBS, 4),
            "frac_of_hbm_peak_decode": round(decode_bytes / dus / 1e3 / HBM_PEAK_GBS, 4),
            "lengths": "S_b ~ U[1024, 131072], torch.Generator().manual_seed(%d)" % seed}
-    print(f"# ragged 70b K4/V2: step {us:.1f} us (decode {dus:.1f} us, fused append+decode "
-          f"{fus:.1f} us), {total / us / 1e3:.0f} GB/s", file=sys.stderr, flush=True)
+    print(f"# ragged 70b K4/V2: step {us:.1f} us (decode {dus:.1f} us, natural order "
+          f"{nus:.1f} us, fused append+decode {fus:.1f} us), {total / us / 1e3:.0f} GB/s",
+          file=sys.stderr, flush=True)
     del kc, vc, ws
     torch.cuda.empty_cache()
     return res

@@ -115,6 +115,19 @@ typedef struct tkv_decode_args {
    * *_attention entry points need split_base == 0 and num_splits_total equal
    * to num_splits (or 0); counters likewise. */
   int32_t split_base, num_splits_total;
+  /* Dispatch order (quantized path only; NULL: the natural order).  A caller
+   * buffer of B * HKV * num_splits int32 that the call fills, with one small
+   * launch ahead of the split kernel, with a longest-piece-first order of the
+   * split workgroups: piece (b, s), tokens [s * split_size, (s + 1) *
+   * split_size) of row b, ranked by its length under seq_lens, longest first.
+   * The split kernel then takes its (unit, split) from that order, so in a
+   * ragged batch the short pieces fill the end of the launch instead of a full
+   * piece of a long row starting last.  Every (unit, split) still runs once and
+   * writes its own partial row, so out is bit-identical to work_order == NULL.
+   * Unused when num_splits == 1; the fp16 path returns TKV_EUNSUPPORTED and
+   * the _noalloc entry TKV_EINVAL for a non-NULL work_order.  No counterpart
+   * in the reference (its Triton grid runs splits in program-id order). */
+  int32_t *work_order;
 } tkv_decode_args;
 
 /* Fused 2/4-bit split-P decode attention: the split kernel, then (if
@@ -290,7 +303,7 @@ const char *tkv_status_string(int status);
  * fused-append fields, 5 the per-channel key and partials-placement fields,
  * tkv_quantize_keys_channel, tkv_channel_decode_attention and the
  * tkv_channel_window_* calls, 6 tkv_fused_decode_attention_noalloc,
- * TKV_ESCRATCH and tkv_read_probe). */
+ * TKV_ESCRATCH and tkv_read_probe, 7 the work_order field). */
 int tkv_abi_version(void);
 
 #ifdef __cplusplus

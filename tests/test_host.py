@@ -45,7 +45,7 @@ def test_library_exports_every_declared_symbol():
     for name in _declared_symbols():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.tkv_abi_version() == 6
+    assert lib.tkv_abi_version() == 7
 
 
 def test_library_is_gfx950_only():
@@ -93,6 +93,44 @@ def test_decode_args_layout_matches_c():
                     A.block_table.offset, A.page_size.offset, A.num_pages.offset,
                     A.k_new.offset, A.new_is_fp32.offset, A.key_block.offset,
                     A.num_splits_total.offset, ctypes.sizeof(_lib.DeviceInfo)]
+
+
+def test_work_order_argument_checks_without_a_gpu():
+    """work_order: 4-byte aligned, slots that fit int32, quantized path only and
+    not with the allocation-free entry (each check returns before any launch)."""
+    from tritonkv_amd import _lib
+
+    lib = _lib.load()
+    dummy = 0x1000
+    a = _lib.DecodeArgs(q=dummy, k=dummy, v=dummy, k_scale=dummy, k_zero=dummy, v_scale=dummy,
+                        v_zero=dummy, out=dummy, acc=dummy, maxs=dummy, sums=dummy, B=2, HQ=4,
+                        HKV=2, S=256, D=128, k_nbits=4, v_nbits=4, group_size=32, sm_scale=0.1,
+                        split_size=64, num_splits=4, waves=8, work_order=dummy + 2)
+    assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    assert lib.tkv_fused_decode_split(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    a.work_order = dummy
+    assert lib.tkv_fp16_decode_attention(ctypes.byref(a), None) == _lib.TKV_EUNSUPPORTED
+    assert lib.tkv_fp16_decode_split(ctypes.byref(a), None) == _lib.TKV_EUNSUPPORTED
+    a.acc = a.maxs = a.sums = None
+    assert lib.tkv_fused_decode_attention_noalloc(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    a.acc = a.maxs = a.sums = dummy
+    a.B, a.HQ, a.HKV = 1 << 15, 1 << 15, 1 << 15  # B * HKV * num_splits = 2^32 slots
+    assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
+
+
+def test_order_buffer_policy():
+    """The Python entries take a work_order buffer for ragged split calls only."""
+    from tritonkv_amd.kernels.fused_decode_attn import _order_for
+
+    lens = object()  # only its presence matters
+    assert _order_for({}, 2, 2, 1, "cpu", lens, None) is None      # unsplit
+    assert _order_for({}, 2, 2, 4, "cpu", None, None) is None      # equal lengths
+    assert _order_for({}, 2, 2, 4, "cpu", lens, False) is None
+    ws = {}
+    buf = _order_for(ws, 2, 3, 4, "cpu", lens, None)
+    assert buf.dtype == torch.int32 and buf.numel() == 24 and ws["work_order"] is buf
+    assert _order_for(ws, 2, 3, 2, "cpu", lens, None) is buf       # reused when large enough
+    assert _order_for({}, 2, 3, 4, "cpu", None, True).numel() == 24
 
 
 def test_c_entry_points_reject_bad_arguments_without_a_gpu():

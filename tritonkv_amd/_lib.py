@@ -67,6 +67,7 @@ class DecodeArgs(ctypes.Structure):
         ("key_block", ctypes.c_int32),
         ("split_base", ctypes.c_int32),
         ("num_splits_total", ctypes.c_int32),
+        ("work_order", ctypes.c_void_p),
     ]
 
 

@@ -423,6 +423,25 @@ __global__ void __launch_bounds__(256) combine_window_kernel(const float* __rest
   combine_row<D, true>(acc, maxs, sums, out, ns, stride, w);
 }
 
+// ---------------------------------------------------------------------------
+// Dispatch order of a ragged batch: one thread per piece (b, s), piece index
+// s * B + b; writes the HKV (unit, split) slots of its rank (longest piece
+// first, ragged_piece_rank).  O(B) per thread, with seq_lens read at uniform
+// addresses.  The ranks of all pieces are distinct, so order is a permutation
+// of the B * HKV * ns workgroups of the split grid.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+ragged_order_kernel(const int32_t* __restrict__ seq_lens, int B, int S, int HKV, int ns, int ss,
+                    int32_t* __restrict__ order) {
+  const int p = blockIdx.x * 256 + threadIdx.x;
+  if (p >= B * ns) return;
+  const int s = p / B, b = p - s * B;
+  auto lens = [&](int i) { return seq_lens ? max(0, min(seq_lens[i], S)) : S; };
+  const int rank = ragged_piece_rank(b, s, B, ss, lens);
+  const int BU = B * HKV;
+  for (int hk = 0; hk < HKV; ++hk) order[(int64_t)rank * HKV + hk] = s * BU + b * HKV + hk;
+}
+
 // ===========================================================================
 // Host side: validation and dispatch.
 // ===========================================================================
@@ -461,6 +480,11 @@ static int validate_common(const tkv_decode_args* a) {
     if (!a->v_new) return TKV_EINVAL;
     if (((uintptr_t)a->k_new | (uintptr_t)a->v_new) & (a->new_is_fp32 ? 3 : 1)) return TKV_EINVAL;
   }
+  if (a->work_order) {
+    if ((uintptr_t)a->work_order & 3) return TKV_EINVAL;
+    // slots hold s * B * HKV + unit as int32
+    if ((int64_t)a->B * a->HKV * a->num_splits > INT32_MAX) return TKV_EINVAL;
+  }
   if (a->D != 64 && a->D != 128) return TKV_EUNSUPPORTED;
   return TKV_OK;
 }
@@ -498,6 +522,7 @@ static SplitParams make_params(const tkv_decode_args* a) {
   p.key_block = a->key_block;
   p.split_base = a->split_base;
   p.ns_total = a->num_splits_total ? a->num_splits_total : a->num_splits;
+  p.order = nullptr;  // set by launch_fused_split once the order is written
   return p;
 }
 
@@ -594,9 +619,15 @@ static int launch_fused_split(const tkv_decode_args* a, hipStream_t st, bool pro
   if ((a->k_nbits != 2 && a->k_nbits != 4) || (a->v_nbits != 2 && a->v_nbits != 4))
     return TKV_EINVAL;
   if (a->key_block && gs > 32) return TKV_EUNSUPPORTED;  // per-channel keys: V groups of 16 or 32
-  const SplitParams p = make_params(a);
+  SplitParams p = make_params(a);
   const dim3 grid = split_grid(a);
   (void)hipGetLastError();
+  if (a->work_order && a->num_splits > 1) {
+    const int pieces = a->B * a->num_splits;
+    ragged_order_kernel<<<dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, st>>>(
+        a->seq_lens, a->B, a->S, a->HKV, a->num_splits, a->split_size, a->work_order);
+    p.order = a->work_order;
+  }
   rc = a->D == 128 ? dispatch_bits<128>(p, grid, a->k_nbits, a->v_nbits, gs, a->waves, st, probe)
                    : dispatch_bits<64>(p, grid, a->k_nbits, a->v_nbits, gs, a->waves, st, probe);
   if (rc) return rc;
@@ -606,8 +637,8 @@ static int launch_fused_split(const tkv_decode_args* a, hipStream_t st, bool pro
 static int launch_fp16_split(const tkv_decode_args* a, hipStream_t st) {
   const int rc = validate_common(a);
   if (rc) return rc;
-  // the fp16 control reads contiguous caches and has no fused append
-  if (a->page_size > 0 || a->k_new || a->key_block) return TKV_EUNSUPPORTED;
+  // the fp16 control reads contiguous caches in the natural order and has no fused append
+  if (a->page_size > 0 || a->k_new || a->key_block || a->work_order) return TKV_EUNSUPPORTED;
   const SplitParams p = make_params(a);
   const dim3 grid = split_grid(a);
   (void)hipGetLastError();
@@ -709,6 +740,7 @@ extern "C" int tkv_channel_decode_attention(const tkv_decode_args* a, const void
   ra.counters = nullptr;
   ra.key_block = 0;
   ra.waves = 4;
+  ra.work_order = nullptr;
   rc = launch_fp16_split(&ra, st);
   if (rc) return rc;
   (void)hipGetLastError();
@@ -759,7 +791,8 @@ constexpr uint64_t align256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
 extern "C" int tkv_fused_decode_attention_noalloc(const tkv_decode_args* a, tkv_stream_t stream) {
   using namespace tkv;
   if (!a || !own_all_splits(a)) return TKV_EINVAL;
-  if (a->acc || a->maxs || a->sums || a->counters) return TKV_EINVAL;  // the partials are ours
+  if (a->acc || a->maxs || a->sums || a->counters || a->work_order)  // the partials are ours
+    return TKV_EINVAL;
   if (a->B <= 0 || a->HQ <= 0 || a->D <= 0 || a->num_splits <= 0) return TKV_EINVAL;
   tkv_decode_args s = *a;
   if (a->num_splits > 1) {

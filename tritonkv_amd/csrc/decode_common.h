@@ -44,7 +44,42 @@ struct SplitParams {
   int key_block;
   // This launch's splits are partial rows split_base + split of ns_total.
   int split_base, ns_total;
+  // Dispatch order (quantized path), or null: workgroup i = y * gridDim.x + x
+  // of each z slice runs (unit, split) = (order[i] % gridDim.x, order[i] /
+  // gridDim.x) instead of (x, y).  A permutation, so every (unit, split) runs
+  // once and writes its own partial row: the result does not depend on it.
+  const int32_t* order;
 };
+
+// Longest piece first: the dispatch order ragged_order_kernel writes.  Piece
+// (b, s) is tokens [s * ss, min((s + 1) * ss, L_b)) of row b (empty past the
+// row's end); pieces are ranked by length, longest first, ties by s * B + b
+// (the natural y-major order), and the HKV units of a piece take consecutive
+// slots.  The dispatcher starts workgroups in slot order as CUs free up, so
+// the short pieces fill the gaps at the end instead of a full piece of a long
+// row starting last.  Returns the rank of piece (b, s); lens(i) gives L_i
+// already clamped to [0, S].
+template <class Lens>
+__host__ __device__ inline int ragged_piece_rank(int b, int s, int B, int ss, Lens lens) {
+  const int Lb = lens(b);
+  const int len = max(0, min(Lb - s * ss, ss));
+  int rank = 0;
+  for (int b2 = 0; b2 < B; ++b2) {
+    const int L2 = lens(b2);
+    const int f2 = L2 / ss, r2 = L2 - f2 * ss;  // full pieces, remainder
+    const int n2 = f2 + (r2 > 0);                // non-empty pieces
+    const int before = s + (b2 < b);             // pieces s2 of row b2 with s2 * B + b2 < s * B + b
+    if (len < ss) rank += f2;                    // full pieces are longer
+    if (r2 > len) rank += 1;
+    if (len == ss)
+      rank += min(f2, before);
+    else if (len > 0)
+      rank += (r2 == len && f2 < before);
+    else
+      rank += max(0, before - n2);  // empty pieces s2 in [n2, before)
+  }
+  return rank;
+}
 
 constexpr int kChunk = 32;  // tokens per wave iteration (two 16-row MFMA tiles)
 

@@ -425,8 +425,16 @@ quant_split_lds_kernel(SplitParams prm) {
 
   __shared__ __attribute__((aligned(16))) uint8_t smem[NW * SM::WAVE + SM::PATCH + (PT ? 0 : SM::QOP)];
 
-  const int unit = blockIdx.x;   // fastest: consecutive workgroups (which the
-  const int split = blockIdx.y;  // dispatcher deals to the 8 XCDs in turn) take other units
+  // x fastest: consecutive workgroups (which the dispatcher deals to the 8 XCDs
+  // in turn) take other units.  A ragged batch may pass a longest-first order.
+  int unit_ = blockIdx.x, split_ = blockIdx.y;
+  if (prm.order) {
+    const int idx = prm.order[blockIdx.y * gridDim.x + blockIdx.x];
+    unit_ = idx % (int)gridDim.x;
+    split_ = idx / (int)gridDim.x;
+  }
+  const int unit = __builtin_amdgcn_readfirstlane(unit_);
+  const int split = __builtin_amdgcn_readfirstlane(split_);
   const int b = unit / prm.HKV, hk = unit % prm.HKV;
   const int hb0 = blockIdx.z * 16;
   const int nh = min(16, prm.G - hb0);
@@ -1216,7 +1224,14 @@ __global__ void __launch_bounds__(NW * 64) read_probe_kernel(SplitParams prm) {
   constexpr int NG = SG::NG;
   constexpr int NI = SG::NINSTR;
   __shared__ __attribute__((aligned(16))) uint8_t smem[NW * 2 * SG::BYTES];
-  const int unit = blockIdx.x, split = blockIdx.y;
+  int unit_ = blockIdx.x, split_ = blockIdx.y;
+  if (prm.order) {  // the split kernel's dispatch order
+    const int idx = prm.order[blockIdx.y * gridDim.x + blockIdx.x];
+    unit_ = idx % (int)gridDim.x;
+    split_ = idx / (int)gridDim.x;
+  }
+  const int unit = __builtin_amdgcn_readfirstlane(unit_);
+  const int split = __builtin_amdgcn_readfirstlane(split_);
   const int b = unit / prm.HKV;
   const int L = prm.seq_lens ? min(prm.seq_lens[b], prm.S) : prm.S;
   const int lo = split * prm.split_size;

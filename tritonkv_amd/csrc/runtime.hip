@@ -42,4 +42,4 @@ extern "C" const char* tkv_status_string(int status) {
   return "unknown tritonkv_amd status";
 }
 
-extern "C" int tkv_abi_version(void) { return 6; }
+extern "C" int tkv_abi_version(void) { return 7; }

@@ -237,6 +237,27 @@ def _workspace_for(ws: dict | None, B: int, HQ: int, num_splits: int, D: int, de
     return ws["acc"], ws["maxs"], ws["sums"], cnt
 
 
+def _order_for(ws: dict | None, B: int, HKV: int, num_splits: int, device, seq_lens,
+               dispatch_order: bool | None):
+    """The ``work_order`` buffer of a split call, or None.
+
+    ``dispatch_order=None`` takes it whenever ``seq_lens`` is given and the
+    history is split: the call then runs the split workgroups longest piece
+    first (``ragged_order_kernel``), which evens out the end of the launch when
+    rows differ in length (B=64, HKV=8, lengths U[1k, 128k], K4/V2).  The
+    output is bit-identical either way; ``False`` keeps the natural order.
+    """
+    if num_splits <= 1 or dispatch_order is False or (dispatch_order is None and seq_lens is None):
+        return None
+    ws = ws if ws is not None else {}
+    n = B * HKV * num_splits
+    buf = ws.get("work_order")
+    if buf is None or buf.numel() < n or buf.device != torch.device(device):
+        buf = torch.empty(n, device=device, dtype=torch.int32)
+        ws["work_order"] = buf
+    return buf
+
+
 def _aligned16(t: torch.Tensor) -> torch.Tensor:
     """q (a few KB) as the kernels load it: contiguous and 16-byte aligned,
     copied if it is not."""
@@ -329,12 +350,15 @@ def fused_decode_attention(
     fused_combine: bool = False,
     k_new: torch.Tensor | None = None,
     v_new: torch.Tensor | None = None,
+    dispatch_order: bool | None = None,
 ) -> torch.Tensor:
     """Single decode step of attention, computed directly on packed low-bit K/V.
 
     q: ``(B, HQ, D)`` fp16 or fp32 (rounded to fp16 in the kernel, as the
     reference does); kq, vq: quantized caches with ``packed`` of shape
     ``(B, HKV, S, D//P)``.  Returns ``(B, HQ, D)`` float32.
+    ``dispatch_order`` (new): longest-piece-first order of the split
+    workgroups (``_order_for``); the result does not depend on it.
     """
     if kq.group_size != vq.group_size or (kq.nbits != vq.nbits and not allow_mixed_bits):
         raise ValueError("K and V must use the same nbits/group_size")
@@ -379,6 +403,7 @@ def fused_decode_attention(
     out = _check_out(out, B, HQ, D, q.device)
     acc, maxs, sums, counters = _workspace_for(_workspace, B, HQ, num_splits, D, q.device, HKV)
     lens = _seq_lens_arg(seq_lens, B, S, q.device)
+    order = _order_for(_workspace, B, HKV, num_splits, q.device, seq_lens, dispatch_order)
 
     args = _lib.DecodeArgs(
         q=q.data_ptr(), q_is_fp32=int(q.dtype == torch.float32),
@@ -391,7 +416,8 @@ def fused_decode_attention(
         counters=_lib.ptr(counters) if fused_combine else None,
         waves=choose_waves(B, HKV, group, split_size, num_splits, D=D, k_nbits=kq.nbits,
                            v_nbits=vq.nbits, group_size=kq.group_size),
-        k_new=_lib.ptr(kn), v_new=_lib.ptr(vn), new_is_fp32=new_f32)
+        k_new=_lib.ptr(kn), v_new=_lib.ptr(vn), new_is_fp32=new_f32,
+        work_order=_lib.ptr(order))
     with torch.cuda.device(q.device):
         rc = _lib.load().tkv_fused_decode_attention(args, _lib.stream_handle(q.device))
     _lib.check(rc, "fused_decode_attention")

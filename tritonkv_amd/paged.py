@@ -29,8 +29,9 @@ import math
 import torch
 
 from . import _lib
-from .kernels.fused_decode_attn import (_aligned16, _check_out, _workspace_for, choose_waves,
-                                        new_token_args, plan_splits, triton_available)
+from .kernels.fused_decode_attn import (_aligned16, _check_out, _order_for, _workspace_for,
+                                        choose_waves, new_token_args, plan_splits,
+                                        triton_available)
 from .quantize import QuantizedTensor, _check_bits, _require_gpu, empty_cache
 
 PAGE_MULTIPLE = 32
@@ -120,6 +121,7 @@ def paged_decode_attention(
     allow_mixed_bits: bool = False,
     k_new: torch.Tensor | None = None,
     v_new: torch.Tensor | None = None,
+    dispatch_order: bool | None = None,
 ) -> torch.Tensor:
     """One decode step of attention over paged 2/4-bit K/V pools.
 
@@ -132,7 +134,7 @@ def paged_decode_attention(
     cache holding the same tokens with the same ``num_splits``.  ``k_new`` /
     ``v_new`` fuse the step's append into the same launch (the token lands at
     ``seq_lens[b] - 1``), bit-identical to :func:`paged_append` followed by
-    this call.
+    this call.  ``dispatch_order`` as for ``fused_decode_attention``.
     """
     if k_pool.group_size != v_pool.group_size or (k_pool.nbits != v_pool.nbits
                                                   and not allow_mixed_bits):
@@ -172,6 +174,7 @@ def paged_decode_attention(
     out = _check_out(out, B, HQ, D, q.device)
     acc, maxs, sums, _ = _workspace_for(_workspace, B, HQ, num_splits, D, q.device, HKV)
     lens = seq_lens.contiguous() if seq_lens is not None else None
+    order = _order_for(_workspace, B, HKV, num_splits, q.device, seq_lens, dispatch_order)
     args = _lib.DecodeArgs(
         q=q.data_ptr(), q_is_fp32=int(q.dtype == torch.float32),
         k=k_pool.packed.data_ptr(), k_scale=k_pool.scale.data_ptr(),
@@ -184,7 +187,8 @@ def paged_decode_attention(
         waves=choose_waves(B, HKV, group, split_size, num_splits, D=D, k_nbits=k_pool.nbits,
                            v_nbits=v_pool.nbits, group_size=k_pool.group_size, paged=True),
         block_table=table.data_ptr(), block_table_stride=table.shape[1], page_size=page_size,
-        num_pages=num_pages, k_new=_lib.ptr(kn), v_new=_lib.ptr(vn), new_is_fp32=new_f32)
+        num_pages=num_pages, k_new=_lib.ptr(kn), v_new=_lib.ptr(vn), new_is_fp32=new_f32,
+        work_order=_lib.ptr(order))
     with torch.cuda.device(q.device):
         rc = _lib.load().tkv_fused_decode_attention(args, _lib.stream_handle(q.device))
     _lib.check(rc, "paged_decode_attention")
