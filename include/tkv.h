@@ -116,10 +116,12 @@ typedef struct tkv_decode_args {
    * to num_splits (or 0); counters likewise. */
   int32_t split_base, num_splits_total;
   /* Dispatch order (quantized path only; NULL: the natural order).  A caller
-   * buffer of B * HKV * num_splits int32 that the call fills, with one small
-   * launch ahead of the split kernel, with a longest-piece-first order of the
-   * split workgroups: piece (b, s), tokens [s * split_size, (s + 1) *
-   * split_size) of row b, ranked by its length under seq_lens, longest first.
+   * buffer of 2 * B * HKV * num_splits int32 (8-byte aligned) that the call
+   * fills, with one small launch ahead of the split kernel, with a
+   * longest-piece-first order of the split workgroups: piece (b, s), tokens
+   * [s * split_size, (s + 1) * split_size) of row b, ranked by its length
+   * under seq_lens, longest first; each slot holds the workgroup's
+   * s * B * HKV + unit and its row's length.
    * The split kernel then takes its (unit, split) from that order, so in a
    * ragged batch the short pieces fill the end of the launch instead of a full
    * piece of a long row starting last.  Every (unit, split) still runs once and

@@ -6,7 +6,8 @@ order must be *bit-identical* to the decode without it, under every path that
 reads the order (plain, counters merge, fused append, paged, 12-wave, query
 heads in several 16-head blocks).  The order buffer itself is checked against
 a brute-force sort of the pieces: length under ``seq_lens`` descending, ties
-in the natural ``s * B + b`` order, the HKV units of a piece consecutive.
+in the natural ``s * B + b`` order, the HKV units of a piece consecutive,
+each slot carrying its row's length.
 """
 
 from __future__ import annotations
@@ -36,15 +37,16 @@ def _lengths(B, S, split_size, seed):
 
 
 def _expected_order(lens, B, HKV, num_splits, split_size, S):
+    """(s * B * HKV + unit, row length) per slot, by a sort of the pieces."""
     pieces = []
     for s in range(num_splits):
         for b in range(B):
             L = min(int(lens[b]), S)
-            pieces.append((-max(0, min(L - s * split_size, split_size)), s * B + b, s, b))
+            pieces.append((-max(0, min(L - s * split_size, split_size)), s * B + b, s, b, L))
     pieces.sort()
     out = []
-    for _, _, s, b in pieces:
-        out += [s * B * HKV + b * HKV + hk for hk in range(HKV)]
+    for _, _, s, b, L in pieces:
+        out += [(s * B * HKV + b * HKV + hk, L) for hk in range(HKV)]
     return torch.tensor(out, dtype=torch.int32)
 
 
@@ -80,7 +82,7 @@ def test_ordered_dispatch_is_bit_identical(B, HQ, HKV, S, kbits, vbits, gs, ns):
                             seq_lens=lens.to(DEV), allow_mixed_bits=True,
                             fused_combine=fused_combine)
         assert torch.equal(on, off), f"fused_combine={fused_combine}"
-        order = ws["work_order"][:B * HKV * n_s].cpu()
+        order = ws["work_order"][:2 * B * HKV * n_s].cpu().view(-1, 2)
         assert torch.equal(order, _expected_order(lens, B, HKV, n_s, split, S))
     ref = oracle_attention_on_quant(q, kq, vq, seq_lens=lens.numpy())
     assert_close_to_reference(on, ref, f"ordered K{kbits}V{vbits} gs{gs}")

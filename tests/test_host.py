@@ -96,7 +96,7 @@ def test_decode_args_layout_matches_c():
 
 
 def test_work_order_argument_checks_without_a_gpu():
-    """work_order: 4-byte aligned, slots that fit int32, quantized path only and
+    """work_order: 8-byte aligned, slots that fit int32, quantized path only and
     not with the allocation-free entry (each check returns before any launch)."""
     from tritonkv_amd import _lib
 
@@ -108,6 +108,8 @@ def test_work_order_argument_checks_without_a_gpu():
                         split_size=64, num_splits=4, waves=8, work_order=dummy + 2)
     assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
     assert lib.tkv_fused_decode_split(ctypes.byref(a), None) == _lib.TKV_EINVAL
+    a.work_order = dummy + 4  # (idx, length) pairs: 8-byte aligned
+    assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
     a.work_order = dummy
     assert lib.tkv_fp16_decode_attention(ctypes.byref(a), None) == _lib.TKV_EUNSUPPORTED
     assert lib.tkv_fp16_decode_split(ctypes.byref(a), None) == _lib.TKV_EUNSUPPORTED
@@ -123,14 +125,16 @@ def test_order_buffer_policy():
     from tritonkv_amd.kernels.fused_decode_attn import _order_for
 
     lens = object()  # only its presence matters
-    assert _order_for({}, 2, 2, 1, "cpu", lens, None) is None      # unsplit
-    assert _order_for({}, 2, 2, 4, "cpu", None, None) is None      # equal lengths
-    assert _order_for({}, 2, 2, 4, "cpu", lens, False) is None
+    assert _order_for({}, 64, 8, 1, "cpu", lens, None) is None     # unsplit
+    assert _order_for({}, 64, 8, 4, "cpu", None, None) is None     # equal lengths
+    assert _order_for({}, 64, 8, 4, "cpu", lens, False) is None
+    assert _order_for({}, 1, 2, 32, "cpu", lens, None) is None     # 64 workgroups fit the CUs
+    assert _order_for({}, 1, 2, 32, "cpu", lens, None, G=256) is not None  # 16 head blocks each
     ws = {}
-    buf = _order_for(ws, 2, 3, 4, "cpu", lens, None)
-    assert buf.dtype == torch.int32 and buf.numel() == 24 and ws["work_order"] is buf
-    assert _order_for(ws, 2, 3, 2, "cpu", lens, None) is buf       # reused when large enough
-    assert _order_for({}, 2, 3, 4, "cpu", None, True).numel() == 24
+    buf = _order_for(ws, 64, 8, 4, "cpu", lens, None)
+    assert buf.dtype == torch.int32 and buf.numel() == 4096 and ws["work_order"] is buf
+    assert _order_for(ws, 64, 8, 2, "cpu", lens, None) is buf      # reused when large enough
+    assert _order_for({}, 2, 3, 4, "cpu", None, True).numel() == 48  # forced
 
 
 def test_c_entry_points_reject_bad_arguments_without_a_gpu():

@@ -425,21 +425,36 @@ __global__ void __launch_bounds__(256) combine_window_kernel(const float* __rest
 
 // ---------------------------------------------------------------------------
 // Dispatch order of a ragged batch: one thread per piece (b, s), piece index
-// s * B + b; writes the HKV (unit, split) slots of its rank (longest piece
-// first, ragged_piece_rank).  O(B) per thread, with seq_lens read at uniform
-// addresses.  The ranks of all pieces are distinct, so order is a permutation
-// of the B * HKV * ns workgroups of the split grid.
+// s * B + b; writes the HKV (idx, L) pairs of its rank (longest piece first,
+// ragged_rank_term), idx = s * B * HKV + unit, L = min(seq_lens[b], S) as the
+// split kernel would read it.  The row lengths pass through LDS 256 at a time
+// (one coalesced load, then O(B) LDS reads per thread).  The ranks of all
+// pieces are distinct, so the pairs are a permutation of the B * HKV * ns
+// workgroups of the split grid.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256)
 ragged_order_kernel(const int32_t* __restrict__ seq_lens, int B, int S, int HKV, int ns, int ss,
                     int32_t* __restrict__ order) {
+  __shared__ int lens[256];
   const int p = blockIdx.x * 256 + threadIdx.x;
-  if (p >= B * ns) return;
-  const int s = p / B, b = p - s * B;
-  auto lens = [&](int i) { return seq_lens ? max(0, min(seq_lens[i], S)) : S; };
-  const int rank = ragged_piece_rank(b, s, B, ss, lens);
+  const bool live = p < B * ns;
+  const int s = live ? p / B : 0, b = live ? p - s * B : 0;
+  const int Lb = seq_lens ? min(seq_lens[b], S) : S;
+  const int len = max(0, min(max(Lb, 0) - s * ss, ss));
+  int rank = 0;
+  for (int base = 0; base < B; base += 256) {
+    const int n = min(256, B - base);
+    __syncthreads();  // the previous block of lengths has been read
+    if ((int)threadIdx.x < n)
+      lens[threadIdx.x] = seq_lens ? max(0, min(seq_lens[base + threadIdx.x], S)) : S;
+    __syncthreads();
+    if (live)
+      for (int j = 0; j < n; ++j) rank += ragged_rank_term(len, s, b, ss, base + j, lens[j]);
+  }
+  if (!live) return;
   const int BU = B * HKV;
-  for (int hk = 0; hk < HKV; ++hk) order[(int64_t)rank * HKV + hk] = s * BU + b * HKV + hk;
+  int2* out = reinterpret_cast<int2*>(order);
+  for (int hk = 0; hk < HKV; ++hk) out[(int64_t)rank * HKV + hk] = make_int2(s * BU + b * HKV + hk, Lb);
 }
 
 // ===========================================================================
@@ -481,7 +496,7 @@ static int validate_common(const tkv_decode_args* a) {
     if (((uintptr_t)a->k_new | (uintptr_t)a->v_new) & (a->new_is_fp32 ? 3 : 1)) return TKV_EINVAL;
   }
   if (a->work_order) {
-    if ((uintptr_t)a->work_order & 3) return TKV_EINVAL;
+    if ((uintptr_t)a->work_order & 7) return TKV_EINVAL;  // int2 pairs
     // slots hold s * B * HKV + unit as int32
     if ((int64_t)a->B * a->HKV * a->num_splits > INT32_MAX) return TKV_EINVAL;
   }

@@ -45,9 +45,11 @@ struct SplitParams {
   // This launch's splits are partial rows split_base + split of ns_total.
   int split_base, ns_total;
   // Dispatch order (quantized path), or null: workgroup i = y * gridDim.x + x
-  // of each z slice runs (unit, split) = (order[i] % gridDim.x, order[i] /
-  // gridDim.x) instead of (x, y).  A permutation, so every (unit, split) runs
-  // once and writes its own partial row: the result does not depend on it.
+  // of each z slice reads the pair order[2i], order[2i + 1] = (idx, L) and runs
+  // (unit, split) = (idx % gridDim.x, idx / gridDim.x) of a row of L tokens
+  // (min(seq_lens[b], S), carried here so the prologue's dependent loads stay
+  // one deep).  A permutation, so every (unit, split) runs once and writes its
+  // own partial row: the result does not depend on it.
   const int32_t* order;
 };
 
@@ -57,27 +59,29 @@ struct SplitParams {
 // (the natural y-major order), and the HKV units of a piece take consecutive
 // slots.  The dispatcher starts workgroups in slot order as CUs free up, so
 // the short pieces fill the gaps at the end instead of a full piece of a long
-// row starting last.  Returns the rank of piece (b, s); lens(i) gives L_i
-// already clamped to [0, S].
+// row starting last.  The rank of piece (b, s), of length len, is the sum over
+// rows b2 (length L2, clamped to [0, S]) of ragged_rank_term.
+__host__ __device__ inline int ragged_rank_term(int len, int s, int b, int ss, int b2, int L2) {
+  const int f2 = L2 / ss, r2 = L2 - f2 * ss;  // full pieces, remainder
+  const int n2 = f2 + (r2 > 0);                // non-empty pieces
+  const int before = s + (b2 < b);             // pieces s2 of row b2 with s2 * B + b2 < s * B + b
+  int t = 0;
+  if (len < ss) t += f2;                       // full pieces are longer
+  if (r2 > len) t += 1;
+  if (len == ss)
+    t += min(f2, before);
+  else if (len > 0)
+    t += (r2 == len && f2 < before);
+  else
+    t += max(0, before - n2);  // empty pieces s2 in [n2, before)
+  return t;
+}
+
 template <class Lens>
 __host__ __device__ inline int ragged_piece_rank(int b, int s, int B, int ss, Lens lens) {
-  const int Lb = lens(b);
-  const int len = max(0, min(Lb - s * ss, ss));
+  const int len = max(0, min(lens(b) - s * ss, ss));
   int rank = 0;
-  for (int b2 = 0; b2 < B; ++b2) {
-    const int L2 = lens(b2);
-    const int f2 = L2 / ss, r2 = L2 - f2 * ss;  // full pieces, remainder
-    const int n2 = f2 + (r2 > 0);                // non-empty pieces
-    const int before = s + (b2 < b);             // pieces s2 of row b2 with s2 * B + b2 < s * B + b
-    if (len < ss) rank += f2;                    // full pieces are longer
-    if (r2 > len) rank += 1;
-    if (len == ss)
-      rank += min(f2, before);
-    else if (len > 0)
-      rank += (r2 == len && f2 < before);
-    else
-      rank += max(0, before - n2);  // empty pieces s2 in [n2, before)
-  }
+  for (int b2 = 0; b2 < B; ++b2) rank += ragged_rank_term(len, s, b, ss, b2, lens(b2));
   return rank;
 }
 

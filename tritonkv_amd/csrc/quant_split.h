@@ -427,11 +427,12 @@ quant_split_lds_kernel(SplitParams prm) {
 
   // x fastest: consecutive workgroups (which the dispatcher deals to the 8 XCDs
   // in turn) take other units.  A ragged batch may pass a longest-first order.
-  int unit_ = blockIdx.x, split_ = blockIdx.y;
+  int unit_ = blockIdx.x, split_ = blockIdx.y, L_ = 0;
   if (prm.order) {
-    const int idx = prm.order[blockIdx.y * gridDim.x + blockIdx.x];
-    unit_ = idx % (int)gridDim.x;
-    split_ = idx / (int)gridDim.x;
+    const int2 e = reinterpret_cast<const int2*>(prm.order)[blockIdx.y * gridDim.x + blockIdx.x];
+    unit_ = e.x % (int)gridDim.x;
+    split_ = e.x / (int)gridDim.x;
+    L_ = e.y;
   }
   const int unit = __builtin_amdgcn_readfirstlane(unit_);
   const int split = __builtin_amdgcn_readfirstlane(split_);
@@ -439,7 +440,8 @@ quant_split_lds_kernel(SplitParams prm) {
   const int hb0 = blockIdx.z * 16;
   const int nh = min(16, prm.G - hb0);
   const int h0 = hk * prm.G + hb0;
-  const int L = prm.seq_lens ? min(prm.seq_lens[b], prm.S) : prm.S;
+  const int L = prm.order ? __builtin_amdgcn_readfirstlane(L_)
+                          : (prm.seq_lens ? min(prm.seq_lens[b], prm.S) : prm.S);
   const int lo = split * prm.split_size;
   const int hi = min(lo + prm.split_size, L);
   const int last = hi - 1;
@@ -1224,16 +1226,18 @@ __global__ void __launch_bounds__(NW * 64) read_probe_kernel(SplitParams prm) {
   constexpr int NG = SG::NG;
   constexpr int NI = SG::NINSTR;
   __shared__ __attribute__((aligned(16))) uint8_t smem[NW * 2 * SG::BYTES];
-  int unit_ = blockIdx.x, split_ = blockIdx.y;
+  int unit_ = blockIdx.x, split_ = blockIdx.y, L_ = 0;
   if (prm.order) {  // the split kernel's dispatch order
-    const int idx = prm.order[blockIdx.y * gridDim.x + blockIdx.x];
-    unit_ = idx % (int)gridDim.x;
-    split_ = idx / (int)gridDim.x;
+    const int2 e = reinterpret_cast<const int2*>(prm.order)[blockIdx.y * gridDim.x + blockIdx.x];
+    unit_ = e.x % (int)gridDim.x;
+    split_ = e.x / (int)gridDim.x;
+    L_ = e.y;
   }
   const int unit = __builtin_amdgcn_readfirstlane(unit_);
   const int split = __builtin_amdgcn_readfirstlane(split_);
   const int b = unit / prm.HKV;
-  const int L = prm.seq_lens ? min(prm.seq_lens[b], prm.S) : prm.S;
+  const int L = prm.order ? __builtin_amdgcn_readfirstlane(L_)
+                          : (prm.seq_lens ? min(prm.seq_lens[b], prm.S) : prm.S);
   const int lo = split * prm.split_size;
   const int hi = min(lo + prm.split_size, L);
   const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6), lane = threadIdx.x & 63;

@@ -238,19 +238,27 @@ def _workspace_for(ws: dict | None, B: int, HQ: int, num_splits: int, D: int, de
 
 
 def _order_for(ws: dict | None, B: int, HKV: int, num_splits: int, device, seq_lens,
-               dispatch_order: bool | None):
+               dispatch_order: bool | None, G: int = 1):
     """The ``work_order`` buffer of a split call, or None.
 
-    ``dispatch_order=None`` takes it whenever ``seq_lens`` is given and the
-    history is split: the call then runs the split workgroups longest piece
-    first (``ragged_order_kernel``), which evens out the end of the launch when
-    rows differ in length (B=64, HKV=8, lengths U[1k, 128k], K4/V2).  The
-    output is bit-identical either way; ``False`` keeps the natural order.
+    ``dispatch_order=None`` takes it when ``seq_lens`` is given, the history
+    is split and the grid holds more workgroups than the GPU has compute
+    units: the call then runs the split workgroups longest piece first
+    (``ragged_order_kernel``), which evens out the end of the launch when rows
+    differ in length (B=64, HKV=8, lengths U[1k, 128k], K4/V2: decode 715 ->
+    676 us).  A grid that fits the CUs at once has no tail to even out, and
+    the order would only add its launch (~1.6 us, a fifth of a batch-1 step).
+    The output is bit-identical either way; ``True`` forces the order,
+    ``False`` keeps the grid order.
     """
-    if num_splits <= 1 or dispatch_order is False or (dispatch_order is None and seq_lens is None):
+    if num_splits <= 1 or dispatch_order is False:
         return None
+    if dispatch_order is None:
+        workgroups = B * HKV * _cdiv(G, 16) * num_splits
+        if seq_lens is None or workgroups <= (compute_units(device) or 256):
+            return None
     ws = ws if ws is not None else {}
-    n = B * HKV * num_splits
+    n = 2 * B * HKV * num_splits  # (s * B * HKV + unit, row length) pairs
     buf = ws.get("work_order")
     if buf is None or buf.numel() < n or buf.device != torch.device(device):
         buf = torch.empty(n, device=device, dtype=torch.int32)
@@ -403,7 +411,7 @@ def fused_decode_attention(
     out = _check_out(out, B, HQ, D, q.device)
     acc, maxs, sums, counters = _workspace_for(_workspace, B, HQ, num_splits, D, q.device, HKV)
     lens = _seq_lens_arg(seq_lens, B, S, q.device)
-    order = _order_for(_workspace, B, HKV, num_splits, q.device, seq_lens, dispatch_order)
+    order = _order_for(_workspace, B, HKV, num_splits, q.device, seq_lens, dispatch_order, group)
 
     args = _lib.DecodeArgs(
         q=q.data_ptr(), q_is_fp32=int(q.dtype == torch.float32),
