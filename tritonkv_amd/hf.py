@@ -162,10 +162,12 @@ class TkvLayer(_LayerBase):
             out = fp16_decode_attention(q, self.kc, self.vc, sm_scale=scaling, out=self.out,
                                         _workspace=self.workspace, seq_lens=self.lens)
         else:
+            # every row holds the same length: no uneven tail for a dispatch order to fix
             out = fused_decode_attention(q, self.kc, self.vc, sm_scale=scaling, out=self.out,
                                          _workspace=self.workspace, seq_lens=self.lens,
                                          k_new=key[:, :, 0].to(torch.float16),
-                                         v_new=value[:, :, 0].to(torch.float16))
+                                         v_new=value[:, :, 0].to(torch.float16),
+                                         dispatch_order=False)
         return out.to(query.dtype).view(B, 1, HQ, D)
 
 
