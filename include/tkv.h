@@ -125,8 +125,8 @@ typedef struct tkv_decode_args {
    * The split kernel then takes its (unit, split) from that order, so in a
    * ragged batch the short pieces fill the end of the launch instead of a full
    * piece of a long row starting last.  Every (unit, split) still runs once and
-   * writes its own partial row, so out is bit-identical to work_order == NULL.
-   * Unused when num_splits == 1; the fp16 path returns TKV_EUNSUPPORTED and
+   * writes its own partial row (or, unsplit, its own rows of out), so out is
+   * bit-identical to work_order == NULL.  The fp16 path returns TKV_EUNSUPPORTED and
    * the _noalloc entry TKV_EINVAL for a non-NULL work_order.  No counterpart
    * in the reference (its Triton grid runs splits in program-id order). */
   int32_t *work_order;

@@ -64,6 +64,7 @@ def _both(fn, **kw):
     (9, 64, 8, 2048, 4, 2, 32, 3),    # the 70B-style format, G = 8
     (5, 32, 1, 3072, 4, 4, 128, 5),   # G = 32: two blocks of 16 query heads
     (16, 8, 2, 1024, 2, 2, 128, None),
+    (10, 16, 4, 2048, 4, 2, 32, 1),   # unsplit: whole rows in order, out written directly
 ])
 def test_ordered_dispatch_is_bit_identical(B, HQ, HKV, S, kbits, vbits, gs, ns):
     from tritonkv_amd.kernels import fused_decode_attention
@@ -75,7 +76,7 @@ def test_ordered_dispatch_is_bit_identical(B, HQ, HKV, S, kbits, vbits, gs, ns):
     q, k, v, kq, _ = make_case(B, HQ, HKV, 128, S, kbits, gs, seed=B + S)
     vq = quantize_groupwise(v, vbits, gs)
     _, n_s, split = plan_splits(S, 64, ns, B, HKV, HQ // HKV, ragged=True)
-    assert n_s > 1
+    assert (n_s > 1) == (ns != 1)
     lens = _lengths(B, S, split, seed=S + 3)
     for fused_combine in (False, True):
         on, off, ws = _both(fused_decode_attention, q=q, kq=kq, vq=vq, num_splits=ns,

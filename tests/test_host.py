@@ -125,7 +125,8 @@ def test_order_buffer_policy():
     from tritonkv_amd.kernels.fused_decode_attn import _order_for
 
     lens = object()  # only its presence matters
-    assert _order_for({}, 64, 8, 1, "cpu", lens, None) is None     # unsplit
+    assert _order_for({}, 32, 8, 1, "cpu", lens, None) is None     # 256 workgroups: one per CU
+    assert _order_for({}, 64, 8, 1, "cpu", lens, None).numel() == 1024  # unsplit, 512 workgroups
     assert _order_for({}, 64, 8, 4, "cpu", None, None) is None     # equal lengths
     assert _order_for({}, 64, 8, 4, "cpu", lens, False) is None
     assert _order_for({}, 1, 2, 32, "cpu", lens, None) is None     # 64 workgroups fit the CUs

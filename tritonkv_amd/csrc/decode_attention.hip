@@ -637,7 +637,7 @@ static int launch_fused_split(const tkv_decode_args* a, hipStream_t st, bool pro
   SplitParams p = make_params(a);
   const dim3 grid = split_grid(a);
   (void)hipGetLastError();
-  if (a->work_order && a->num_splits > 1) {
+  if (a->work_order) {
     const int pieces = a->B * a->num_splits;
     ragged_order_kernel<<<dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, st>>>(
         a->seq_lens, a->B, a->S, a->HKV, a->num_splits, a->split_size, a->work_order);

@@ -241,9 +241,8 @@ def _order_for(ws: dict | None, B: int, HKV: int, num_splits: int, device, seq_l
                dispatch_order: bool | None, G: int = 1):
     """The ``work_order`` buffer of a split call, or None.
 
-    ``dispatch_order=None`` takes it when ``seq_lens`` is given, the history
-    is split and the grid holds more workgroups than the GPU has compute
-    units: the call then runs the split workgroups longest piece first
+    ``dispatch_order=None`` takes it when ``seq_lens`` is given and the grid
+    holds more workgroups than the GPU has compute units: the call then runs the split workgroups longest piece first
     (``ragged_order_kernel``), which evens out the end of the launch when rows
     differ in length (B=64, HKV=8, lengths U[1k, 128k], K4/V2: decode 715 ->
     676 us).  A grid that fits the CUs at once has no tail to even out, and
@@ -251,7 +250,7 @@ def _order_for(ws: dict | None, B: int, HKV: int, num_splits: int, device, seq_l
     The output is bit-identical either way; ``True`` forces the order,
     ``False`` keeps the grid order.
     """
-    if num_splits <= 1 or dispatch_order is False:
+    if dispatch_order is False:
         return None
     if dispatch_order is None:
         workgroups = B * HKV * _cdiv(G, 16) * num_splits
