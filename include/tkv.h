@@ -126,7 +126,8 @@ typedef struct tkv_decode_args {
    * ragged batch the short pieces fill the end of the launch instead of a full
    * piece of a long row starting last.  Every (unit, split) still runs once and
    * writes its own partial row (or, unsplit, its own rows of out), so out is
-   * bit-identical to work_order == NULL.  The fp16 path returns TKV_EUNSUPPORTED and
+   * bit-identical to work_order == NULL.  The order launch costs O(B) per
+   * piece (B * num_splits pieces).  The fp16 path returns TKV_EUNSUPPORTED and
    * the _noalloc entry TKV_EINVAL for a non-NULL work_order.  No counterpart
    * in the reference (its Triton grid runs splits in program-id order). */
   int32_t *work_order;

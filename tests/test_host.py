@@ -131,6 +131,7 @@ def test_order_buffer_policy():
     assert _order_for({}, 64, 8, 4, "cpu", lens, False) is None
     assert _order_for({}, 1, 2, 32, "cpu", lens, None) is None     # 64 workgroups fit the CUs
     assert _order_for({}, 1, 2, 32, "cpu", lens, None, G=256) is not None  # 16 head blocks each
+    assert _order_for({}, 4096, 8, 1, "cpu", lens, None) is None   # past ORDER_MAX_ROWS
     ws = {}
     buf = _order_for(ws, 64, 8, 4, "cpu", lens, None)
     assert buf.dtype == torch.int32 and buf.numel() == 4096 and ws["work_order"] is buf

@@ -237,6 +237,12 @@ def _workspace_for(ws: dict | None, B: int, HQ: int, num_splits: int, D: int, de
     return ws["acc"], ws["maxs"], ws["sums"], cnt
 
 
+# The order kernel ranks each piece against every row (O(B) per piece), so
+# the automatic order stops at this many rows; past it the many short jobs
+# even out the tail by themselves.
+ORDER_MAX_ROWS = 2048
+
+
 def _order_for(ws: dict | None, B: int, HKV: int, num_splits: int, device, seq_lens,
                dispatch_order: bool | None, G: int = 1):
     """The ``work_order`` buffer of a split call, or None.
@@ -246,7 +252,8 @@ def _order_for(ws: dict | None, B: int, HKV: int, num_splits: int, device, seq_l
     (``ragged_order_kernel``), which evens out the end of the launch when rows
     differ in length (B=64, HKV=8, lengths U[1k, 128k], K4/V2: decode 715 ->
     676 us).  A grid that fits the CUs at once has no tail to even out, and
-    the order would only add its launch (~1.6 us, a fifth of a batch-1 step).
+    the order would only add its launch (~1.6 us, a fifth of a batch-1 step);
+    past ``ORDER_MAX_ROWS`` rows neither does it.
     The output is bit-identical either way; ``True`` forces the order,
     ``False`` keeps the grid order.
     """
@@ -254,7 +261,8 @@ def _order_for(ws: dict | None, B: int, HKV: int, num_splits: int, device, seq_l
         return None
     if dispatch_order is None:
         workgroups = B * HKV * _cdiv(G, 16) * num_splits
-        if seq_lens is None or workgroups <= (compute_units(device) or 256):
+        if seq_lens is None or workgroups <= (compute_units(device) or 256) \
+                or B > ORDER_MAX_ROWS:
             return None
     ws = ws if ws is not None else {}
     n = 2 * B * HKV * num_splits  # (s * B * HKV + unit, row length) pairs
