@@ -156,3 +156,32 @@ def test_ordered_dispatch_paged_and_twelve_waves():
     assert torch.equal(on, off)
     contiguous = fused_decode_attention(q, kq, vq, num_splits=ns, seq_lens=lens)
     assert torch.equal(on, contiguous)
+
+
+@pytest.mark.parametrize("ns", [1, 3])
+def test_ordered_dispatch_with_empty_and_overlong_rows(ns):
+    """Rows of length 0 and lengths past the cache's capacity reach the split
+    kernel as the same L either way (the order's slots carry min(len, S)), so
+    whatever those rows produce, both orders produce it bit for bit."""
+    from tritonkv_amd.kernels import fused_decode_attention
+    from tritonkv_amd.kernels.fused_decode_attn import plan_splits
+
+    B, HQ, HKV, S = 20, 16, 4, 2048
+    print(f"ordered dispatch empty/overlong rows B={B} S={S} ns={ns}", flush=True)
+    q, k, v, kq, vq = make_case(B, HQ, HKV, 128, S, 4, 32, seed=41)
+    _, n_s, split = plan_splits(S, 64, ns, B, HKV, HQ // HKV, ragged=True)
+    lens = _lengths(B, S, split, seed=12)
+    lens[5] = 0
+    lens[6] = S + 1000
+    lens[7] = 0
+    on, off, ws = _both(fused_decode_attention, q=q, kq=kq, vq=vq, num_splits=ns,
+                        seq_lens=lens.to(DEV))
+    torch.testing.assert_close(on, off, rtol=0, atol=0, equal_nan=True)
+    order = ws["work_order"][:2 * B * HKV * n_s].cpu().view(-1, 2)
+    assert torch.equal(order, _expected_order(lens, B, HKV, n_s, split, S))
+    keep = [i for i in range(B) if i not in (5, 7)]
+    kd = torch.tensor(keep, device=DEV)
+    sub = [type(t)(t.packed[kd], t.scale[kd], t.zero[kd], 4, 32, 128) for t in (kq, vq)]
+    ref = oracle_attention_on_quant(q[kd], sub[0], sub[1],
+                                    seq_lens=lens[keep].clamp(max=S).numpy())
+    assert_close_to_reference(on[kd], ref, f"ordered rows with empty neighbours ns={ns}")
