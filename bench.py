@@ -86,6 +86,10 @@ def _args():
     ap.add_argument("--regime-probe", choices=("hot", "cold"), default=None,
                     help="no timing: 60 eager Qwen2.5-1.5B ctx-16384 4-bit decode calls on one "
                          "cache (hot) or rotating copies >= 768 MB (cold), for rocprofv3 --pmc")
+    ap.add_argument("--order-sweep", action="store_true",
+                    help="the dispatch-order measurements: the 70B-style ragged batch's decode "
+                         "and read probe at 1-16 splits in grid and longest-first order, and "
+                         "the Llama-3-8B step with equal lengths passed as seq_lens")
     ap.add_argument("--qwen-trace", type=int, metavar="CTX", default=None,
                     help="no timing: 200 eager hot decode calls each of the fused 4-bit, fused "
                          "2-bit and fp16 control paths at the Qwen2.5-1.5B shape and context "
@@ -1036,6 +1040,80 @@ def counter_summary(dirs) -> int:
     return 0
 
 
+def order_sweep(steps=30, warmup=200):
+    """Longest-piece-first dispatch order against the grid order (one JSON line).
+
+    * the 70B-style ragged batch of ``ragged_70b`` (K4/V2, lengths U[1024,
+      131072], seed 2024): decode and ``tkv_read_probe`` at 1, 2, 3, 4, 6, 8
+      and 16 splits per row, each in both orders;
+    * the Llama-3-8B step (4-bit gs32, B=32, ctx 32768) with every length
+      passed as ``seq_lens``: grid order, the order, and no ``seq_lens``."""
+    import torch
+
+    from tritonkv_amd import _lib, synthetic
+    from tritonkv_amd.kernels import fused_decode_attention
+    from tritonkv_amd.kernels.fused_decode_attn import _workspace_for, plan_splits
+    from tritonkv_amd.quantize import quantize_groupwise
+
+    B, HQ, HKV, D, gs, S = 64, 64, 8, 128, 32, 131072 + 64
+    lens = synthetic.ragged_lengths(B, 1024, 131072, seed=2024)
+    q, kc, vc, _, _ = synthetic.ragged_batch(B, HQ, HKV, D, lens, S, 4, 2, gs, seed=2024)
+    lens1 = (lens + 1).to("cuda")
+    out = torch.empty(B, HQ, D, device="cuda")
+    lib = _lib.load()
+    rows = []
+    for ns in (1, 2, 3, 4, 6, 8, 16):
+        _, n, size = plan_splits(S, 64, ns, B, HKV, HQ // HKV, ragged=True)
+        acc, mx, sm, _ = _workspace_for({}, B, HQ, n, D, q.device, HKV)
+        order = torch.empty(2 * B * HKV * n, dtype=torch.int32, device="cuda")
+        row = {"splits": n, "split_size": size}
+        for use in (False, True):
+            ws = {}
+
+            def decode():
+                fused_decode_attention(q, kc, vc, seq_lens=lens1, allow_mixed_bits=True,
+                                       out=out, _workspace=ws, num_splits=ns,
+                                       dispatch_order=use)
+            args = _lib.DecodeArgs(
+                q=q.data_ptr(), k=kc.packed.data_ptr(), k_scale=kc.scale.data_ptr(),
+                k_zero=kc.zero.data_ptr(), v=vc.packed.data_ptr(), v_scale=vc.scale.data_ptr(),
+                v_zero=vc.zero.data_ptr(), seq_lens=lens1.data_ptr(), acc=_lib.ptr(acc),
+                maxs=_lib.ptr(mx), sums=_lib.ptr(sm), out=out.data_ptr(), B=B, HQ=HQ, HKV=HKV,
+                S=S, D=D, k_nbits=4, v_nbits=2, group_size=gs, sm_scale=D ** -0.5,
+                split_size=size, num_splits=n, waves=8,
+                work_order=order.data_ptr() if use else None)
+
+            def probe(args=args):
+                _lib.check(lib.tkv_read_probe(args, torch.cuda.current_stream().cuda_stream),
+                           "tkv_read_probe")
+            key = "longest_first" if use else "grid"
+            row[key + "_decode_us"] = round(timed_steps([decode], steps, warmup)[0], 1)
+            row[key + "_probe_us"] = round(timed_steps([probe], steps, warmup)[0], 1)
+        print(f"# ragged 70b {json.dumps(row)}", file=sys.stderr, flush=True)
+        rows.append(row)
+    del q, kc, vc, out
+    torch.cuda.empty_cache()
+
+    Bq, HQq, Sq = 32, 32, 32768
+    g = torch.Generator(device="cuda").manual_seed(7)
+    qq = torch.randn(Bq, HQq, D, device="cuda", generator=g).half()
+    kq = quantize_groupwise(torch.randn(Bq, HKV, Sq, D, device="cuda", generator=g).half(), 4, gs)
+    vq = quantize_groupwise(torch.randn(Bq, HKV, Sq, D, device="cuda", generator=g).half(), 4, gs)
+    eq = torch.full((Bq,), Sq, dtype=torch.int32, device="cuda")
+    outq = torch.empty(Bq, HQq, D, device="cuda")
+    equal = {}
+    for name, kw in (("no_seq_lens", {}), ("seq_lens_grid_order", dict(seq_lens=eq, dispatch_order=False)),
+                     ("seq_lens_longest_first", dict(seq_lens=eq))):
+        ws = {}
+
+        def step(kw=kw, ws=ws):
+            fused_decode_attention(qq, kq, vq, out=outq, _workspace=ws, **kw)
+        equal[name + "_us"] = round(timed_steps([step], steps, warmup)[0], 1)
+    print(f"# llama equal lengths {json.dumps(equal)}", file=sys.stderr, flush=True)
+    print(json.dumps({"order_sweep": {"ragged_70b_k4v2": rows, "llama3_8b_equal_lengths": equal}}))
+    return 0
+
+
 def regime_probe(mode):
     """Eager decode calls at the Qwen2.5-1.5B shape, ctx 16384, 4-bit gs32, on one
     cache ('hot') or on rotating copies totalling >= 768 MB ('cold')."""
@@ -1101,6 +1179,8 @@ def main() -> int:
         return regime_probe(a.regime_probe)
     if a.qwen_trace:
         return qwen_trace(a.qwen_trace)
+    if a.order_sweep:
+        return order_sweep()
     if a.compare:
         return compare(a.compare)
     global MIN_WARMUP_S

@@ -134,10 +134,13 @@ def default_num_splits(B: int, HKV: int, G: int, S: int, block_n: int,
     unit and a history of at least 16384 tokens is cut into pieces of at most
     32768 tokens, and at least two: rows of very different lengths make one
     workgroup per unit finish unevenly, and shorter pieces even that out.
-    B=64, HKV=8, lengths U[1k, 128k], K4/V2: 875 us unsplit, 736 us at 2
-    splits, 718 us at 4 (a split past a row's end leaves at once), 725 us at
-    8.  Two splits cost nothing when the lengths are equal (Llama-3-8B shape:
-    208.7 vs 209.2 us).
+    B=64, HKV=8, lengths U[1k, 128k], K4/V2, in grid order: 823 us unsplit,
+    746 us at 2 splits, 733 us at 4 (a split past a row's end leaves at
+    once), 743 us at 8; run longest piece first (``_order_for``), 672, 683,
+    699 and 715 us.  The cap stays because the host cannot see the lengths:
+    a few full-length rows among many short ones would each sit on one CU
+    unsplit.  Equal lengths pay for the second split (Llama-3-8B shape:
+    206.6 vs 200.7 us).
 
     Returned in units of ``block_n`` blocks so the reference's tightening
     applies unchanged.
