@@ -427,29 +427,48 @@ __global__ void __launch_bounds__(256) combine_window_kernel(const float* __rest
 // Dispatch order of a ragged batch: one thread per piece (b, s), piece index
 // s * B + b; writes the HKV (idx, L) pairs of its rank (longest piece first,
 // ragged_rank_term), idx = s * B * HKV + unit, L = min(seq_lens[b], S) as the
-// split kernel would read it.  The row lengths pass through LDS 256 at a time
-// (one coalesced load, then O(B) LDS reads per thread).  The ranks of all
-// pieces are distinct, so the pairs are a permutation of the B * HKV * ns
-// workgroups of the split grid.
+// split kernel would read it.  The rows pass through LDS 256 at a time as
+// (full pieces, remainder), one division per row per workgroup, so each
+// thread's O(B) sum is compares and adds.  The ranks of all pieces are
+// distinct, so the pairs are a permutation of the B * HKV * ns workgroups of
+// the split grid.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256)
 ragged_order_kernel(const int32_t* __restrict__ seq_lens, int B, int S, int HKV, int ns, int ss,
                     int32_t* __restrict__ order) {
-  __shared__ int lens[256];
+  __shared__ int2 rows[256];  // (full pieces, remainder) of each row
   const int p = blockIdx.x * 256 + threadIdx.x;
   const bool live = p < B * ns;
   const int s = live ? p / B : 0, b = live ? p - s * B : 0;
   const int Lb = seq_lens ? min(seq_lens[b], S) : S;
-  const int len = max(0, min(max(Lb, 0) - s * ss, ss));
+  auto stage = [&](int base) -> int2 {  // this thread's row of the block at base
+    int2 r = make_int2(0, 0);
+    if (base + (int)threadIdx.x < B) {
+      const int L2 = seq_lens ? max(0, min(seq_lens[base + threadIdx.x], S)) : S;
+      const int f2 = L2 / ss;
+      r = make_int2(f2, L2 - f2 * ss);
+    }
+    return r;
+  };
   int rank = 0;
+  // The first block is staged outside the loop, so its load and Lb's share one wait.
+  int2 mine = stage(0);
   for (int base = 0; base < B; base += 256) {
     const int n = min(256, B - base);
-    __syncthreads();  // the previous block of lengths has been read
-    if ((int)threadIdx.x < n)
-      lens[threadIdx.x] = seq_lens ? max(0, min(seq_lens[base + threadIdx.x], S)) : S;
+    if (base) {
+      __syncthreads();  // the previous block of rows has been read
+      mine = stage(base);
+    }
+    rows[threadIdx.x] = mine;
     __syncthreads();
-    if (live)
-      for (int j = 0; j < n; ++j) rank += ragged_rank_term(len, s, b, ss, base + j, lens[j]);
+    const int len = max(0, min(max(Lb, 0) - s * ss, ss));
+    if (live) {
+#pragma unroll 4
+      for (int j = 0; j < n; ++j) {
+        const int2 r = rows[j];
+        rank += ragged_rank_term(len, s, b, ss, base + j, r.x, r.y);
+      }
+    }
   }
   if (!live) return;
   const int BU = B * HKV;

@@ -60,28 +60,29 @@ struct SplitParams {
 // slots.  The dispatcher starts workgroups in slot order as CUs free up, so
 // the short pieces fill the gaps at the end instead of a full piece of a long
 // row starting last.  The rank of piece (b, s), of length len, is the sum over
-// rows b2 (length L2, clamped to [0, S]) of ragged_rank_term.
-__host__ __device__ inline int ragged_rank_term(int len, int s, int b, int ss, int b2, int L2) {
-  const int f2 = L2 / ss, r2 = L2 - f2 * ss;  // full pieces, remainder
-  const int n2 = f2 + (r2 > 0);                // non-empty pieces
-  const int before = s + (b2 < b);             // pieces s2 of row b2 with s2 * B + b2 < s * B + b
-  int t = 0;
-  if (len < ss) t += f2;                       // full pieces are longer
-  if (r2 > len) t += 1;
-  if (len == ss)
-    t += min(f2, before);
-  else if (len > 0)
-    t += (r2 == len && f2 < before);
-  else
-    t += max(0, before - n2);  // empty pieces s2 in [n2, before)
-  return t;
+// rows b2 of ragged_rank_term, where row b2 (length clamped to [0, S]) holds
+// f2 full pieces and a remainder of r2 tokens (divided once per row, so the
+// sum itself needs no division).
+__host__ __device__ inline int ragged_rank_term(int len, int s, int b, int ss, int b2, int f2,
+                                                int r2) {
+  // Selects, not branches: len differs from lane to lane.
+  const int n2 = f2 + (r2 > 0 ? 1 : 0);     // non-empty pieces
+  const int before = s + (b2 < b ? 1 : 0);  // pieces s2 of row b2 with s2 * B + b2 < s * B + b
+  const int longer = (len < ss ? f2 : 0) + (r2 > len ? 1 : 0);  // full pieces, a longer remainder
+  const int tie_full = min(f2, before);
+  const int tie_rem = (r2 == len && f2 < before) ? 1 : 0;
+  const int tie_empty = max(0, before - n2);  // empty pieces s2 in [n2, before)
+  return longer + (len == ss ? tie_full : (len > 0 ? tie_rem : tie_empty));
 }
 
 template <class Lens>
 __host__ __device__ inline int ragged_piece_rank(int b, int s, int B, int ss, Lens lens) {
   const int len = max(0, min(lens(b) - s * ss, ss));
   int rank = 0;
-  for (int b2 = 0; b2 < B; ++b2) rank += ragged_rank_term(len, s, b, ss, b2, lens(b2));
+  for (int b2 = 0; b2 < B; ++b2) {
+    const int L2 = lens(b2), f2 = L2 / ss;
+    rank += ragged_rank_term(len, s, b, ss, b2, f2, L2 - f2 * ss);
+  }
   return rank;
 }
 
