@@ -240,9 +240,8 @@ def _workspace_for(ws: dict | None, B: int, HQ: int, num_splits: int, D: int, de
     return ws["acc"], ws["maxs"], ws["sums"], cnt
 
 
-# The order kernel ranks each piece against every row (O(B) per piece), so
-# the automatic order stops at this many rows; past it the many short jobs
-# even out the tail by themselves.
+# The order kernel ranks each piece against every row (O(B) per piece, so
+# O(B^2 * num_splits) in all); the automatic order stops at this many rows.
 ORDER_MAX_ROWS = 2048
 
 
@@ -250,15 +249,16 @@ def _order_for(ws: dict | None, B: int, HKV: int, num_splits: int, device, seq_l
                dispatch_order: bool | None, G: int = 1):
     """The ``work_order`` buffer of a split call, or None.
 
-    ``dispatch_order=None`` takes it when ``seq_lens`` is given and the grid
-    holds more workgroups than the GPU has compute units: the call then runs the split workgroups longest piece first
-    (``ragged_order_kernel``), which evens out the end of the launch when rows
-    differ in length (B=64, HKV=8, lengths U[1k, 128k], K4/V2: decode 715 ->
-    676 us).  A grid that fits the CUs at once has no tail to even out, and
-    the order would only add its launch (~1.6 us, a fifth of a batch-1 step);
-    past ``ORDER_MAX_ROWS`` rows neither does it.
-    The output is bit-identical either way; ``True`` forces the order,
-    ``False`` keeps the grid order.
+    ``dispatch_order=None`` takes it when ``seq_lens`` is given, the batch
+    has at most ``ORDER_MAX_ROWS`` rows and the grid holds more workgroups
+    than the GPU has compute units: the call then runs the split workgroups
+    longest piece first (``ragged_order_kernel``), which evens out the end of
+    the launch when rows differ in length (B=64, HKV=8, lengths U[1k, 128k],
+    K4/V2: decode 711-720 -> 669-671 us).  A grid that fits the CUs at once
+    has no tail to even out, and the order would only add its launch
+    boundary (4.7-7.7 us measured ahead of the split kernel).  The output is
+    bit-identical either way; ``True`` forces the order, ``False`` keeps the
+    grid order.
     """
     if dispatch_order is False:
         return None
