@@ -111,6 +111,9 @@ def test_work_order_argument_checks_without_a_gpu():
     a.work_order = dummy + 4  # (idx, length) pairs: 8-byte aligned
     assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
     a.work_order = dummy
+    a.group_size = 8  # not instantiated: refused before the order launch as well
+    assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EUNSUPPORTED
+    a.group_size = 32
     assert lib.tkv_fp16_decode_attention(ctypes.byref(a), None) == _lib.TKV_EUNSUPPORTED
     assert lib.tkv_fp16_decode_split(ctypes.byref(a), None) == _lib.TKV_EUNSUPPORTED
     a.acc = a.maxs = a.sums = None

@@ -653,6 +653,8 @@ static int launch_fused_split(const tkv_decode_args* a, hipStream_t st, bool pro
   if ((a->k_nbits != 2 && a->k_nbits != 4) || (a->v_nbits != 2 && a->v_nbits != 4))
     return TKV_EINVAL;
   if (a->key_block && gs > 32) return TKV_EUNSUPPORTED;  // per-channel keys: V groups of 16 or 32
+  // the instantiated group sizes (dispatch_gs), checked before anything is launched
+  if (gs != 16 && gs != 32 && gs != 64 && gs != 128) return TKV_EUNSUPPORTED;
   SplitParams p = make_params(a);
   const dim3 grid = split_grid(a);
   (void)hipGetLastError();
