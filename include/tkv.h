@@ -31,7 +31,8 @@ typedef struct ihipStream_t *tkv_stream_t; /* == hipStream_t */
 enum {
   TKV_OK = 0,
   TKV_EINVAL = -1,       /* inconsistent or out-of-range argument */
-  TKV_EUNSUPPORTED = -2, /* valid but not compiled: D, nbits, group size combination */
+  TKV_EUNSUPPORTED = -2, /* valid but not compiled: D, nbits, group size combination,
+                            or a cache block past the 32-bit buffer range (below) */
   TKV_ENODEVICE = -3,    /* no HIP device visible */
   TKV_ESCRATCH = -4      /* split partials larger than TKV_NOALLOC_SCRATCH_BYTES */
 };
@@ -44,6 +45,16 @@ enum {
 /* Arguments of one decode step.  For the quantized path k/v are the packed
  * codes and k_scale/k_zero/v_scale/v_zero the fp16 metadata; for the fp16
  * control path k/v are fp16 (B, HKV, S, D) and the metadata pointers are unused.
+ *
+ * Buffer range limit: the split kernels address each (b, kv-head) block of a
+ * tensor -- each (page, kv-head) slab of a paged pool -- through a buffer
+ * resource with a 32-bit byte range, so one block must span less than 2^32
+ * bytes: rows * D * nbits / 8 (codes) and rows * (D / group_size) * 2 (scale,
+ * zero) on the quantized path, rows * D * 2 on the fp16 control, with rows = S
+ * (page_size for a paged pool).  Larger blocks return TKV_EUNSUPPORTED before
+ * anything is launched (e.g. 4-bit at D = 128: S < 2^26; the fp16 control at
+ * D = 128: S < 2^24).  The quantize / append entry points use 64-bit offsets
+ * and have no such limit.
  *
  * S is the token capacity of each (b, kv-head) block.  If seq_lens is NULL every
  * row attends to all S tokens; otherwise row b attends to its first seq_lens[b]

@@ -62,13 +62,16 @@ def quantize_keys_per_channel(x: np.ndarray, nbits: int, block: int = BLOCK) -> 
     xt = np.swapaxes(np.asarray(x).reshape(*lead, nb, block, D), -1, -2)
     qmax = (1 << nbits) - 1
     xf = xt.astype(np.float32)
-    gmin = xf.min(axis=-1)
-    gmax = xf.max(axis=-1)
-    scale = (gmax - gmin) / np.float32(qmax)
-    scale = np.where(scale > 0, scale, np.float32(1.0)).astype(np.float32)
-    scale16 = scale.astype(np.float16)
-    zero16 = gmin.astype(np.float16)
-    with np.errstate(invalid="ignore", divide="ignore"):
+    with np.errstate(invalid="ignore", over="ignore"):
+        gmin = xf.min(axis=-1)  # NaN-propagating, as torch's amin / amax
+        gmax = xf.max(axis=-1)
+        scale = (gmax - gmin) / np.float32(qmax)
+        scale = np.where(scale > 0, scale, np.float32(1.0)).astype(np.float32)
+        scale16 = scale.astype(np.float16)
+        zero16 = gmin.astype(np.float16)
+    # a NaN channel's zero is the canonical fp16 NaN, as in oracle.quant
+    zero16 = np.where(np.isnan(gmin), np.uint16(0x7E00).view(np.float16), zero16)
+    with np.errstate(invalid="ignore", divide="ignore", over="ignore"):
         codes = np.rint((xf - zero16.astype(np.float32)[..., None])
                         / scale16.astype(np.float32)[..., None])
     codes = np.where(np.isnan(codes), np.float32(0.0), codes)

@@ -96,18 +96,25 @@ def quantize_groupwise(x: np.ndarray, nbits: int, group_size: int) -> QuantNP:
     ng = D // group_size
 
     xg = np.asarray(x).astype(np.float32).reshape(*x.shape[:-1], ng, group_size)
-    gmin = xg.min(axis=-1)
-    gmax = xg.max(axis=-1)
-    scale = (gmax - gmin) / np.float32(qmax)
-    scale = np.where(scale > 0, scale, np.float32(1.0)).astype(np.float32)
-    scale16 = scale.astype(np.float16)
-    zero16 = gmin.astype(np.float16)
+    # numpy's min/max propagate a NaN, as torch's amin/amax do (quantize.py:209-210)
+    with np.errstate(invalid="ignore", over="ignore"):
+        gmin = xg.min(axis=-1)
+        gmax = xg.max(axis=-1)
+        scale = (gmax - gmin) / np.float32(qmax)
+        scale = np.where(scale > 0, scale, np.float32(1.0)).astype(np.float32)
+        scale16 = scale.astype(np.float16)
+        zero16 = gmin.astype(np.float16)
+    # torch's amin returns the canonical quiet NaN whatever the NaN's sign or
+    # payload (golden cases nan_one_*, f32_range_*), so a NaN group's zero is
+    # fp16 0x7E00; numpy would keep the sign and payload bits.
+    zero16 = np.where(np.isnan(gmin), np.uint16(0x7E00).view(np.float16), zero16)
     scale_f = scale16.astype(np.float32)
     zero_f = zero16.astype(np.float32)
-    with np.errstate(invalid="ignore", divide="ignore"):
+    with np.errstate(invalid="ignore", divide="ignore", over="ignore"):
         codes = np.rint((xg - zero_f[..., None]) / scale_f[..., None])
     # A scale that rounds to fp16 zero makes 0/0 = NaN (torch.clamp keeps it and the
     # uint8 cast then yields 0 -- pinned by the golden vectors) and c/0 = +inf -> qmax.
+    # The same holds for a NaN zero, inf/inf and (inf - inf): code 0.
     codes = np.where(np.isnan(codes), np.float32(0.0), codes)
     codes = np.clip(codes, 0, qmax).astype(np.uint8).reshape(*x.shape[:-1], D)
     return QuantNP(pack_codes(codes, nbits), scale16, zero16, nbits, group_size, D)
@@ -117,7 +124,8 @@ def dequantize_groupwise(qt: QuantNP) -> np.ndarray:
     """fp32 ``code * scale + zero``, ``quantize.py:239-246``."""
     codes = unpack_codes(qt.packed, qt.nbits, qt.head_dim)
     cg = codes.reshape(*codes.shape[:-1], qt.n_groups, qt.group_size).astype(np.float32)
-    out = cg * qt.scale.astype(np.float32)[..., None] + qt.zero.astype(np.float32)[..., None]
+    with np.errstate(invalid="ignore"):  # code 0 times an infinite scale is NaN
+        out = cg * qt.scale.astype(np.float32)[..., None] + qt.zero.astype(np.float32)[..., None]
     return out.reshape(*codes.shape[:-1], qt.head_dim).astype(np.float32)
 
 

@@ -109,13 +109,20 @@ int tkvo_quantize(const float *x, int64_t rows, int D, int nbits, int gs,
         for (int g = 0; g < NG; ++g) {
             const float *xg = xr + g * gs;
             float lo = xg[0], hi = xg[0];
-            for (int i = 1; i < gs; ++i) {
+            int has_nan = 0;
+            for (int i = 0; i < gs; ++i) {
+                if (xg[i] != xg[i]) has_nan = 1;
                 if (xg[i] < lo) lo = xg[i];
                 if (xg[i] > hi) hi = xg[i];
             }
+            /* torch's amin/amax propagate a NaN and return the canonical quiet
+             * NaN, whatever the input NaN's sign and payload: the group gets
+             * scale 1 (NaN > 0 is false), zero fp16 0x7E00 and codes 0. */
+            if (has_nan) lo = hi = NAN;
             float scale = (hi - lo) / (float)qmax;
             if (!(scale > 0.0f)) scale = 1.0f;
-            uint16_t s16 = tkvo_f32_to_f16(scale), z16 = tkvo_f32_to_f16(lo);
+            uint16_t s16 = tkvo_f32_to_f16(scale);
+            uint16_t z16 = has_nan ? (uint16_t)0x7e00u : tkvo_f32_to_f16(lo);
             float sf = tkvo_f16_to_f32(s16), zf = tkvo_f16_to_f32(z16);
             scale16[r * NG + g] = s16;
             zero16[r * NG + g] = z16;

@@ -62,6 +62,58 @@ def _cases():
     x = torch.cat([sub, tiny, sub * 1024, torch.randn(32, generator=g)])[None].half()
     out.append(("subnormal_b4", x, 4, 32))
     out.append(("subnormal_b2", x, 2, 32))
+    return out + _nonfinite_cases()
+
+
+def _nonfinite_cases():
+    """NaN, +-Inf and fp32-beyond-fp16 input, at nbits 2/4 and gs 32/128.
+
+    These pin how the reference's ``amin``/``amax`` propagate a NaN (the group
+    gets the canonical fp16 NaN zero, scale 1, codes 0), how an infinite range
+    becomes an infinite scale, and how a range or minimum past 65504 rounds to
+    an infinite fp16 scale or zero.  A generator of their own keeps the earlier
+    cases' vectors unchanged.
+    """
+    g = torch.Generator().manual_seed(4321)
+    nan, inf = float("nan"), float("inf")
+    out = []
+    for nbits in (2, 4):
+        for gs in (32, 128):
+            tag = f"b{nbits}_g{gs}"
+            # one NaN per row, at different dims; a negative NaN bit pattern;
+            # the last row stays finite
+            x = torch.randn(4, 128, generator=g).half()
+            x[0, 5] = nan
+            x[1, 127] = nan
+            x.view(torch.int16)[2, 40] = -512  # 0xFE00: NaN with the sign bit
+            out.append((f"nan_one_{tag}", x, nbits, gs))
+            # a whole group of NaN, and a whole row
+            x = torch.randn(3, 128, generator=g).half()
+            x[0, :gs] = nan
+            x[1, :] = nan
+            x[2, 64:64 + gs // 2] = nan
+            out.append((f"nan_all_{tag}", x, nbits, gs))
+            # +Inf, -Inf, both in one group, Inf beside NaN, a group of +Inf
+            x = torch.randn(5, 128, generator=g).half()
+            x[0, 3] = inf
+            x[1, 70] = -inf
+            x[2, 10], x[2, 11] = inf, -inf
+            x[3, 0], x[3, 1] = inf, nan
+            x[4, 96:] = inf
+            out.append((f"inf_{tag}", x, nbits, gs))
+            # fp32 input beyond fp16's range: an overflowing scale, an
+            # overflowing zero (-inf) with a finite scale, a zero of +inf,
+            # the rounding edge at 65520, and an fp32 NaN with a payload
+            x = torch.randn(6, 128, generator=g)
+            x[0, 7] = 1.0e6
+            x[1, :] = -7.0e4 + torch.rand(128, generator=g)
+            x[2, :] = 1.0e5 + torch.rand(128, generator=g)
+            x[3, :] = 65519.0
+            x[3, 1] = 65520.0
+            x[4, :] = -65520.0
+            x[4, 2] = -65519.0
+            x.view(torch.int32)[5, 9] = 0x7FC12345
+            out.append((f"f32_range_{tag}", x, nbits, gs))
     return out
 
 

@@ -24,6 +24,23 @@ MAX_ABS_TOL = 2e-3
 MEAN_ABS_TOL = 1e-3
 
 
+def same_float_bits(a, b) -> bool:
+    """Bit-for-bit equal float arrays, where a NaN matches any NaN in the same place.
+
+    A NaN's sign and payload are not a value: the reference's dequant computes
+    ``0 * inf`` on the host CPU, which returns x86's default NaN (sign bit set),
+    while the GPU returns the positive canonical one.
+    """
+    a, b = np.asarray(a), np.asarray(b)
+    if a.shape != b.shape or a.dtype != b.dtype:
+        return False
+    na, nb = np.isnan(a), np.isnan(b)
+    if not np.array_equal(na, nb):
+        return False
+    ui = {2: np.uint16, 4: np.uint32, 8: np.uint64}[a.dtype.itemsize]
+    return bool(np.array_equal(a[~na].view(ui), b[~nb].view(ui)))
+
+
 def metrics(got, ref) -> dict:
     if isinstance(got, torch.Tensor):
         got = got.detach().float().cpu().numpy()

@@ -525,6 +525,56 @@ def test_twelve_wave_splits_and_combine_modes(fused_combine):
         assert int(cnt.abs().sum()) == 0
 
 
+@pytest.mark.parametrize("num_splits", [8, 32])
+def test_fused_combine_reads_this_calls_partials(num_splits):
+    """The in-kernel combine hands partials between workgroups (possibly on
+    other XCDs) through coherent stores and loads.  Back-to-back calls on one
+    workspace with a different q each: a partial read stale from the previous
+    call would hold that call's values.  Each output must equal, bit for bit,
+    the same fused call on a fresh workspace whose partials start as NaN, and
+    the oracle within tolerance."""
+    from tritonkv_amd import _lib
+    from tritonkv_amd.kernels import plan_splits
+
+    B, HQ, HKV, D, S = 2, 12, 2, 128, 6000
+    print(f"fused combine, new q per call, ns={num_splits}", flush=True)
+    _, _, _, kq, vq = make_case(B, HQ, HKV, D, S, 4, 32, 41)
+    _, ns, size = plan_splits(S, 64, num_splits, B, HKV, HQ // HKV)
+    lib, st = _lib.load(), _lib.stream_handle(torch.device(DEV))
+
+    def workspace(fill):
+        return (torch.full((B, HQ, ns, D), fill, device=DEV),
+                torch.full((B, HQ, ns), fill, device=DEV),
+                torch.full((B, HQ, ns), fill, device=DEV),
+                torch.zeros(B * HKV, dtype=torch.int32, device=DEV))
+
+    def call(q, ws, out):
+        acc, mx, sm, cnt = ws
+        a = _lib.DecodeArgs(q=q.data_ptr(), k=kq.packed.data_ptr(), k_scale=kq.scale.data_ptr(),
+                            k_zero=kq.zero.data_ptr(), v=vq.packed.data_ptr(),
+                            v_scale=vq.scale.data_ptr(), v_zero=vq.zero.data_ptr(),
+                            acc=acc.data_ptr(), maxs=mx.data_ptr(), sums=sm.data_ptr(),
+                            out=out.data_ptr(), B=B, HQ=HQ, HKV=HKV, S=S, D=D, k_nbits=4,
+                            v_nbits=4, group_size=32, sm_scale=D ** -0.5, split_size=size,
+                            num_splits=ns, counters=cnt.data_ptr(), waves=8)
+        _lib.check(lib.tkv_fused_decode_attention(a, st), "fused combine")
+
+    shared = workspace(0.0)
+    g = torch.Generator().manual_seed(5)
+    qs = [(torch.randn(B, HQ, D, generator=g) * (1 + 2 * i)).half().to(DEV) for i in range(6)]
+    outs = [torch.full((B, HQ, D), float("nan"), device=DEV) for _ in qs]
+    for q, out in zip(qs, outs):  # back to back, no host sync between the calls
+        call(q, shared, out)
+    torch.cuda.synchronize()
+    assert int(shared[3].abs().sum()) == 0
+    for i, (q, out) in enumerate(zip(qs, outs)):
+        fresh_out = torch.full((B, HQ, D), float("nan"), device=DEV)
+        call(q, workspace(float("nan")), fresh_out)
+        torch.cuda.synchronize()
+        assert torch.equal(out, fresh_out), f"call {i}: differs from the fresh-workspace call"
+        assert_close_to_reference(out, oracle_attention_on_quant(q, kq, vq), f"call {i}")
+
+
 @pytest.mark.parametrize("kbits,vbits,gs,waves", [(4, 4, 32, 8), (2, 2, 128, 4), (4, 2, 32, 8)])
 def test_read_probe_runs_over_the_split_kernels_reads(kbits, vbits, gs, waves):
     """tkv_read_probe (the bandwidth-ceiling probe of the split kernel's access

@@ -185,3 +185,33 @@ def test_ordered_dispatch_with_empty_and_overlong_rows(ns):
     ref = oracle_attention_on_quant(q[kd], sub[0], sub[1],
                                     seq_lens=lens[keep].clamp(max=S).numpy())
     assert_close_to_reference(on[kd], ref, f"ordered rows with empty neighbours ns={ns}")
+
+
+@pytest.mark.parametrize("length", [16384, 15000])
+def test_equal_lengths_take_the_unragged_plan(monkeypatch, length):
+    """``equal_lengths=True`` with ``seq_lens``: the split plan of a batch
+    without lengths (here one workgroup per unit, where the ragged rule cuts
+    histories of >= 16384 tokens into two pieces), still stopping each row at
+    its length.  At the full length the output is bit-identical to the call
+    without ``seq_lens``; both plans match the oracle."""
+    from tritonkv_amd.kernels import fused_decode_attn as fda
+
+    monkeypatch.setattr(fda, "compute_units", lambda device=None: 8)  # B * HKV units fill the GPU
+    B, HQ, HKV, D, S = 2, 8, 4, 128, 16384
+    print(f"equal lengths {length} of S={S}", flush=True)
+    q, _, _, kq, vq = make_case(B, HQ, HKV, D, S, 4, 32, 77)
+    lens = torch.full((B,), length, dtype=torch.int32, device=DEV)
+    ws_eq, ws_rag = {}, {}
+    out_eq = fda.fused_decode_attention(q, kq, vq, seq_lens=lens, equal_lengths=True,
+                                        _workspace=ws_eq)
+    out_rag = fda.fused_decode_attention(q, kq, vq, seq_lens=lens, _workspace=ws_rag)
+    torch.cuda.synchronize()
+    assert "acc" not in ws_eq and "work_order" not in ws_eq  # one split, no order
+    assert ws_rag["key"][2] == 2                            # the ragged rule's two pieces
+    ref = oracle_attention_on_quant(q, kq, vq, seq_lens=lens.cpu().numpy())
+    assert_close_to_reference(out_eq, ref, "equal lengths")
+    assert_close_to_reference(out_rag, ref, "ragged plan")
+    if length == S:
+        out_none = fda.fused_decode_attention(q, kq, vq)
+        torch.cuda.synchronize()
+        assert torch.equal(out_eq, out_none)

@@ -17,6 +17,7 @@ import torch
 
 from oracle import inputs as oinp
 from oracle import quant as oq
+from tests.helpers import same_float_bits
 
 pytestmark = pytest.mark.gpu
 
@@ -45,7 +46,7 @@ def test_gpu_quantize_matches_reference_golden(name):
     assert np.array_equal(_bits16(qt.scale), z[f"{name}__scale"].view(np.uint16))
     assert np.array_equal(_bits16(qt.zero), z[f"{name}__zero"].view(np.uint16))
     deq = dequantize_groupwise(qt).cpu().numpy()
-    assert np.array_equal(deq.view(np.uint32), z[f"{name}__deq"].view(np.uint32))
+    assert same_float_bits(deq, z[f"{name}__deq"])
 
 
 @pytest.mark.parametrize("D", [64, 128])

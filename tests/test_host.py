@@ -123,6 +123,52 @@ def test_work_order_argument_checks_without_a_gpu():
     assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
 
 
+def test_blocks_past_the_32bit_buffer_range_are_refused_without_a_gpu():
+    """One (b, kv head) block (or page slab) of any cache tensor must span less
+    than 2^32 bytes: the split kernels' buffer resources have 32-bit ranges.
+    Larger ones are refused before any launch, where a wrapped range would
+    have read zeros past the wrap."""
+    from tritonkv_amd import _lib
+
+    lib = _lib.load()
+    dummy = 0x1000
+    a = _lib.DecodeArgs(q=dummy, k=dummy, v=dummy, k_scale=dummy, k_zero=dummy, v_scale=dummy,
+                        v_zero=dummy, out=dummy, acc=dummy, maxs=dummy, sums=dummy, B=1, HQ=8,
+                        HKV=2, D=128, k_nbits=4, v_nbits=4, group_size=32, sm_scale=0.1,
+                        waves=8)
+
+    def with_s(S, ns=64):
+        a.S, a.num_splits, a.split_size = S, ns, -(-S // ns)
+        return a
+
+    # 4-bit codes: 64 B per row, so 2^26 rows are exactly 2^32 bytes
+    rc = lib.tkv_fused_decode_attention(ctypes.byref(with_s(1 << 26)), None)
+    assert rc == _lib.TKV_EUNSUPPORTED
+    assert lib.tkv_fused_decode_split(ctypes.byref(a), None) == _lib.TKV_EUNSUPPORTED
+    assert lib.tkv_read_probe(ctypes.byref(a), None) == _lib.TKV_EUNSUPPORTED
+    a.acc = a.maxs = a.sums = None
+    assert lib.tkv_fused_decode_attention_noalloc(ctypes.byref(a), None) == _lib.TKV_EUNSUPPORTED
+    a.acc = a.maxs = a.sums = dummy
+    # 2-bit K with 4-bit V: the V codes are the larger range
+    a.k_nbits = 2
+    assert lib.tkv_fused_decode_attention(ctypes.byref(with_s(1 << 26)), None) == \
+        _lib.TKV_EUNSUPPORTED
+    # 2-bit K and V, groups of 16: 32 B of codes and 16 B of scale per row -> 2^27 rows
+    a.v_nbits, a.group_size = 2, 16
+    assert lib.tkv_fused_decode_attention(ctypes.byref(with_s(1 << 27)), None) == \
+        _lib.TKV_EUNSUPPORTED
+    # the fp16 control: 256 B per row, 2^24 rows
+    assert lib.tkv_fp16_decode_attention(ctypes.byref(with_s(1 << 24)), None) == \
+        _lib.TKV_EUNSUPPORTED
+    # a paged pool is bounded per page slab, not per sequence: a huge page is refused
+    a.k_nbits = a.v_nbits = 4
+    a.group_size = 32
+    a.block_table, a.block_table_stride, a.num_pages = dummy, 1, 4
+    a.page_size = 1 << 26
+    assert lib.tkv_fused_decode_attention(ctypes.byref(with_s(1 << 26)), None) == \
+        _lib.TKV_EUNSUPPORTED
+
+
 def test_order_buffer_policy():
     """The Python entries take a work_order buffer for ragged split calls only."""
     from tritonkv_amd.kernels.fused_decode_attn import _order_for

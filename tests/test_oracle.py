@@ -23,6 +23,8 @@ from oracle import inputs as oinp
 from oracle import quant as oq
 from oracle import splits as osp
 
+from tests.helpers import same_float_bits
+
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "quantize_golden.npz")
 
 
@@ -100,7 +102,7 @@ def test_numpy_oracle_matches_reference_golden(case):
         assert np.array_equal(qt.scale.view(np.uint16), z[f"{name}__scale"].view(np.uint16))
         assert np.array_equal(qt.zero.view(np.uint16), z[f"{name}__zero"].view(np.uint16))
         deq = oq.dequantize_groupwise(qt)
-        assert np.array_equal(deq.view(np.uint32), z[f"{name}__deq"].view(np.uint32))
+        assert same_float_bits(deq, z[f"{name}__deq"])
 
 
 @pytest.mark.parametrize("case", [c[0] for c in _golden_cases()])
@@ -114,7 +116,7 @@ def test_c_oracle_matches_reference_golden(case):
         assert np.array_equal(zz.view(np.uint16), z[f"{name}__zero"].view(np.uint16))
         deq = c_oracle.dequantize(z[f"{name}__packed"], z[f"{name}__scale"], z[f"{name}__zero"],
                                   nbits, gs, x.shape[-1])
-        assert np.array_equal(deq.view(np.uint32), z[f"{name}__deq"].view(np.uint32))
+        assert same_float_bits(deq, z[f"{name}__deq"])
 
 
 def test_golden_covers_ties_and_underflow():

@@ -30,6 +30,10 @@ def test_per_channel_equals_per_token_quantizer_on_transposed_blocks(nbits, D):
     x = _rand((B, H, S, D), seed=nbits + D)
     x[0, 1, 40:50, 7] = 1.25                                  # a constant stretch
     x[1, 2, 64:96, 5] = 0.5                                   # a constant group
+    x[0, 0, 3, 9] = np.nan                                    # non-finite input, which
+    x[0, 2, 70, 11] = np.inf                                  # the per-token quantizer's
+    x[1, 0, 33, 2] = -np.inf                                  # golden cases pin
+    x.view(np.uint16)[1, 1, 90, 4] = 0xFE00                   # a NaN with the sign bit
     ck = och.quantize_keys_per_channel(x, nbits, T)
     codes = oq.unpack_codes(ck.packed, nbits, D)              # (B, H, S, D)
     assert ck.scale.shape == (B, H, S // T, D) and ck.scale.dtype == np.float16
@@ -43,6 +47,9 @@ def test_per_channel_equals_per_token_quantizer_on_transposed_blocks(nbits, D):
     # the constant group: scale 1, zero = the value, codes 0
     assert float(ck.scale[1, 2, 2, 5]) == 1.0 and float(ck.zero[1, 2, 2, 5]) == 0.5
     assert not codes[1, 2, 64:96, 5].any()
+    # a NaN channel block: scale 1, the canonical NaN zero, codes 0
+    assert ck.zero[0, 0, 0, 9].view(np.uint16) == 0x7E00 == ck.zero[1, 1, 2, 4].view(np.uint16)
+    assert float(ck.scale[0, 0, 0, 9]) == 1.0 and not codes[0, 0, 0:32, 9].any()
 
 
 @pytest.mark.parametrize("nbits", [2, 4])

@@ -134,6 +134,8 @@ def channel_decode_attention(
     num_splits: int | None = None,
     out: torch.Tensor | None = None,
     _workspace: dict | None = None,
+    *,
+    equal_lengths: bool = False,
 ) -> torch.Tensor:
     """One decode step over per-channel keys, per-token values and an fp16 window.
 
@@ -144,7 +146,9 @@ def channel_decode_attention(
     quantized tokens followed by its window tokens.  ``vq.group_size`` must be
     16 or 32.  ``num_splits`` / ``out`` / ``_workspace`` as for
     :func:`~tritonkv_amd.kernels.fused_decode_attention` (the workspace holds
-    one more split, the window's).
+    one more split, the window's); ``equal_lengths``: every entry of
+    ``q_lens`` is the same, so the split plan of a batch without lengths
+    applies.
     """
     for t, what in ((q, "q"), (k_res, "k_res"), (v_res, "v_res")):
         if not isinstance(t, torch.Tensor):
@@ -173,7 +177,7 @@ def channel_decode_attention(
     group = HQ // HKV
     sm_scale = 1.0 / math.sqrt(D) if sm_scale is None else sm_scale
     _, num_splits, split_size = plan_splits(S, block_n, num_splits, B, HKV, group,
-                                            ragged=q_lens is not None)
+                                            ragged=q_lens is not None and not equal_lengths)
     if q.dtype not in (torch.float16, torch.float32):
         q = q.float()
     q = _aligned16(q)
@@ -304,10 +308,13 @@ class ChannelKVCache:
 
     def attend(self, q: torch.Tensor, sm_scale: float | None = None,
                out: torch.Tensor | None = None) -> torch.Tensor:
-        """Attention of ``q`` ``(B, HQ, D)`` over everything appended so far."""
+        """Attention of ``q`` ``(B, HQ, D)`` over everything appended so far.
+        Every row holds the same number of tokens, so the split plan is the
+        one for equal lengths."""
         return channel_decode_attention(q, self.keys, self.values, self.k_res, self.v_res,
                                         q_lens=self._qlens, res_lens=self._rlens,
-                                        sm_scale=sm_scale, out=out, _workspace=self.workspace)
+                                        sm_scale=sm_scale, out=out, _workspace=self.workspace,
+                                        equal_lengths=True)
 
     def step(self, k: torch.Tensor, v: torch.Tensor, q: torch.Tensor,
              sm_scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:

@@ -309,7 +309,7 @@ __device__ __forceinline__ void combine_row(const float* __restrict__ acc,
     const float ms = maxs[ps];
     const float ls = sums[ps];
     const f4 as = reinterpret_cast<const f4*>(acc + ps * D)[dq];
-    if (ms == -INFINITY) continue;
+    if (is_empty_partial(ms, ls)) continue;
     const float mn = fmaxf(m, ms);
     const float al = safe_exp2_diff(m, mn);
     const float be = __builtin_amdgcn_exp2f(ms - mn);
@@ -380,7 +380,7 @@ __global__ void __launch_bounds__(64) combine_small_kernel(const float* __restri
   f4 a = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
-    if (g + NGRP * i >= ns || ms[i] == -INFINITY) continue;
+    if (g + NGRP * i >= ns || is_empty_partial(ms[i], ls[i])) continue;
     const float mn = fmaxf(m, ms[i]);
     const float al = safe_exp2_diff(m, mn);
     const float be = __builtin_amdgcn_exp2f(ms[i] - mn);
@@ -523,6 +523,20 @@ static int validate_common(const tkv_decode_args* a) {
   return TKV_OK;
 }
 
+// The split kernels open one buffer resource per (b, kv head) block -- or per
+// (page, kv head) slab of a paged pool -- and tensor, with a 32-bit byte range
+// and 32-bit lane offsets.  A block of `rows` rows of `row_bytes` bytes each
+// must therefore span less than 2^32 bytes, or its range would wrap and the
+// hardware range check would return zeros for the rows past the wrap.
+static bool block_fits_range(int64_t rows, int64_t row_bytes) {
+  return rows * row_bytes < (int64_t(1) << 32);
+}
+
+// Rows of one buffer range: a page slab for paged pools, else the block's capacity.
+static int64_t range_rows(const tkv_decode_args* a) {
+  return a->page_size > 0 ? a->page_size : a->S;
+}
+
 static SplitParams make_params(const tkv_decode_args* a) {
   SplitParams p;
   p.q = a->q;
@@ -643,8 +657,9 @@ static int status_of_launch() {
 
 namespace tkv {
 
-static int launch_fused_split(const tkv_decode_args* a, hipStream_t st, bool probe = false) {
-  int rc = validate_common(a);
+// Every argument check of the quantized split launch; nothing touches the GPU.
+static int check_fused_split(const tkv_decode_args* a, bool probe) {
+  const int rc = validate_common(a);
   if (rc) return rc;
   if (probe && (a->page_size > 0 || a->k_new || a->key_block)) return TKV_EUNSUPPORTED;
   if (!a->k_scale || !a->k_zero || !a->v_scale || !a->v_zero) return TKV_EINVAL;
@@ -655,6 +670,19 @@ static int launch_fused_split(const tkv_decode_args* a, hipStream_t st, bool pro
   if (a->key_block && gs > 32) return TKV_EUNSUPPORTED;  // per-channel keys: V groups of 16 or 32
   // the instantiated group sizes (dispatch_gs), checked before anything is launched
   if (gs != 16 && gs != 32 && gs != 64 && gs != 128) return TKV_EUNSUPPORTED;
+  // codes (K, V) and fp16 scale/zero rows of one buffer range
+  const int64_t rows = range_rows(a);
+  if (!block_fits_range(rows, (int64_t)a->D * a->k_nbits / 8) ||
+      !block_fits_range(rows, (int64_t)a->D * a->v_nbits / 8) ||
+      !block_fits_range(rows, (int64_t)(a->D / gs) * 2))
+    return TKV_EUNSUPPORTED;
+  return TKV_OK;
+}
+
+static int launch_fused_split(const tkv_decode_args* a, hipStream_t st, bool probe = false) {
+  int rc = check_fused_split(a, probe);
+  if (rc) return rc;
+  const int gs = a->group_size;
   SplitParams p = make_params(a);
   const dim3 grid = split_grid(a);
   (void)hipGetLastError();
@@ -675,6 +703,7 @@ static int launch_fp16_split(const tkv_decode_args* a, hipStream_t st) {
   if (rc) return rc;
   // the fp16 control reads contiguous caches in the natural order and has no fused append
   if (a->page_size > 0 || a->k_new || a->key_block || a->work_order) return TKV_EUNSUPPORTED;
+  if (!block_fits_range(a->S, (int64_t)a->D * 2)) return TKV_EUNSUPPORTED;  // fp16 rows
   const SplitParams p = make_params(a);
   const dim3 grid = split_grid(a);
   (void)hipGetLastError();
@@ -836,8 +865,13 @@ extern "C" int tkv_fused_decode_attention_noalloc(const tkv_decode_args* a, tkv_
     const uint64_t acc_bytes = align256(rows * (uint64_t)a->D * 4);
     const uint64_t ml_bytes = align256(rows * 4);
     if (acc_bytes + 2 * ml_bytes > TKV_NOALLOC_SCRATCH_BYTES) return TKV_ESCRATCH;
+    // Every argument is checked before the device is touched; any aligned
+    // non-null address stands in for the partials, which are not read here.
+    s.acc = s.maxs = s.sums = reinterpret_cast<float*>(uintptr_t(256));
+    int rc = check_fused_split(&s, false);
+    if (rc) return rc;
     void* base = nullptr;
-    const int rc = scratch_on_current_device(&base);
+    rc = scratch_on_current_device(&base);
     if (rc) return rc;
     unsigned char* p = static_cast<unsigned char*>(base);
     s.acc = reinterpret_cast<float*>(p);

@@ -196,6 +196,15 @@ __device__ void merge_and_store(const SplitParams& prm, const MergeView& mv, int
         o = fmaf(f, mv.o[w * mv.stride + n * (D + 1) + d], o);
         l = fmaf(f, mv.l[w * mv.stride + n], l);
       }
+    } else {
+      // No wave saw a finite score for this head.  Every wave's o and l are
+      // then 0 (no tokens), or NaN where its scores were NaN (a NaN key in the
+      // cache); the sum keeps the NaN, as the reference's softmax would.
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        o += mv.o[w * mv.stride + n * (D + 1) + d];
+        l += mv.l[w * mv.stride + n];
+      }
     }
     const int64_t row = (int64_t)b * prm.HQ + h0 + n;
     if (prm.ns_total == 1) {
@@ -266,7 +275,7 @@ __device__ void merge_and_store(const SplitParams& prm, const MergeView& mv, int
       }
 #pragma unroll
       for (int i = 0; i < NB; ++i) {
-        if (s0 + i >= ns || ms[i] == -INFINITY) continue;
+        if (s0 + i >= ns || is_empty_partial(ms[i], ls[i])) continue;
         const float mn = fmaxf(m, ms[i]);
         const float al = safe_exp2_diff(m, mn);
         const float be = __builtin_amdgcn_exp2f(ms[i] - mn);

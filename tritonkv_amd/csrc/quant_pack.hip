@@ -113,7 +113,7 @@ quantize_pack_wide_kernel(const void* __restrict__ x, int rows, int HKV, int N,
 #pragma unroll
     for (int p = 0; p < P; ++p) {
       if constexpr (F32) {
-        // Whole-vector casts: this compiler folds fminf/fmaxf over floats cast
+        // Whole-vector casts: this compiler folds a min/max over floats cast
         // one by one from the elements of an integer vector to the first one.
         const f4 lo = __builtin_bit_cast(f4, raw[s][p][0]), hi = __builtin_bit_cast(f4, raw[s][p][1]);
 #pragma unroll
@@ -126,8 +126,8 @@ quantize_pack_wide_kernel(const void* __restrict__ x, int rows, int HKV, int N,
       mn[p] = mx[p] = v[p][0];
 #pragma unroll
       for (int e = 1; e < E; ++e) {
-        mn[p] = fminf(mn[p], v[p][e]);
-        mx[p] = fmaxf(mx[p], v[p][e]);
+        mn[p] = nan_min(mn[p], v[p][e]);
+        mx[p] = nan_max(mx[p], v[p][e]);
       }
     }
     if constexpr (GS <= DP) {
@@ -139,8 +139,8 @@ quantize_pack_wide_kernel(const void* __restrict__ x, int rows, int HKV, int N,
       for (int p = 0; p < P; p += SPG) {
 #pragma unroll
         for (int e = 1; e < SPG; ++e) {
-          mn[p] = fminf(mn[p], mn[p + e]);
-          mx[p] = fmaxf(mx[p], mx[p + e]);
+          mn[p] = nan_min(mn[p], mn[p + e]);
+          mx[p] = nan_max(mx[p], mx[p + e]);
         }
         minmax_lanes<LPR>(mn[p], mx[p]);
 #pragma unroll
@@ -162,7 +162,7 @@ quantize_pack_wide_kernel(const void* __restrict__ x, int rows, int HKV, int N,
       sf[p] = (float)s16;
       zf[p] = (float)z16;
       s16b[p] = __builtin_bit_cast(uint16_t, s16);
-      z16b[p] = __builtin_bit_cast(uint16_t, z16);
+      z16b[p] = zero_bits(mn[p]);
       const float rs = __builtin_amdgcn_rcpf(sf[p]);
 #pragma unroll
       for (int e = 0; e < E; ++e) {
@@ -249,8 +249,8 @@ __device__ __forceinline__ void quantize_key_block(const void* __restrict__ x, i
     float mn = v[p][0], mx = v[p][0];
 #pragma unroll
     for (int t = 1; t < T; ++t) {
-      mn = fminf(mn, v[p][t]);
-      mx = fmaxf(mx, v[p][t]);
+      mn = nan_min(mn, v[p][t]);
+      mx = nan_max(mx, v[p][t]);
     }
     float sc = (mx - mn) / (float)QMAX;
     if (!(sc > 0.0f)) sc = 1.0f;
@@ -266,7 +266,7 @@ __device__ __forceinline__ void quantize_key_block(const void* __restrict__ x, i
     }
     if (ok) {
       scale[meta + j + p * DP] = __builtin_bit_cast(uint16_t, s16);
-      zero[meta + j + p * DP] = __builtin_bit_cast(uint16_t, z16);
+      zero[meta + j + p * DP] = zero_bits(mn);
     }
   }
   if (!ok) return;

@@ -177,6 +177,14 @@ __device__ __forceinline__ float safe_exp2_diff(float a, float b) {
   return (a == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(a - b);
 }
 
+// A split partial that saw no token: max -inf and sum 0.  A partial whose
+// scores were all NaN also keeps max -inf (the max steps drop NaN), but its sum
+// is NaN, and it must be merged so that the NaN reaches the output.  A partial
+// with any finite score has a sum of at least 1 (its largest score's term).
+__device__ __forceinline__ bool is_empty_partial(float m, float l) {
+  return m == -INFINITY && l == 0.0f;
+}
+
 // ---------------------------------------------------------------------------
 // Raw buffer loads.  A buffer resource (base, size) lives in SGPRs; each load
 // takes a 32-bit lane offset (VGPR) plus an immediate, so per-chunk addressing

@@ -14,6 +14,13 @@
 // fp16 zero) gives code 0, as torch's clamp of NaN does.  The file that uses
 // this must not be compiled with fast-math.
 //
+// Non-finite input follows torch's amin / amax (quantize.py:209-210): a NaN
+// anywhere in a group makes its min and max NaN, so the group gets scale 1,
+// codes 0 and the canonical fp16 NaN 0x7E00 as its zero, whatever the sign or
+// payload of the input NaN.  An infinite range gives an infinite scale and
+// codes 0; a range or minimum past 65504 rounds to an infinite fp16 scale or
+// zero, as Tensor.half() does.
+//
 // The group min/max reductions run on the VALU (DPP row permutations and the
 // gfx950 permlane swaps), not through LDS.  The code's division is taken as a
 // product with the reciprocal; the IEEE quotient is computed only for the
@@ -38,6 +45,23 @@ struct RowQuant {
   uint32_t meta;  // lanes g < NG: group g's fp16 scale (bits 0..15) and zero (16..31)
 };
 
+// IEEE 754-2019 minimum / maximum: NaN when either operand is NaN, as torch's
+// amin / amax (v_minimum3_f32 / v_maximum3_f32 on gfx950, one instruction
+// each).  fminf / fmaxf would drop the NaN and give the group the range of its
+// other values.
+__device__ __forceinline__ float nan_min(float a, float b) {
+  return __builtin_elementwise_minimum(a, b);
+}
+__device__ __forceinline__ float nan_max(float a, float b) {
+  return __builtin_elementwise_maximum(a, b);
+}
+
+// The fp16 bits of a group's zero point (its minimum): torch returns the
+// canonical quiet NaN from amin, so a NaN minimum is stored as 0x7E00.
+__device__ __forceinline__ uint16_t zero_bits(float mn) {
+  return mn != mn ? (uint16_t)0x7E00u : __builtin_bit_cast(uint16_t, (_Float16)mn);
+}
+
 // One butterfly step of a min/max reduction: combine with the value DPP
 // control CTRL brings from another lane of the same row of 16 lanes.
 template <int CTRL>
@@ -46,8 +70,8 @@ __device__ __forceinline__ void minmax_dpp(float& mn, float& mx) {
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, mn), CTRL, 0xF, 0xF, false));
   const float b = __builtin_bit_cast(
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, mx), CTRL, 0xF, 0xF, false));
-  mn = fminf(mn, a);
-  mx = fmaxf(mx, b);
+  mn = nan_min(mn, a);
+  mx = nan_max(mx, b);
 }
 
 
@@ -56,7 +80,7 @@ __device__ __forceinline__ void minmax_dpp(float& mn, float& mx) {
 // value v twice, the swap returns v with each odd part replaced by its even
 // partner in one output and each even part by its odd partner in the other,
 // so the min (max) of the two outputs is the pair's in every lane.  The
-// outputs go through opaque(): this compiler folds fminf/fmaxf of the two
+// outputs go through opaque(): this compiler folds a min/max of the two
 // outputs of the swap builtin to its first output.
 template <bool SWAP32>
 __device__ __forceinline__ void minmax_swap(float& mn, float& mx) {
@@ -65,13 +89,14 @@ __device__ __forceinline__ void minmax_swap(float& mn, float& mx) {
                          : __builtin_amdgcn_permlane16_swap(n, n, false, false);
   const auto sx = SWAP32 ? __builtin_amdgcn_permlane32_swap(x, x, false, false)
                          : __builtin_amdgcn_permlane16_swap(x, x, false, false);
-  mn = fminf(__builtin_bit_cast(float, opaque(sn[0])), __builtin_bit_cast(float, opaque(sn[1])));
-  mx = fmaxf(__builtin_bit_cast(float, opaque(sx[0])), __builtin_bit_cast(float, opaque(sx[1])));
+  mn = nan_min(__builtin_bit_cast(float, opaque(sn[0])), __builtin_bit_cast(float, opaque(sn[1])));
+  mx = nan_max(__builtin_bit_cast(float, opaque(sx[0])), __builtin_bit_cast(float, opaque(sx[1])));
 }
 
 // Min and max over aligned runs of W lanes (W a power of two, 1..64); every
-// lane of a run ends with the run's min and max.  fminf/fmaxf select one of
-// their operands, so the result does not depend on the order of the steps.
+// lane of a run ends with the run's min and max.  nan_min/nan_max select one
+// of their operands (or give NaN), so the result does not depend on the order
+// of the steps.
 //   lane^1, lane^2: quad_perm; the other quad of 8 lanes: row_half_mirror
 //   (lane 7-i); the other half of a 16-lane row: row_mirror (lane 15-i);
 //   rows 2k and 2k+1: v_permlane16_swap; the two 32-lane halves:
@@ -124,8 +149,8 @@ __device__ __forceinline__ RowQuant<D, NB, GS> quantize_row(const float (&x)[8 /
     for (int p = 0; p < P; p += SPG) {
 #pragma unroll
       for (int e = 1; e < SPG; ++e) {
-        mn[p] = fminf(mn[p], mn[p + e]);
-        mx[p] = fmaxf(mx[p], mx[p + e]);
+        mn[p] = nan_min(mn[p], mn[p + e]);
+        mx[p] = nan_max(mx[p], mx[p + e]);
       }
       minmax_lanes<DP>(mn[p], mx[p]);
 #pragma unroll
@@ -147,8 +172,7 @@ __device__ __forceinline__ RowQuant<D, NB, GS> quantize_row(const float (&x)[8 /
     if (c != c) c = 0.0f;
     c = fminf(fmaxf(c, 0.0f), (float)QMAX);
     byte |= (uint32_t)c << (p * NB);
-    sz[p] = (uint32_t)__builtin_bit_cast(uint16_t, s16) |
-            ((uint32_t)__builtin_bit_cast(uint16_t, z16) << 16);
+    sz[p] = (uint32_t)__builtin_bit_cast(uint16_t, s16) | ((uint32_t)zero_bits(mn[p]) << 16);
   }
   // Group g starts at dim g*GS: byte (g*GS) % DP, slice (g*GS) / DP.
   const int src = (lane * GS) % DP, slice = (lane * GS) / DP;

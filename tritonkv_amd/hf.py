@@ -160,14 +160,16 @@ class TkvLayer(_LayerBase):
             self.kc.index_copy_(2, pos, key.to(torch.float16))
             self.vc.index_copy_(2, pos, value.to(torch.float16))
             out = fp16_decode_attention(q, self.kc, self.vc, sm_scale=scaling, out=self.out,
-                                        _workspace=self.workspace, seq_lens=self.lens)
+                                        _workspace=self.workspace, seq_lens=self.lens,
+                                        equal_lengths=True)
         else:
-            # every row holds the same length: no uneven tail for a dispatch order to fix
+            # every row holds the same length: the split plan of an unragged
+            # batch, and no uneven tail for a dispatch order to fix
             out = fused_decode_attention(q, self.kc, self.vc, sm_scale=scaling, out=self.out,
                                          _workspace=self.workspace, seq_lens=self.lens,
                                          k_new=key[:, :, 0].to(torch.float16),
                                          v_new=value[:, :, 0].to(torch.float16),
-                                         dispatch_order=False)
+                                         equal_lengths=True)
         return out.to(query.dtype).view(B, 1, HQ, D)
 
 

@@ -51,10 +51,12 @@ def fp16_decode_attention(
     _workspace: dict | None = None,
     *,
     seq_lens: torch.Tensor | None = None,
+    equal_lengths: bool = False,
 ) -> torch.Tensor:
     """Decode attention on an unquantized fp16 cache, same shape as the fused kernel.
 
     q: (B, HQ, D); k, v: (B, HKV, S, D) fp16. Returns (B, HQ, D) float32.
+    ``seq_lens`` / ``equal_lengths`` as for ``fused_decode_attention``.
     """
     B, HQ, D = q.shape
     _, HKV, S, _ = k.shape
@@ -73,7 +75,7 @@ def fp16_decode_attention(
     sm_scale = 1.0 / math.sqrt(D) if sm_scale is None else sm_scale
     _, num_splits, split_size = plan_splits(S, block_n, num_splits, B, HKV, group,
                                             TOKENS_PER_WORKGROUP_FP16,
-                                            ragged=seq_lens is not None)
+                                            ragged=seq_lens is not None and not equal_lengths)
 
     if q.dtype not in (torch.float16, torch.float32):
         q = q.float()

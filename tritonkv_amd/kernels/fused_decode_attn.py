@@ -34,6 +34,12 @@ Differences a caller can observe, all deliberate:
   its L2), so it is off by default.
 * ``k_new`` / ``v_new`` (new, keyword-only): the decode-step append fused into
   the same launch -- see :func:`new_token_args`.
+* ``equal_lengths`` (new, keyword-only): the caller promises that every entry
+  of ``seq_lens`` is the same.  The split plan is then the one of a call
+  without ``seq_lens`` -- no cut of long histories into pieces, no dispatch
+  order -- while the kernel still stops each row at its length.  The promise
+  only steers the plan: a batch that breaks it still gets the right answer,
+  only less evenly spread over the compute units.
 """
 
 from __future__ import annotations
@@ -369,6 +375,7 @@ def fused_decode_attention(
     k_new: torch.Tensor | None = None,
     v_new: torch.Tensor | None = None,
     dispatch_order: bool | None = None,
+    equal_lengths: bool = False,
 ) -> torch.Tensor:
     """Single decode step of attention, computed directly on packed low-bit K/V.
 
@@ -377,6 +384,8 @@ def fused_decode_attention(
     ``(B, HKV, S, D//P)``.  Returns ``(B, HQ, D)`` float32.
     ``dispatch_order`` (new): longest-piece-first order of the split
     workgroups (``_order_for``); the result does not depend on it.
+    ``equal_lengths`` (new): every row of ``seq_lens`` holds the same length,
+    so the split plan of a batch without ``seq_lens`` applies.
     """
     if kq.group_size != vq.group_size or (kq.nbits != vq.nbits and not allow_mixed_bits):
         raise ValueError("K and V must use the same nbits/group_size")
@@ -412,8 +421,8 @@ def fused_decode_attention(
 
     group = HQ // HKV
     sm_scale = 1.0 / math.sqrt(D) if sm_scale is None else sm_scale
-    _, num_splits, split_size = plan_splits(S, block_n, num_splits, B, HKV, group,
-                                            ragged=seq_lens is not None)
+    ragged = seq_lens is not None and not equal_lengths
+    _, num_splits, split_size = plan_splits(S, block_n, num_splits, B, HKV, group, ragged=ragged)
 
     if q.dtype not in (torch.float16, torch.float32):
         q = q.float()
@@ -421,7 +430,8 @@ def fused_decode_attention(
     out = _check_out(out, B, HQ, D, q.device)
     acc, maxs, sums, counters = _workspace_for(_workspace, B, HQ, num_splits, D, q.device, HKV)
     lens = _seq_lens_arg(seq_lens, B, S, q.device)
-    order = _order_for(_workspace, B, HKV, num_splits, q.device, seq_lens, dispatch_order, group)
+    order = _order_for(_workspace, B, HKV, num_splits, q.device, seq_lens if ragged else None,
+                       dispatch_order, group)
 
     args = _lib.DecodeArgs(
         q=q.data_ptr(), q_is_fp32=int(q.dtype == torch.float32),

@@ -122,6 +122,7 @@ def paged_decode_attention(
     k_new: torch.Tensor | None = None,
     v_new: torch.Tensor | None = None,
     dispatch_order: bool | None = None,
+    equal_lengths: bool = False,
 ) -> torch.Tensor:
     """One decode step of attention over paged 2/4-bit K/V pools.
 
@@ -134,7 +135,8 @@ def paged_decode_attention(
     cache holding the same tokens with the same ``num_splits``.  ``k_new`` /
     ``v_new`` fuse the step's append into the same launch (the token lands at
     ``seq_lens[b] - 1``), bit-identical to :func:`paged_append` followed by
-    this call.  ``dispatch_order`` as for ``fused_decode_attention``.
+    this call.  ``dispatch_order`` and ``equal_lengths`` as for
+    ``fused_decode_attention``.
     """
     if k_pool.group_size != v_pool.group_size or (k_pool.nbits != v_pool.nbits
                                                   and not allow_mixed_bits):
@@ -166,15 +168,16 @@ def paged_decode_attention(
 
     group = HQ // HKV
     sm_scale = 1.0 / math.sqrt(D) if sm_scale is None else sm_scale
-    _, num_splits, split_size = plan_splits(S, block_n, num_splits, B, HKV, group,
-                                            ragged=seq_lens is not None)
+    ragged = seq_lens is not None and not equal_lengths
+    _, num_splits, split_size = plan_splits(S, block_n, num_splits, B, HKV, group, ragged=ragged)
     if q.dtype not in (torch.float16, torch.float32):
         q = q.float()
     q = _aligned16(q)
     out = _check_out(out, B, HQ, D, q.device)
     acc, maxs, sums, _ = _workspace_for(_workspace, B, HQ, num_splits, D, q.device, HKV)
     lens = seq_lens.contiguous() if seq_lens is not None else None
-    order = _order_for(_workspace, B, HKV, num_splits, q.device, seq_lens, dispatch_order, group)
+    order = _order_for(_workspace, B, HKV, num_splits, q.device, seq_lens if ragged else None,
+                       dispatch_order, group)
     args = _lib.DecodeArgs(
         q=q.data_ptr(), q_is_fp32=int(q.dtype == torch.float32),
         k=k_pool.packed.data_ptr(), k_scale=k_pool.scale.data_ptr(),
