@@ -531,6 +531,207 @@ def cpu_baseline(q, kq, vq, got, threads=None, one_thread_units=16):
     return base, check
 
 
+# ---------------------------------------------------------------------------
+# correctness snapshot: the checker of every timed leg (oracle/, outside every
+# timed region, as the reference re-checks what it times: benchmark.py:1050-1110)
+# ---------------------------------------------------------------------------
+
+CHECK_TOL = {"max_abs": 2e-3, "mean_abs": 1e-3}
+
+
+def _host_rows(t, b, h, L=None):
+    x = t[b, h] if L is None else t[b, h, :L]
+    return x.contiguous().cpu().numpy()
+
+
+def _qnp(qt, b, h, L=None):
+    """One (batch row, kv head) block of a device QuantizedTensor as the oracle's container."""
+    from oracle import quant as oq
+
+    return oq.QuantNP(_host_rows(qt.packed, b, h, L), _host_rows(qt.scale, b, h, L),
+                      _host_rows(qt.zero, b, h, L), qt.nbits, qt.group_size, qt.head_dim)
+
+
+def _attend(qrows, krows, vrows):
+    """fp32 attention of G query rows over one block's fp32 K/V rows
+    (oracle/tkv_oracle.c, sums in binary64)."""
+    from oracle import c_oracle
+
+    D = qrows.shape[-1]
+    return c_oracle.decode_attention(qrows[None], krows[None, None], vrows[None, None],
+                                     D ** -0.5)[0]
+
+
+def unit_refs(q, kq, vq, units, lens=None, fp16_dequant=False):
+    """The oracle's fp32 dequantise-then-attend of (batch row, kv head) units of
+    device caches (K and V may differ in bit width), or with ``fp16_dequant``
+    the reference's fp16 dequant baseline (``reference.py:96-108``) then fp32
+    attention.  -> {unit: (G, D) float32}"""
+    import numpy as np
+
+    from oracle import quant as oq
+
+    B, HQ, D = q.shape
+    G = HQ // kq.packed.shape[1]
+    qf = q.float().cpu().numpy()
+    out = {}
+    for b, h in units:
+        L = None if lens is None else int(lens[b])
+        kn, vn = _qnp(kq, b, h, L), _qnp(vq, b, h, L)
+        if fp16_dequant:
+            kd = oq.dequantize_fp16(kn).astype(np.float32)
+            vd = oq.dequantize_fp16(vn).astype(np.float32)
+        else:
+            kd, vd = oq.dequantize_groupwise(kn), oq.dequantize_groupwise(vn)
+        out[(b, h)] = _attend(qf[b, h * G:(h + 1) * G], kd, vd)
+    return out
+
+
+def truth_refs(q, k, v, units, lens=None):
+    """fp32 attention over the unquantized fp16 K/V: the end-to-end "truth" of
+    the reference's snapshot (``benchmark.py:1058-1062``)."""
+    B, HQ, D = q.shape
+    G = HQ // k.shape[1]
+    qf = q.float().cpu().numpy()
+    out = {}
+    for b, h in units:
+        L = None if lens is None else int(lens[b])
+        out[(b, h)] = _attend(qf[b, h * G:(h + 1) * G], _host_rows(k, b, h, L).astype("float32"),
+                              _host_rows(v, b, h, L).astype("float32"))
+    return out
+
+
+def unit_check(got, refs, G, what):
+    """Max-abs and mean-abs of the GPU output rows of each unit against the
+    oracle's, over all the units, and whether they meet the tolerance."""
+    import numpy as np
+
+    max_abs, sum_abs, count, worst = 0.0, 0.0, 0, None
+    for (b, h), ref in refs.items():
+        d = np.abs(got[b, h * G:(h + 1) * G].astype(np.float64) - ref)
+        if float(d.max()) >= max_abs:
+            max_abs, worst = float(d.max()), [b, h]
+        sum_abs += float(d.sum())
+        count += d.size
+    mean = sum_abs / max(count, 1)
+    return {"units": len(refs), "max_abs_err": max_abs, "mean_abs_err": mean, "worst_unit": worst,
+            "ok": bool(max_abs <= CHECK_TOL["max_abs"] and mean <= CHECK_TOL["mean_abs"]),
+            "reference": what}
+
+
+def rel_l2_units(got, refs, G):
+    """Relative L2 error of the GPU rows of the units against ``refs`` (one
+    norm over all of them)."""
+    import numpy as np
+
+    num = den = 0.0
+    for (b, h), ref in refs.items():
+        g = got[b, h * G:(h + 1) * G].astype(np.float64)
+        num += float(((g - ref) ** 2).sum())
+        den += float((ref.astype(np.float64) ** 2).sum())
+    return (num / max(den, 1e-300)) ** 0.5
+
+
+# the sampled (batch row, kv head) units of the Llama-3-8B-shape legs
+LLAMA_UNITS = [(b, (5 * b) % 8) for b in range(0, 32, 4)]
+
+
+def llama_leg_check(got, q, kq, vq, truth):
+    """Check of one Llama-3-8B-shape leg on its first cache copy: the sampled
+    units against the oracle, plus the end-to-end rel-L2 against fp32
+    attention over the unquantized K/V next to the fp16 dequant baseline's
+    (``truth``: the units' reference rows)."""
+    G = q.shape[1] // kq.packed.shape[1]
+    chk = unit_check(got, unit_refs(q, kq, vq, LLAMA_UNITS), G,
+                     "oracle fp32 dequantise-then-attend, sampled units")
+    chk["kernel_rel_l2_vs_fp16_truth"] = round(rel_l2_units(got, truth, G), 5)
+    chk["fp16_baseline_rel_l2_vs_fp16_truth"] = round(rel_l2_units(
+        _stack(unit_refs(q, kq, vq, LLAMA_UNITS, fp16_dequant=True), q.shape), truth, G), 5)
+    return chk
+
+
+def _stack(refs, shape):
+    """Unit rows back into a (B, HQ, D) array (zeros elsewhere)."""
+    import numpy as np
+
+    B, HQ, D = shape
+    out = np.zeros((B, HQ, D), np.float32)
+    for (b, h), r in refs.items():
+        g = r.shape[0]
+        out[b, h * g:(h + 1) * g] = r
+    return out
+
+
+def qwen_snapshot(ctxs=(512, 2048, 8192, 16384), seeds=(0, 1, 2)):
+    """The reference's correctness snapshot (``benchmark.py:1050-1110``) on the
+    Qwen2.5-1.5B shape: per (ctx, nbits) and seeds 0-2, the reference's own
+    inputs (``make_random_kv``: N(0,1) with 1% x8 outliers), quantized on the
+    GPU and decoded with the default plan the table times; kernel against the
+    fp32 dequantise-then-attend oracle (max/mean abs, rel-L2, cosine), and
+    end-to-end rel-L2 against fp32 attention over the fp16 K/V, for the kernel
+    and for the fp16 dequant baseline.  The fp16 control is checked against the
+    same truth.  ``published`` holds the reference's table
+    (``README.md:286-295``): rel-L2 vs fp16 truth, kernel / baseline."""
+    import numpy as np
+    import torch
+
+    from oracle import attention as oatt
+    from oracle import inputs as oinp
+    from tritonkv_amd.kernels import fp16_decode_attention, fused_decode_attention
+    from tritonkv_amd.quantize import quantize_kv
+
+    published = {(512, 4): (0.1207, 0.1208), (2048, 4): (0.1396, 0.1397),
+                 (8192, 4): (0.1251, 0.1249), (16384, 4): (0.1509, 0.1514),
+                 (512, 2): (0.6558, 0.6560), (2048, 2): (0.8110, 0.8105),
+                 (8192, 2): (0.6589, 0.6585), (16384, 2): (0.7560, 0.7557)}
+    B, HQ, HKV, D = 1, 12, 2, 128
+    units = [(0, 0), (0, 1)]
+    rows, ctrl = [], []
+    for S in ctxs:
+        ctrl_max = 0.0
+        for nbits in (4, 2):
+            per = []
+            for seed in seeds:
+                q, k, v = oinp.make_random_kv(B, HQ, HKV, S, D, seed=seed)
+                qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+                kq, vq = quantize_kv(kd, vd, nbits, 32)
+                got = fused_decode_attention(qd, kq, vq).cpu().numpy()
+                ref = _stack(unit_refs(qd, kq, vq, units), q.shape)
+                base = _stack(unit_refs(qd, kq, vq, units, fp16_dequant=True), q.shape)
+                truth = _stack(truth_refs(qd, kd, vd, units), q.shape)
+                m = oatt.metrics(got, ref)
+                per.append({"seed": seed, "max_abs_err": m["max_abs_err"],
+                            "mean_abs_err": m["mean_abs_err"], "rel_l2": m["rel_l2"],
+                            "cosine": m["cosine"],
+                            "kernel_rel_l2_vs_fp16_truth": oatt.metrics(got, truth)["rel_l2"],
+                            "baseline_rel_l2_vs_fp16_truth": oatt.metrics(base, truth)["rel_l2"]})
+                if nbits == 4:  # the control on the same inputs, once per seed
+                    gc = fp16_decode_attention(qd, kd, vd).cpu().numpy()
+                    ctrl_max = max(ctrl_max, oatt.metrics(gc, truth)["max_abs_err"])
+                del qd, kd, vd, kq, vq
+            mean = lambda key: float(np.mean([p[key] for p in per]))
+            pub = published.get((S, nbits))
+            rows.append({
+                "ctx": S, "nbits": nbits, "seeds": per,
+                "max_abs_err": max(p["max_abs_err"] for p in per),
+                "mean_abs_err": max(p["mean_abs_err"] for p in per),
+                "min_cosine": min(p["cosine"] for p in per),
+                "mean_kernel_rel_l2_vs_fp16_truth": round(mean("kernel_rel_l2_vs_fp16_truth"), 5),
+                "mean_baseline_rel_l2_vs_fp16_truth": round(mean("baseline_rel_l2_vs_fp16_truth"), 5),
+                "published_kernel_baseline_rel_l2": pub,
+                "ok": bool(max(p["max_abs_err"] for p in per) <= CHECK_TOL["max_abs"]
+                           and max(p["mean_abs_err"] for p in per) <= CHECK_TOL["mean_abs"])})
+            print(f"# qwen snapshot ctx={S} {nbits}-bit: max abs {rows[-1]['max_abs_err']:.2e}, "
+                  f"rel-L2 vs fp16 truth {rows[-1]['mean_kernel_rel_l2_vs_fp16_truth']} "
+                  f"(published {pub})", file=sys.stderr, flush=True)
+        ctrl.append({"ctx": S, "max_abs_err_vs_fp32_attention": ctrl_max,
+                     "ok": bool(ctrl_max <= CHECK_TOL["max_abs"])})
+        torch.cuda.empty_cache()
+    return {"fused": rows, "fp16_control": ctrl,
+            "inputs": "oracle.inputs.make_random_kv (the reference's generator: N(0,1), "
+                      "1% of values x8), seeds 0-2; units: both kv heads"}
+
+
 def cpu_config1(reps=50):
     """the reference's CPU decode step at the Qwen shape,
     ctx 512 -- dequantise K, V (4-bit gs32) to fp32, then fp32 attention -- as
@@ -585,7 +786,7 @@ def cpu_config1(reps=50):
 # ---------------------------------------------------------------------------
 
 
-def ragged_70b(steps, warmup, seed=2024):
+def ragged_70b(steps, warmup, seed=2024, check=False):
     """B=64, HQ=64, HKV=8, D=128; per-sequence length S_b ~ U[1024, 131072]
     (seeded); K 4-bit / V 2-bit, group 32; inputs from
     ``tritonkv_amd.synthetic.ragged_batch`` (the full-size GPU parity test's).
@@ -632,6 +833,14 @@ def ragged_70b(steps, warmup, seed=2024):
     fus, _, _ = timed_steps([fused_step], steps, warmup)
     nus, _, _ = timed_steps([decode_natural], steps, warmup)
     total = decode_bytes + append_bytes
+    if check:  # out: the last timed call's decode over S_b + 1 tokens
+        lh = lens1.cpu()
+        rows = sorted({int(lh.argmax()), int(lh.argmin()), 0, 17, 33, 50})
+        units = [(b, b % HKV) for b in rows]
+        chk = unit_check(out.cpu().numpy(), unit_refs(q, kc, vc, units, lens=lh), HQ // HKV,
+                         "oracle fp32 dequantise-then-attend (K 4-bit, V 2-bit), rows of "
+                         "the longest and shortest sequences among the sampled units")
+        chk["row_lengths"] = [int(lh[b]) for b in rows]
     res = {"us_per_step": round(us, 2), "decode_us": round(dus, 2),
            "append_us": round(us - dus, 2), "fused_append_step_us": round(fus, 2),
            "decode_us_natural_order": round(nus, 2),
@@ -641,6 +850,8 @@ def ragged_70b(steps, warmup, seed=2024):
            "frac_of_hbm_peak_step": round(total / us / 1e3 / HBM_PEAK_GBS, 4),
            "frac_of_hbm_peak_decode": round(decode_bytes / dus / 1e3 / HBM_PEAK_GBS, 4),
            "lengths": "S_b ~ U[1024, 131072], torch.Generator().manual_seed(%d)" % seed}
+    if check:
+        res["check"] = chk
     print(f"# ragged 70b K4/V2: step {us:.1f} us (decode {dus:.1f} us, natural order "
           f"{nus:.1f} us, fused append+decode {fus:.1f} us), {total / us / 1e3:.0f} GB/s",
           file=sys.stderr, flush=True)
@@ -649,7 +860,31 @@ def ragged_70b(steps, warmup, seed=2024):
     return res
 
 
-def channel_keys(steps, warmup, B=32, HQ=32, HKV=8, S=32768, D=128, window=16):
+def channel_unit_check(out, q, ck, vq, kr, vr, S, window, units=((0, 0), (9, 3), (21, 5), (31, 7))):
+    """The per-channel step's output on sampled units against the oracle
+    (``oracle/channel.py``: per-channel keys and per-token values dequantized,
+    then the fp16 window, fp32 attention)."""
+    from oracle import channel as och
+
+    G = q.shape[1] // ck.packed.shape[1]
+    qf = q.float().cpu().numpy()
+    refs = {}
+    for b, h in units:
+        ckn = och.ChannelKeysNP(_host_rows(ck.packed, b, h)[None, None],
+                                _host_rows(ck.scale, b, h)[None, None],
+                                _host_rows(ck.zero, b, h)[None, None], ck.nbits, 32, ck.head_dim)
+        vqn = _qnp(vq, b, h)
+        vqn.packed, vqn.scale, vqn.zero = vqn.packed[None, None], vqn.scale[None, None], \
+            vqn.zero[None, None]
+        kk, vv, _ = och.history(ckn, vqn, _host_rows(kr, b, h)[None, None],
+                                _host_rows(vr, b, h)[None, None], [S], [window])
+        refs[(b, h)] = _attend(qf[b, h * G:(h + 1) * G], kk[0, 0], vv[0, 0])
+    return unit_check(out.cpu().numpy(), refs, G, "oracle per-channel keys + per-token values "
+                      "+ fp16 window, fp32 attention, sampled units")
+
+
+def channel_keys(steps, warmup, B=32, HQ=32, HKV=8, S=32768, D=128, window=16,
+                 check=False):
     """Per-channel (KIVI-style) keys at the Llama-3-8B shape: keys quantized per
     (32-token block, channel), values per token (group 32), a 16-token fp16
     window; one step = split kernel (per-channel key path) + fp16 window split
@@ -680,11 +915,11 @@ def channel_keys(steps, warmup, B=32, HQ=32, HKV=8, S=32768, D=128, window=16):
 
             def step(q=q, ck=ck, vq=vq, kr=kr, vr=vr, ql=ql, rl=rl, out=out, ws=ws):
                 channel_decode_attention(q, ck, vq, kr, vr, q_lens=ql, res_lens=rl, out=out,
-                                         _workspace=ws)
+                                         _workspace=ws, equal_lengths=True)
             step()
             calls.append(step)
             if c == 0:
-                first = (q, k, v, ck, vq)
+                first = (q, k, v, ck, vq, kr, vr, out)
             else:
                 del k, v
         us, _, _ = timed_steps(calls, steps, warmup)
@@ -695,7 +930,9 @@ def channel_keys(steps, warmup, B=32, HQ=32, HKV=8, S=32768, D=128, window=16):
                  "gbps_step": round(nbytes / us / 1e3, 1),
                  "frac_of_hbm_peak_step": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
         # accuracy, batch rows 0-3
-        q, k, v, ck, vq = first
+        q, k, v, ck, vq, kr, vr, out0 = first
+        if check:
+            entry["check"] = channel_unit_check(out0, q, ck, vq, kr, vr, S, window)
         r = slice(0, 4)
         kf, vf = k[r].float(), v[r].float()
         codes = unpack_codes(ck.packed[r], nb, D).float()
@@ -739,11 +976,16 @@ def channel_keys(steps, warmup, B=32, HQ=32, HKV=8, S=32768, D=128, window=16):
 # ---------------------------------------------------------------------------
 
 
-def qwen_table(ctxs=(512, 2048, 8192, 16384)):
+def qwen_table(ctxs=(512, 2048, 8192, 16384), check=False):
+    """The Qwen2.5-1.5B batch-1 table (configs 2 and 3): hot and cold µs per
+    call of each method at each context; with ``check``, each row also
+    carries the check of its first cache copy's output (both kv heads):
+    against the oracle's fp32 dequantise-then-attend (fused), or fp32
+    attention over the fp16 K/V (fp16 control, torch)."""
     import torch
 
     from tritonkv_amd.quantize import QuantizedTensor, quantize_groupwise
-    from tritonkv_amd.timing import replicas_for
+    from tritonkv_amd.timing import per_call, replicas_for
 
     B, HQ, HKV, D, gs = 1, 12, 2, 128, 32
     rows = []
@@ -780,14 +1022,33 @@ def qwen_table(ctxs=(512, 2048, 8192, 16384)):
                     calls.append(fused_call(q, ki, vi))
             if method == "fused4":
                 ns_fused4 = calls[0].num_splits
-            hot = per_call_us([calls[0]] * 50)
-            cold = per_call_us(calls)
+            hot_t = per_call([calls[0]] * 50)
+            cold_t = per_call(calls)
+            hot, cold = hot_t.us, cold_t.us
             rows.append({"ctx": S, "method": method, "cache_bytes": cache, "replicas": R,
                          "splits": calls[0].num_splits,
                          "hot_us": round(hot, 3), "cold_us": round(cold, 3),
                          "cold_gbps": round(step_bytes / cold / 1e3, 1),
                          "cold_frac_of_hbm_peak": round(step_bytes / cold / 1e3 / HBM_PEAK_GBS, 4),
-                         "hot_effective_gbps": round(step_bytes / hot / 1e3, 1)})
+                         "hot_effective_gbps": round(step_bytes / hot / 1e3, 1),
+                         "warmup": {"hot_replays": hot_t.warmup_replays,
+                                    "hot_s": round(hot_t.warmup_s, 3),
+                                    "cold_replays": cold_t.warmup_replays,
+                                    "cold_s": round(cold_t.warmup_s, 3)}})
+            if check:
+                units = [(0, 0), (0, 1)]
+                c0 = calls[0]
+                if method.startswith("fused"):
+                    got = c0.keep[0].cpu().numpy()
+                    refs = unit_refs(c0.keep[5], c0.keep[6], c0.keep[7], units)
+                    what = "oracle fp32 dequantise-then-attend"
+                else:
+                    got = (c0() if method == "torch_fp16" else c0.keep[0]).float().cpu().numpy()
+                    qq, kk, vv = (q, c0.keep[1].transpose(-1, -2), c0.keep[2]) \
+                        if method == "torch_fp16" else (q, c0.keep[6], c0.keep[7])
+                    refs = truth_refs(qq, kk, vv, units)
+                    what = "fp32 attention over the fp16 K/V"
+                rows[-1]["check"] = unit_check(got, refs, HQ // HKV, what)
             print(f"# qwen ctx={S} {method}: hot {hot:.2f} us  cold {cold:.2f} us  (R={R})",
                   file=sys.stderr, flush=True)
             del calls
@@ -811,7 +1072,59 @@ def qwen_table(ctxs=(512, 2048, 8192, 16384)):
     return {"rows": rows, "effects": effects}
 
 
-def qwen_serving_steps(ctxs=(2048, 16384)):
+def qwen_eager(ctxs=(512, 2048, 8192, 16384), check=False):
+    """Eager per-call latency at the Qwen2.5-1.5B shape (B=1, 4-bit gs32, one
+    cache): ``fused_decode_attention`` / ``fp16_decode_attention`` called from
+    Python with no graph, back to back (the reference's pipelined timing,
+    ``benchmark.py:532-553``), next to the same Python call replayed from a
+    graph; ``launch_overhead_us`` = eager - graph (``:1542-1545``).
+    ``host_us`` is what issuing one call costs the host (validation, split
+    plan, argument block, ctypes): while it exceeds the GPU time of a call the
+    eager stream waits on Python."""
+    import torch
+
+    from tritonkv_amd.kernels import fp16_decode_attention, fused_decode_attention
+    from tritonkv_amd.quantize import quantize_kv
+    from tritonkv_amd.timing import eager_per_call, per_call
+
+    B, HQ, HKV, D, gs = 1, 12, 2, 128, 32
+    res = {}
+    for S in ctxs:
+        g = torch.Generator(device="cuda").manual_seed(3000 + S)
+        q = torch.randn(B, HQ, D, device="cuda", generator=g, dtype=torch.float16)
+        k = torch.randn(B, HKV, S, D, device="cuda", generator=g, dtype=torch.float16)
+        v = torch.randn(B, HKV, S, D, device="cuda", generator=g, dtype=torch.float16)
+        kq, vq = quantize_kv(k, v, 4, gs)
+        row = {}
+        for name, fn in (("fused4", lambda o, w: fused_decode_attention(q, kq, vq, out=o,
+                                                                       _workspace=w)),
+                         ("fp16", lambda o, w: fp16_decode_attention(q, k, v, out=o,
+                                                                     _workspace=w))):
+            out, ws = torch.empty(B, HQ, D, device="cuda"), {}
+            call = lambda fn=fn, out=out, ws=ws: fn(out, ws)  # noqa: E731
+            call()
+            e = eager_per_call(call)
+            gr = per_call([call] * 50).us
+            row[name] = {"eager_us": round(e.us, 3), "graph_us": round(gr, 3),
+                         "launch_overhead_us": round(e.us - gr, 3),
+                         "host_us_per_call": round(e.host_us, 3)}
+            if check:
+                units = [(0, 0), (0, 1)]
+                refs = (unit_refs(q, kq, vq, units) if name == "fused4"
+                        else truth_refs(q, k, v, units))
+                row[name]["check"] = unit_check(out.cpu().numpy(), refs, HQ // HKV,
+                                                "oracle (as the Qwen table)")
+        res[str(S)] = row
+        print(f"# qwen eager ctx={S}: fused4 {row['fused4']['eager_us']} us eager vs "
+              f"{row['fused4']['graph_us']} graph (host {row['fused4']['host_us_per_call']} us); "
+              f"fp16 {row['fp16']['eager_us']} vs {row['fp16']['graph_us']}",
+              file=sys.stderr, flush=True)
+        del kq, vq, k, v
+        torch.cuda.empty_cache()
+    return res
+
+
+def qwen_serving_steps(ctxs=(2048, 16384), check=False):
     """A whole decode step at the Qwen2.5-1.5B shape (B=1, 4-bit gs32, one
     cache): append the new token's K and V, then attend over it -- as three
     launches (two appends + decode) and as one (the append fused into the split
@@ -850,6 +1163,10 @@ def qwen_serving_steps(ctxs=(2048, 16384)):
         t1 = per_call_us([one] * 50)
         res[str(S)] = {"three_launches_us": round(t3, 3), "fused_us": round(t1, 3),
                        "speedup": round(t3 / t1, 3)}
+        if check:  # the fused step's output over the cache its own append wrote
+            res[str(S)]["check"] = unit_check(
+                out.cpu().numpy(), unit_refs(q, kq, vq, [(0, 0), (0, 1)]), HQ // HKV,
+                "oracle fp32 dequantise-then-attend over the cache after the fused append")
         print(f"# qwen serving step ctx={S}: append+append+decode {t3:.2f} us, fused {t1:.2f} us",
               file=sys.stderr, flush=True)
         del kq, vq
@@ -857,7 +1174,7 @@ def qwen_serving_steps(ctxs=(2048, 16384)):
     return res
 
 
-def qwen_e2e(ctxs=(8192, 32768), B=16, steps=8, seed=11):
+def qwen_e2e(ctxs=(8192, 32768), B=16, steps=8, seed=11, check=False):
     """End-to-end decode tokens/s of a random-initialised Qwen2.5-1.5B-architecture
     model (transformers, fp16 weights, 28 layers, HQ=12, HKV=2, D=128) at batch B
     with the cache pre-filled to ctx tokens of synthetic K/V: stock transformers
@@ -898,7 +1215,7 @@ def qwen_e2e(ctxs=(8192, 32768), B=16, steps=8, seed=11):
 
     with torch.no_grad():
         for L in ctxs:
-            row = {}
+            row, logits = {}, {}
             for name in ("stock_sdpa", "tkv_fp16", "tkv_4bit", "tkv_2bit_channel"):
                 if name == "stock_sdpa":
                     model.set_attn_implementation("sdpa")
@@ -913,11 +1230,12 @@ def qwen_e2e(ctxs=(8192, 32768), B=16, steps=8, seed=11):
                 pos = torch.full((B, 1), L, dtype=torch.long, device="cuda")
 
                 def step():
-                    model(input_ids=ids, position_ids=pos, past_key_values=cache, use_cache=True,
-                          logits_to_keep=1)
+                    lg = model(input_ids=ids, position_ids=pos, past_key_values=cache,
+                               use_cache=True, logits_to_keep=1).logits
                     pos.add_(1)
+                    return lg
 
-                step()  # warm-up
+                logits[name] = step()[:, -1].float()  # warm-up; every variant's first step
                 entry = {"eager_us": round(timed(step, steps), 1)}
                 if name != "stock_sdpa":
                     try:
@@ -935,6 +1253,20 @@ def qwen_e2e(ctxs=(8192, 32768), B=16, steps=8, seed=11):
                       flush=True)
                 del cache
                 torch.cuda.empty_cache()
+            if check:  # first decode step's logits against stock transformers (SDPA)
+                ref = logits["stock_sdpa"]
+                chk = {}
+                for name in ("tkv_fp16", "tkv_4bit", "tkv_2bit_channel"):
+                    d = logits[name] - ref
+                    chk[name] = {"logits_rel_l2_vs_stock": round(float(d.norm() / ref.norm()), 5),
+                                 "top1_agreement": round(float((logits[name].argmax(-1) ==
+                                                                ref.argmax(-1)).float().mean()), 4)}
+                # the fp16 control attends in fp32 over the same fp16 cache as SDPA
+                chk["ok"] = bool(chk["tkv_fp16"]["logits_rel_l2_vs_stock"] < 1e-2)
+                chk["reference"] = ("stock transformers (SDPA, DynamicCache) on the same weights "
+                                    "and pre-filled cache; only the fp16 control is held to a "
+                                    "bound (rel-L2 < 1e-2), the quantized rows are recorded")
+                row["check"] = chk
             row["speedup_4bit_vs_fp16_control"] = round(
                 row["tkv_4bit"]["tokens_per_s"] / row["tkv_fp16"]["tokens_per_s"], 3)
             row["speedup_4bit_vs_stock"] = round(
@@ -1259,17 +1591,60 @@ def main() -> int:
                                          "frac_of_hbm_peak": round(ceiling4 / HBM_PEAK_GBS, 4),
                                          "kernel_frac_of_ceiling": round(probe_us4 / split_us4, 4)},
                         "clocks": clocks_split4}
-    cpu, check = None, None
-    if not a.quick and not a.no_cpu_baseline:
-        q0, kq0, vq0 = copies4[0]
-        got0 = steps4[0].keep[0].cpu().numpy()  # copy 0's output of the last timed replay
+    cpu, checks, truth = None, {}, None
+    q0, kq0, vq0 = copies4[0]
+    got0 = steps4[0].keep[0].cpu().numpy()  # copy 0's output of the last timed replay
+    checking = not a.quick and not a.no_cpu_baseline
+    if checking:
         cpu, check = cpu_baseline(q0, kq0, vq0, got0)
         print(f"# cpu baseline {cpu['value'] / 1e3:.0f} ms/step on {cpu['cores']} threads; "
               f"check vs oracle: max abs {check['max_abs_err']:.2e}, mean abs "
               f"{check['mean_abs_err']:.2e} over {check['units']} units", file=sys.stderr,
               flush=True)
         cpu["config1_reference_cpu_step"] = cpu_config1()
+        # end-to-end: fp32 attention over copy 0's unquantized K/V, sampled units
+        qt, kt, vt = llama_inputs(seed=10)
+        truth = truth_refs(qt, kt, vt, LLAMA_UNITS)
+        del qt, kt, vt
+        G4 = HQ // HKV
+        check["kernel_rel_l2_vs_fp16_truth"] = round(rel_l2_units(got0, truth, G4), 5)
+        check["fp16_baseline_rel_l2_vs_fp16_truth"] = round(rel_l2_units(
+            _stack(unit_refs(q0, kq0, vq0, LLAMA_UNITS, fp16_dequant=True), q0.shape), truth,
+            G4), 5)
+        checks["llama_fused4"] = check
     del steps4, split4
+    if not a.quick:
+        # the headline step with every row's length passed as seq_lens: with
+        # equal_lengths the unragged plan (the headline's), without it the
+        # ragged rule's two pieces per row
+        from tritonkv_amd.kernels import fused_decode_attention
+
+        lens = torch.full((B,), S, dtype=torch.int32, device="cuda")
+        eq = {}
+        for key, flag in (("equal_lengths", True), ("ragged_plan", False)):
+            calls = []
+            for q, kq, vq in copies4:
+                out, ws = torch.empty(B, HQ, D, device="cuda"), {}
+
+                def f(q=q, kq=kq, vq=vq, out=out, ws=ws, flag=flag):
+                    fused_decode_attention(q, kq, vq, seq_lens=lens, equal_lengths=flag,
+                                           out=out, _workspace=ws)
+                f()  # workspace allocated outside the captured graph
+                f.out = out
+                calls.append(f)
+            t, _, _ = timed_steps(calls, a.steps, a.warmup)
+            eq[key] = {"us_per_step": round(t, 2), "vs_no_seq_lens": round(t / us4, 4)}
+            if key == "equal_lengths" and checking:
+                same = bool((calls[0].out.cpu().numpy() == got0).all())
+                checks["llama_equal_lens"] = {"bitwise_equal_to_no_seq_lens_step": same,
+                                              "ok": same,
+                                              "reference": "the headline step without seq_lens"}
+            del calls
+        eq["no_seq_lens_us"] = round(us4, 2)
+        detail["llama_equal_lens"] = eq
+        print(f"# llama 4-bit, equal seq_lens: {eq['equal_lengths']['us_per_step']} us with "
+              f"equal_lengths, {eq['ragged_plan']['us_per_step']} us with the ragged plan, "
+              f"{us4:.2f} us without seq_lens", file=sys.stderr, flush=True)
     torch.cuda.empty_cache()
     if not a.quick:
         # the same step over page pools in shuffled page order (serving layout)
@@ -1280,7 +1655,15 @@ def main() -> int:
                 kp, table = to_pool(kq, page, seed=100 + i)
                 vp, _ = to_pool(vq, page, seed=100 + i)
                 pools.append((q, kp, vp, table))
-            us, _, _ = timed_steps([paged_call(*p) for p in pools], a.steps, a.warmup)
+            pcalls = [paged_call(*p) for p in pools]
+            us, _, _ = timed_steps(pcalls, a.steps, a.warmup)
+            if checking:  # the paged step reads the same tokens: bit-identical output
+                gp = pcalls[0].keep[0].cpu().numpy()
+                checks[f"paged4_page{page}"] = {
+                    "bitwise_equal_to_contiguous_step": bool((gp == got0).all()),
+                    "ok": bool((gp == got0).all()),
+                    "reference": "the contiguous headline step's output on the same tokens"}
+            del pcalls
             sp, _, sps = timed_steps([paged_call(*p, split_only=True) for p in pools], a.steps,
                                      a.warmup)
             detail["paged4"][f"page{page}"] = {
@@ -1300,7 +1683,16 @@ def main() -> int:
             cps = build_copies(nbits, g_s)
             cache, nbytes = algorithmic_bytes(B, HQ, HKV, S, D, nbits, nbits, g_s)
             mk = fp16_call if nbits == 16 else fused_call
-            us, _, _ = timed_steps([mk(*c) for c in cps], a.steps, a.warmup)
+            lcalls = [mk(*c) for c in cps]
+            us, _, _ = timed_steps(lcalls, a.steps, a.warmup)
+            if checking:
+                got = lcalls[0].keep[0].cpu().numpy()
+                if nbits == 16:
+                    checks[name] = unit_check(got, truth, HQ // HKV,
+                                              "fp32 attention over the fp16 K/V, sampled units")
+                else:
+                    checks[name] = llama_leg_check(got, *cps[0], truth)
+            del lcalls
             sp, _, sps = timed_steps([mk(*c, split_only=True) for c in cps], a.steps, a.warmup)
             detail[name] = {"us_per_step": round(us, 2), "split_kernel_us": round(sp, 2),
                             "cache_bytes": cache, "algorithmic_bytes": nbytes,
@@ -1318,11 +1710,28 @@ def main() -> int:
         detail["quant_effect_4b"] = round(detail["fp16"]["us_per_step"] / us4, 3)
         detail["quant_effect_2b"] = round(detail["fp16"]["us_per_step"] / detail["fused2"]["us_per_step"], 3)
         detail["empty_graph_node_us"] = round(empty_kernel_floor(), 2)
-        detail["qwen2.5-1.5b"] = qwen_table()
-        detail["qwen2.5-1.5b_serving_step"] = qwen_serving_steps()
-        detail["qwen2.5-1.5b_e2e_decode"] = qwen_e2e()
-        detail["ragged_70b_k4v2"] = ragged_70b(a.steps, a.warmup)
-        detail["channel_keys"] = channel_keys(a.steps, a.warmup)
+        detail["qwen2.5-1.5b"] = qwen_table(check=checking)
+        detail["qwen2.5-1.5b_eager"] = qwen_eager(check=checking)
+        detail["qwen2.5-1.5b_serving_step"] = qwen_serving_steps(check=checking)
+        detail["qwen2.5-1.5b_e2e_decode"] = qwen_e2e(check=checking)
+        detail["ragged_70b_k4v2"] = ragged_70b(a.steps, a.warmup, check=checking)
+        detail["channel_keys"] = channel_keys(a.steps, a.warmup, check=checking)
+        if checking:
+            # one check record per timed leg, gathered from the legs
+            checks["qwen_table"] = {f"{r['ctx']}/{r['method']}": r.pop("check")
+                                    for r in detail["qwen2.5-1.5b"]["rows"]}
+            checks["qwen_eager"] = {f"{S_}/{m}": row[m].pop("check")
+                                    for S_, row in detail["qwen2.5-1.5b_eager"].items()
+                                    for m in ("fused4", "fp16")}
+            checks["qwen_serving_step"] = {S_: r.pop("check") for S_, r in
+                                           detail["qwen2.5-1.5b_serving_step"].items()}
+            checks["qwen_e2e"] = {L_: r.pop("check") for L_, r in
+                                  detail["qwen2.5-1.5b_e2e_decode"]["ctx"].items()}
+            checks["ragged_70b_k4v2"] = detail["ragged_70b_k4v2"].pop("check")
+            checks["channel_keys"] = {k_: e.pop("check") for k_, e in
+                                      detail["channel_keys"].items()}
+            # the reference's own snapshot: its inputs, seeds 0-2, every (ctx, nbits)
+            checks["qwen_reference_snapshot"] = qwen_snapshot()
 
     line = {
         "metric": METRIC,
@@ -1352,7 +1761,8 @@ def main() -> int:
                      "read_ceiling_gbps": round(ceiling4, 1),
                      "frac_of_read_ceiling": round(probe_us4 / split_us4, 4)},
         "cpu_baseline": cpu,
-        "check": check,
+        "check": checks or None,
+        "check_ok": all(c.get("ok", True) for c in _check_leaves(checks)) if checks else None,
         "warmup_replays": warm4[0],
         "warmup_s": round(warm4[1], 3),
         "clocks": clocks4,
@@ -1362,6 +1772,19 @@ def main() -> int:
         _CLOCKS.stop()
     print(json.dumps(line))
     return 0
+
+
+def _check_leaves(checks):
+    """Every check record (a dict carrying "ok") of the nested check field."""
+    if isinstance(checks, dict):
+        if "ok" in checks:
+            yield checks
+        else:
+            for v in checks.values():
+                yield from _check_leaves(v)
+    elif isinstance(checks, list):
+        for v in checks:
+            yield from _check_leaves(v)
 
 
 def compare(paths) -> int:

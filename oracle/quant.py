@@ -129,6 +129,18 @@ def dequantize_groupwise(qt: QuantNP) -> np.ndarray:
     return out.reshape(*codes.shape[:-1], qt.head_dim).astype(np.float32)
 
 
+def dequantize_fp16(qt: QuantNP) -> np.ndarray:
+    """The reference baseline's dequant into fp16, ``reference.py:96-108``:
+    codes, scale and zero as fp16, ``code * scale`` then ``+ zero``, each
+    operation rounded to fp16 (numpy's float16 arithmetic computes in fp32 and
+    rounds the result, as half arithmetic on the GPU does)."""
+    codes = unpack_codes(qt.packed, qt.nbits, qt.head_dim)
+    cg = codes.reshape(*codes.shape[:-1], qt.n_groups, qt.group_size).astype(np.float16)
+    with np.errstate(invalid="ignore", over="ignore"):
+        out = cg * qt.scale[..., None] + qt.zero[..., None]
+    return out.reshape(*codes.shape[:-1], qt.head_dim)
+
+
 def quantize_kv(k: np.ndarray, v: np.ndarray, nbits: int, group_size: int):
     """``quantize.py:249-256``: K and V quantized independently."""
     return quantize_groupwise(k, nbits, group_size), quantize_groupwise(v, nbits, group_size)

@@ -94,7 +94,4 @@ def make_case(B, HQ, HKV, D, S, nbits, group_size, seed, device="cuda", outlier_
 
 def fp16_baseline_rows(qnp):
     """The reference baseline's fp16 dequant (reference.py:96-108): c*s then +z, each rounded to fp16."""
-    codes = oq.unpack_codes(qnp.packed, qnp.nbits, qnp.head_dim)
-    cg = codes.reshape(*codes.shape[:-1], qnp.n_groups, qnp.group_size).astype(np.float16)
-    out = cg * qnp.scale[..., None] + qnp.zero[..., None]
-    return out.reshape(*codes.shape[:-1], qnp.head_dim)
+    return oq.dequantize_fp16(qnp)

@@ -204,6 +204,29 @@ def test_dequant_is_correctly_rounded_c_times_s_plus_z():
         assert np.array_equal(oq.dequantize_groupwise(qt).view(np.uint32), exact.view(np.uint32))
 
 
+def test_fp16_dequant_baseline_rounds_each_operation_to_fp16():
+    # reference.py:96-108 works in fp16: fl16(fl16(c*s) + z).  c*s and the sum
+    # of two fp16 values are exact in float64, so rounding them to fp16 once
+    # each (numpy's float64 -> float16 is correctly rounded) is the closed form.
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((64, 128)) * 3).astype(np.float16)
+    for nbits in (2, 4):
+        qt = oq.quantize_groupwise(x, nbits, 32)
+        codes = oq.unpack_codes(qt.packed, nbits, 128).astype(np.float64)
+        s = np.repeat(qt.scale.astype(np.float64), 32, axis=-1)
+        z = np.repeat(qt.zero.astype(np.float64), 32, axis=-1)
+        cs = (codes * s).astype(np.float16).astype(np.float64)
+        exact = (cs + z).astype(np.float16)
+        got = oq.dequantize_fp16(qt)
+        assert got.dtype == np.float16
+        assert np.array_equal(got.view(np.uint16), exact.view(np.uint16))
+        # and it differs from the fp32 dequant by at most the two fp16 roundings
+        # (half an ulp of c*s, then half an ulp of the sum)
+        f32 = oq.dequantize_groupwise(qt)
+        bound = 2.0 ** -11 * (np.abs(codes * s) + np.abs(f32)) + 2.0 ** -24
+        assert np.all(np.abs(got.astype(np.float64) - f32) <= bound)
+
+
 # ---------------------------------------------------------------------------
 # attention
 # ---------------------------------------------------------------------------

@@ -390,10 +390,12 @@ __global__ void __launch_bounds__(64) combine_small_kernel(const float* __restri
   }
 #pragma unroll
   for (int off = DQ; off < 64; off *= 2) {
-    const float mo = __shfl_xor(m, off, 64), lo = __shfl_xor(l, off, 64);
+    // the partner lane i ^ off (off = 16 or 32) through one lane swap each
+    auto partner = [&](float x) { return off == 32 ? lane_partner<true>(x) : lane_partner<false>(x); };
+    const float mo = partner(m), lo = partner(l);
     f4 ao;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) ao[e] = __shfl_xor(a[e], off, 64);
+    for (int e = 0; e < 4; ++e) ao[e] = partner(a[e]);
     const float mn = fmaxf(m, mo);
     const float al = safe_exp2_diff(m, mn), be = safe_exp2_diff(mo, mn);
     a = a * al + ao * be;

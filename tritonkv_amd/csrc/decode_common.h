@@ -183,17 +183,28 @@ __device__ void merge_and_store(const SplitParams& prm, const MergeView& mv, int
                                 int nh, int split) {
   __syncthreads();
   const int tid = threadIdx.x;
-  for (int idx = tid; idx < nh * D; idx += NW * 64) {
-    const int n = idx / D, d = idx % D;
+  // Each thread merges four consecutive dims of one head: every thread of
+  // the workgroup takes at most one item (at most 16 heads x D / 4), so the
+  // two LDS round trips (the waves' maxima, then their partials) are paid
+  // once, not once per element.
+  constexpr int DQ4 = D / 4;
+  for (int idx = tid; idx < nh * DQ4; idx += NW * 64) {
+    const int n = idx / DQ4, d = 4 * (idx % DQ4);
+    float mw[NW];
     float mstar = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) mstar = fmaxf(mstar, mv.m[w * mv.stride + n]);
-    float o = 0.0f, l = 0.0f;
+    for (int w = 0; w < NW; ++w) {
+      mw[w] = mv.m[w * mv.stride + n];
+      mstar = fmaxf(mstar, mw[w]);
+    }
+    f4 o = f4{0.f, 0.f, 0.f, 0.f};
+    float l = 0.0f;
     if (mstar != -INFINITY) {
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
-        const float f = safe_exp2_diff(mv.m[w * mv.stride + n], mstar);
-        o = fmaf(f, mv.o[w * mv.stride + n * (D + 1) + d], o);
+        const float f = safe_exp2_diff(mw[w], mstar);
+        const float* ow = mv.o + w * mv.stride + n * (D + 1) + d;
+        o = o + f4{ow[0], ow[1], ow[2], ow[3]} * f;
         l = fmaf(f, mv.l[w * mv.stride + n], l);
       }
     } else {
@@ -202,23 +213,25 @@ __device__ void merge_and_store(const SplitParams& prm, const MergeView& mv, int
       // cache); the sum keeps the NaN, as the reference's softmax would.
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
-        o += mv.o[w * mv.stride + n * (D + 1) + d];
+        const float* ow = mv.o + w * mv.stride + n * (D + 1) + d;
+        o = o + f4{ow[0], ow[1], ow[2], ow[3]};
         l += mv.l[w * mv.stride + n];
       }
     }
     const int64_t row = (int64_t)b * prm.HQ + h0 + n;
     if (prm.ns_total == 1) {
-      prm.out[row * D + d] = o / l;
+      *reinterpret_cast<f4*>(prm.out + row * D + d) = o / l;
     } else {
       const int64_t pr = row * prm.ns_total + prm.split_base + split;
       if (prm.counters) {  // read back inside this launch: see the fused combine below
-        coherent_store(prm.acc + pr * D + d, o);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) coherent_store(prm.acc + pr * D + d + e, o[e]);
         if (d == 0) {
           coherent_store(prm.maxs + pr, mstar);
           coherent_store(prm.sums + pr, l);
         }
       } else {
-        prm.acc[pr * D + d] = o;
+        *reinterpret_cast<f4*>(prm.acc + pr * D + d) = o;
         if (d == 0) {
           prm.maxs[pr] = mstar;
           prm.sums[pr] = l;

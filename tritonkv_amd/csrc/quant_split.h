@@ -1142,10 +1142,13 @@ quant_split_lds_kernel(SplitParams prm) {
   // ---- this wave's partial into its own ring region -------------------------
   WavePartial<D>& wp = *reinterpret_cast<WavePartial<D>*>(ring);
   {
-    const float lt = __shfl(oz[NG % 4], 16 * (NG / 4) + n, 64);  // the ones row
+    // Row g of the V zero-point MFMA (group g; row NG: the ones row, sum p)
+    // sits in lane 16 * (g / 4) + n, element g % 4: broadcast to every lane
+    // of column n.
+    const float lt = row_bcast(oz[NG % 4], NG / 4);
     float ozg[NG];
 #pragma unroll
-    for (int g = 0; g < NG; ++g) ozg[g] = __shfl(oz[g % 4], 16 * (g / 4) + n, 64);
+    for (int g = 0; g < NG; ++g) ozg[g] = row_bcast(oz[g % 4], g / 4);
 #pragma unroll
     for (int mv = 0; mv < NVM; ++mv) {
       const int p = VL::slice_of(mv);

@@ -127,6 +127,33 @@ __device__ __forceinline__ float xor_sum16_32(float v) {
   swap_pair<true>(a + b, a, b);
   return a + b;
 }
+// The value of lane i ^ 16 (SWAP32 = false) or i ^ 32 (true): one lane swap.
+// The builtins return the first operand with its odd rows (lanes 16-31 and
+// 48-63; for the 32-lane swap its upper half) replaced by the second
+// operand's even rows (lower half), then the second operand with the
+// exchanged rows: given v twice, the first output holds the partner's value
+// in odd rows and the second in even rows.
+template <bool SWAP32>
+__device__ __forceinline__ float lane_partner(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto s = SWAP32 ? __builtin_amdgcn_permlane32_swap(u, u, false, false)
+                        : __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const int lane = (int)(threadIdx.x & 63);
+  const bool even = SWAP32 ? lane < 32 : (lane & 16) == 0;
+  return __builtin_bit_cast(float, even ? s[1] : s[0]);
+}
+// Row R (lanes 16R .. 16R + 15) of v in every row: lane i gets v of lane
+// 16R + i % 16.  The 16-lane swap leaves rows 0 and 2 (first output) or 1
+// and 3 (second) in both rows of each pair, and the 32-lane swap then the
+// lower (first output) or upper pair in all four rows.  Two VALU swaps, no
+// LDS round trip as with ds_bpermute.
+__device__ __forceinline__ float row_bcast(float v, int R) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const uint32_t t = (R & 1) ? a[1] : a[0];
+  const auto c = __builtin_amdgcn_permlane32_swap(t, t, false, false);
+  return __builtin_bit_cast(float, (R & 2) ? c[1] : c[0]);
+}
 // The value of lane i ^ 8 (the other half of the lane's 16-lane row): DPP
 // row_ror:8.
 __device__ __forceinline__ uint32_t lane_xor8(uint32_t v) {
