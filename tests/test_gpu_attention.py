@@ -604,3 +604,60 @@ def test_read_probe_runs_over_the_split_kernels_reads(kbits, vbits, gs, waves):
         _lib.check(_lib.load().tkv_read_probe(a, _lib.stream_handle(q.device)), "read probe")
     torch.cuda.synchronize()
     assert bool((out == 7.0).all())
+
+
+def test_workspace_reuses_the_checked_argument_block():
+    """A ``_workspace`` keeps the checked argument block of its last call
+    (``_PreparedCall``); a later call with the same caches, buffers and flags
+    reuses it with its own q (and new token).  Every output must equal, bit for
+    bit, the same call without a workspace: a new q per call, ``out=None``,
+    another cache on the same workspace, a misaligned q, the fused append with
+    a new token per step, and the fp16 control."""
+    from tritonkv_amd.kernels import fp16_decode_attention, fused_decode_attention
+    from tritonkv_amd.quantize import quantize_groupwise
+
+    B, HQ, HKV, D, S = 2, 12, 2, 128, 3000
+    print("prepared-call reuse", flush=True)
+    _, k, v, kq, vq = make_case(B, HQ, HKV, D, S, 4, 32, 51)
+    g = torch.Generator().manual_seed(52)
+    ws, out = {}, torch.empty(B, HQ, D, device=DEV)
+    for i in range(4):
+        qi = (torch.randn(B, HQ, D, generator=g) * (1 + i)).half().to(DEV)
+        got = fused_decode_attention(qi, kq, vq, out=out, _workspace=ws)
+        assert got is out and "call" in ws
+        assert torch.equal(got, fused_decode_attention(qi, kq, vq)), i
+    prep = ws["call"]
+    got = fused_decode_attention(qi, kq, vq, _workspace=ws)  # out=None: a new tensor
+    assert got is not out and torch.equal(got, out)
+    _, _, _, kq2, vq2 = make_case(B, HQ, HKV, D, S, 4, 32, 53)  # another cache
+    got = fused_decode_attention(qi, kq2, vq2, out=out, _workspace=ws)
+    assert ws["call"] is not prep and torch.equal(got, fused_decode_attention(qi, kq2, vq2))
+    buf = torch.empty(B * HQ * D + 1, dtype=torch.float16, device=DEV)
+    qm = buf[1:].view(B, HQ, D)  # 2 bytes past a 16-byte boundary: the full path
+    qm.copy_(qi)
+    got = fused_decode_attention(qm, kq2, vq2, out=out, _workspace=ws)
+    assert torch.equal(got, fused_decode_attention(qi, kq2, vq2))
+    # fused append: a new token per step, on two copies of the cache
+    ka = quantize_groupwise(k.to(DEV), 4, 32)
+    va = quantize_groupwise(v.to(DEV), 4, 32)
+    kb = type(ka)(ka.packed.clone(), ka.scale.clone(), ka.zero.clone(), 4, 32, D)
+    vb = type(va)(va.packed.clone(), va.scale.clone(), va.zero.clone(), 4, 32, D)
+    ws2 = {}
+    for i in range(3):
+        lens = torch.full((B,), S - 3 + i + 1, dtype=torch.int32, device=DEV)
+        kn = torch.randn(B, HKV, D, generator=g).half().to(DEV)
+        vn = torch.randn(B, HKV, D, generator=g).half().to(DEV)
+        qi = torch.randn(B, HQ, D, generator=g).half().to(DEV)
+        got = fused_decode_attention(qi, ka, va, seq_lens=lens, k_new=kn, v_new=vn,
+                                     out=out, _workspace=ws2)
+        want = fused_decode_attention(qi, kb, vb, seq_lens=lens, k_new=kn, v_new=vn)
+        assert torch.equal(got, want), i
+    assert torch.equal(ka.packed, kb.packed) and torch.equal(va.zero, vb.zero)
+    # the fp16 control
+    kf, vf = k.to(DEV), v.to(DEV)
+    ws3 = {}
+    for i in range(3):
+        qi = torch.randn(B, HQ, D, generator=g).half().to(DEV)
+        got = fp16_decode_attention(qi, kf, vf, out=out, _workspace=ws3)
+        assert torch.equal(got, fp16_decode_attention(qi, kf, vf)), i
+    assert "call" in ws3

@@ -119,6 +119,9 @@ def test_work_order_argument_checks_without_a_gpu():
     a.acc = a.maxs = a.sums = None
     assert lib.tkv_fused_decode_attention_noalloc(ctypes.byref(a), None) == _lib.TKV_EINVAL
     a.acc = a.maxs = a.sums = dummy
+    a.D = 64  # ordered kernels exist for head dim 128 only
+    assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EUNSUPPORTED
+    a.D = 128
     a.B, a.HQ, a.HKV = 1 << 15, 1 << 15, 1 << 15  # B * HKV * num_splits = 2^32 slots
     assert lib.tkv_fused_decode_attention(ctypes.byref(a), None) == _lib.TKV_EINVAL
 
@@ -179,6 +182,7 @@ def test_order_buffer_policy():
     assert _order_for({}, 64, 8, 4, "cpu", None, None) is None     # equal lengths
     assert _order_for({}, 64, 8, 4, "cpu", lens, False) is None
     assert _order_for({}, 1, 2, 32, "cpu", lens, None) is None     # 64 workgroups fit the CUs
+    assert _order_for({}, 64, 8, 4, "cpu", lens, None, D=64) is None  # no ordered D=64 kernels
     assert _order_for({}, 1, 2, 32, "cpu", lens, None, G=256) is not None  # 16 head blocks each
     assert _order_for({}, 4096, 8, 1, "cpu", lens, None) is None   # past ORDER_MAX_ROWS
     ws = {}

@@ -670,6 +670,8 @@ static int check_fused_split(const tkv_decode_args* a, bool probe) {
   if ((a->k_nbits != 2 && a->k_nbits != 4) || (a->v_nbits != 2 && a->v_nbits != 4))
     return TKV_EINVAL;
   if (a->key_block && gs > 32) return TKV_EUNSUPPORTED;  // per-channel keys: V groups of 16 or 32
+  // ordered launches: head dim 128, per-token keys (the instantiated forms)
+  if (a->work_order && (a->D != 128 || a->key_block)) return TKV_EUNSUPPORTED;
   // the instantiated group sizes (dispatch_gs), checked before anything is launched
   if (gs != 16 && gs != 32 && gs != 64 && gs != 128) return TKV_EUNSUPPORTED;
   // codes (K, V) and fp16 scale/zero rows of one buffer range

@@ -396,7 +396,12 @@ template <int VNB, int NG>
 constexpr bool kPsRemainder = VNB == 2 && NG == 1;
 
 
-template <int D, int KNB, int VNB, int GS, int NW, int NSTAGE, bool PAGED, bool PT, bool KCH, int HS>
+// ORD: the launch carries a dispatch order (prm.order).  A separate
+// instantiation, because a run-time test of the pointer ahead of everything
+// else made the compiler fetch the cache pointers in a second, serial round
+// trip to the argument block: 0.1-0.3 us on every Qwen2.5-1.5B-shape call.
+template <int D, int KNB, int VNB, int GS, int NW, int NSTAGE, bool PAGED, bool PT, bool KCH, int HS,
+          bool ORD>
 __global__ void __launch_bounds__(NW * 64)
 quant_split_lds_kernel(SplitParams prm) {
   using SG = StageGeom<D, KNB, VNB, GS>;
@@ -428,7 +433,7 @@ quant_split_lds_kernel(SplitParams prm) {
   // x fastest: consecutive workgroups (which the dispatcher deals to the 8 XCDs
   // in turn) take other units.  A ragged batch may pass a longest-first order.
   int unit_ = blockIdx.x, split_ = blockIdx.y, L_ = 0;
-  if (prm.order) {
+  if constexpr (ORD) {
     const int2 e = reinterpret_cast<const int2*>(prm.order)[blockIdx.y * gridDim.x + blockIdx.x];
     unit_ = e.x % (int)gridDim.x;
     split_ = e.x / (int)gridDim.x;
@@ -440,8 +445,8 @@ quant_split_lds_kernel(SplitParams prm) {
   const int hb0 = blockIdx.z * 16;
   const int nh = min(16, prm.G - hb0);
   const int h0 = hk * prm.G + hb0;
-  const int L = prm.order ? __builtin_amdgcn_readfirstlane(L_)
-                          : (prm.seq_lens ? min(prm.seq_lens[b], prm.S) : prm.S);
+  const int L = ORD ? __builtin_amdgcn_readfirstlane(L_)
+                    : (prm.seq_lens ? min(prm.seq_lens[b], prm.S) : prm.S);
   const int lo = split * prm.split_size;
   const int hi = min(lo + prm.split_size, L);
   const int last = hi - 1;
@@ -1185,27 +1190,37 @@ constexpr int kStages8 = 2;  // also the ring depth of 12-wave workgroups
 static_assert(kStages8 == 2, "kTwelveWaves sizes two-stage rings");
 constexpr int kStages4 = 2;
 
-template <int D, int KNB, int VNB, int GS, bool PT, int HS>
-void launch_quant_pt(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
+template <int D, int KNB, int VNB, int GS, bool PT, int HS, bool ORD>
+void launch_quant_pto(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
   const bool paged = p.page_size > 0;
   if constexpr (kTwelveWaves<D, KNB, VNB, GS, HS, PT>) {
     if (waves == 12 && !paged) {
-      quant_split_lds_kernel<D, KNB, VNB, GS, 12, kStages8, false, PT, false, HS>
+      quant_split_lds_kernel<D, KNB, VNB, GS, 12, kStages8, false, PT, false, HS, ORD>
           <<<grid, dim3(12 * 64), 0, st>>>(p);
       return;
     }
   }
   if (waves >= 8) {
     if (paged)
-      quant_split_lds_kernel<D, KNB, VNB, GS, 8, 2, true, PT, false, HS><<<grid, dim3(8 * 64), 0, st>>>(p);
+      quant_split_lds_kernel<D, KNB, VNB, GS, 8, 2, true, PT, false, HS, ORD><<<grid, dim3(8 * 64), 0, st>>>(p);
     else
-      quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, PT, false, HS><<<grid, dim3(8 * 64), 0, st>>>(p);
+      quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, PT, false, HS, ORD><<<grid, dim3(8 * 64), 0, st>>>(p);
   } else {
     if (paged)
-      quant_split_lds_kernel<D, KNB, VNB, GS, 4, 2, true, PT, false, HS><<<grid, dim3(4 * 64), 0, st>>>(p);
+      quant_split_lds_kernel<D, KNB, VNB, GS, 4, 2, true, PT, false, HS, ORD><<<grid, dim3(4 * 64), 0, st>>>(p);
     else
-      quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false, PT, false, HS><<<grid, dim3(4 * 64), 0, st>>>(p);
+      quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false, PT, false, HS, ORD><<<grid, dim3(4 * 64), 0, st>>>(p);
   }
+}
+
+// Kernels that read a dispatch order exist for head dim 128 only (the host
+// refuses an order elsewhere, before anything is launched).
+template <int D, int KNB, int VNB, int GS, bool PT, int HS>
+void launch_quant_pt(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
+  if constexpr (D == 128) {
+    if (p.order) return launch_quant_pto<D, KNB, VNB, GS, PT, HS, true>(p, grid, waves, st);
+  }
+  launch_quant_pto<D, KNB, VNB, GS, PT, HS, false>(p, grid, waves, st);
 }
 
 // Paired tiles when the GQA group has at most 8 query heads and every
@@ -1294,16 +1309,16 @@ void launch_quant_hs(const SplitParams& p, dim3 grid, int waves, hipStream_t st)
     if (p.key_block) {  // per-channel keys (the host checked: contiguous, no fused append)
       if constexpr (kTwelveWaves<D, KNB, VNB, GS, HS, false>) {
         if (waves == 12) {
-          quant_split_lds_kernel<D, KNB, VNB, GS, 12, kStages8, false, false, true, HS>
+          quant_split_lds_kernel<D, KNB, VNB, GS, 12, kStages8, false, false, true, HS, false>
               <<<grid, dim3(12 * 64), 0, st>>>(p);
           return;
         }
       }
       if (waves >= 8)
-        quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, false, true, HS>
+        quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, false, true, HS, false>
             <<<grid, dim3(8 * 64), 0, st>>>(p);
       else
-        quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false, false, true, HS>
+        quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false, false, true, HS, false>
             <<<grid, dim3(4 * 64), 0, st>>>(p);
       return;
     }

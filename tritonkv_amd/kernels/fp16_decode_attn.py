@@ -30,7 +30,10 @@ from .fused_decode_attn import (
     _aligned16,
     _cache_arg,
     _check_out,
+    _PreparedCall,
+    _prepared,
     _seq_lens_arg,
+    _tensor_key,
     _workspace_for,
     choose_waves,
     plan_splits,
@@ -56,8 +59,19 @@ def fp16_decode_attention(
     """Decode attention on an unquantized fp16 cache, same shape as the fused kernel.
 
     q: (B, HQ, D); k, v: (B, HKV, S, D) fp16. Returns (B, HQ, D) float32.
-    ``seq_lens`` / ``equal_lengths`` as for ``fused_decode_attention``.
+    ``seq_lens`` / ``equal_lengths`` and the reuse of a workspace's checked
+    argument block as for ``fused_decode_attention``.
     """
+    key = None
+    if _workspace is not None:
+        key = ("fp16", q.shape, q.dtype, q.device, q.is_contiguous(), _tensor_key(k),
+               _tensor_key(v), sm_scale, block_n, num_splits, _tensor_key(out),
+               _tensor_key(seq_lens), equal_lengths)
+        prep = _prepared(_workspace, key)
+        if prep is not None:
+            res = prep.run(q, out)
+            if res is not None:
+                return res
     B, HQ, D = q.shape
     _, HKV, S, _ = k.shape
     if HQ % HKV != 0:
@@ -77,9 +91,11 @@ def fp16_decode_attention(
                                             TOKENS_PER_WORKGROUP_FP16,
                                             ragged=seq_lens is not None and not equal_lengths)
 
+    q_in = q
     if q.dtype not in (torch.float16, torch.float32):
         q = q.float()
     q = _aligned16(q)
+    k_in, v_in = k, v
     k = _cache_arg(k if k.dtype == torch.float16 else k.half(), 16, "k")
     v = _cache_arg(v if v.dtype == torch.float16 else v.half(), 16, "v")
     out = _check_out(out, B, HQ, D, q.device)
@@ -96,4 +112,8 @@ def fp16_decode_attention(
     with torch.cuda.device(q.device):
         rc = _lib.load().tkv_fp16_decode_attention(args, _lib.stream_handle(q.device))
     _lib.check(rc, "fp16_decode_attention")
+    # k / v are read in place; a converted copy (not fp16, not contiguous) is not kept
+    if key is not None and q is q_in and k is k_in and v is v_in:
+        _workspace["call"] = _PreparedCall(key, args, _lib.load().tkv_fp16_decode_attention,
+                                           "fp16_decode_attention", (B, HQ, D), q.device, False)
     return out

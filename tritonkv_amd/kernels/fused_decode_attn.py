@@ -252,7 +252,7 @@ ORDER_MAX_ROWS = 2048
 
 
 def _order_for(ws: dict | None, B: int, HKV: int, num_splits: int, device, seq_lens,
-               dispatch_order: bool | None, G: int = 1):
+               dispatch_order: bool | None, G: int = 1, D: int = 128):
     """The ``work_order`` buffer of a split call, or None.
 
     ``dispatch_order=None`` takes it when ``seq_lens`` is given, the batch
@@ -264,14 +264,15 @@ def _order_for(ws: dict | None, B: int, HKV: int, num_splits: int, device, seq_l
     has no tail to even out, and the order would only add its launch
     boundary (4.7-7.7 us measured ahead of the split kernel).  The output is
     bit-identical either way; ``True`` forces the order, ``False`` keeps the
-    grid order.
+    grid order.  Ordered kernels exist for head dim 128 only: elsewhere the
+    automatic order is off, and a forced one is refused (ValueError).
     """
     if dispatch_order is False:
         return None
     if dispatch_order is None:
         workgroups = B * HKV * _cdiv(G, 16) * num_splits
         if seq_lens is None or workgroups <= (compute_units(device) or 256) \
-                or B > ORDER_MAX_ROWS:
+                or B > ORDER_MAX_ROWS or D != 128:
             return None
     ws = ws if ws is not None else {}
     n = 2 * B * HKV * num_splits  # (s * B * HKV + unit, row length) pairs
@@ -354,6 +355,62 @@ def new_token_args(k_new, v_new, B: int, HKV: int, D: int, device):
     return out[0], out[1], int(out[0].dtype == torch.float32)
 
 
+def _tensor_key(t):
+    """What the argument checks and the argument block depend on for a tensor
+    the call reads in place: its storage, shape, dtype and layout."""
+    return None if t is None else (t.data_ptr(), t.shape, t.dtype, t.is_contiguous())
+
+
+def _new_key(t):
+    """The same for the new token's rows, whose storage may change every step."""
+    return None if t is None else (t.shape, t.dtype, t.is_contiguous())
+
+
+class _PreparedCall:
+    """The validated argument block of a decode call, kept in the caller's
+    ``_workspace`` under ``"call"``.  A later call whose key matches (same
+    caches, buffers, shapes and flags; q and the new token's rows may be new
+    tensors of the same shape) reuses it: only those pointers are refreshed.
+    This takes validation, the split plan and the construction of the ctypes
+    argument block (most of the ~16-20 us an eager call spent on the host)
+    off every step of a decode loop."""
+
+    __slots__ = ("key", "args", "entry", "what", "out_shape", "device", "new")
+
+    def __init__(self, key, args, entry, what, out_shape, device, new):
+        self.key, self.args, self.entry, self.what = key, args, entry, what
+        self.out_shape, self.device, self.new = out_shape, device, new
+
+    def run(self, q, out, k_new=None, v_new=None):
+        """Launch with this q (and new token); None when q does not qualify
+        (misaligned), so that the caller takes the full path."""
+        qp = q.data_ptr()
+        if qp % 16:
+            return None
+        a = self.args
+        a.q = qp
+        if self.new:
+            a.k_new, a.v_new = k_new.data_ptr(), v_new.data_ptr()
+        if out is None:
+            out = torch.empty(self.out_shape, device=self.device, dtype=torch.float32)
+            a.out = out.data_ptr()
+        if self.device.index == torch.cuda.current_device():
+            rc = self.entry(a, torch.cuda.current_stream().cuda_stream)
+        else:
+            with torch.cuda.device(self.device):
+                rc = self.entry(a, torch.cuda.current_stream().cuda_stream)
+        _lib.check(rc, self.what)
+        return out
+
+
+def _prepared(ws, key):
+    """The workspace's prepared call if its key matches, else None."""
+    if ws is None:
+        return None
+    prep = ws.get("call")
+    return prep if prep is not None and prep.key == key else None
+
+
 def fused_decode_attention(
     q: torch.Tensor,
     kq: QuantizedTensor,
@@ -386,7 +443,23 @@ def fused_decode_attention(
     workgroups (``_order_for``); the result does not depend on it.
     ``equal_lengths`` (new): every row of ``seq_lens`` holds the same length,
     so the split plan of a batch without ``seq_lens`` applies.
+    With ``_workspace``, a call like the previous one on the same workspace
+    reuses its checked argument block (``_PreparedCall``).
     """
+    key = None
+    if _workspace is not None:
+        key = ("fused", q.shape, q.dtype, q.device, q.is_contiguous(),
+               _tensor_key(kq.packed), _tensor_key(kq.scale), _tensor_key(kq.zero),
+               _tensor_key(vq.packed), _tensor_key(vq.scale), _tensor_key(vq.zero),
+               kq.nbits, vq.nbits, kq.group_size, vq.group_size, kq.head_dim, vq.head_dim,
+               sm_scale, block_n, num_splits, fold_zp, _tensor_key(out), _tensor_key(seq_lens),
+               allow_mixed_bits, fused_combine, _new_key(k_new), _new_key(v_new),
+               dispatch_order, equal_lengths)
+        prep = _prepared(_workspace, key)
+        if prep is not None:
+            res = prep.run(q, out, k_new, v_new)
+            if res is not None:
+                return res
     if kq.group_size != vq.group_size or (kq.nbits != vq.nbits and not allow_mixed_bits):
         raise ValueError("K and V must use the same nbits/group_size")
 
@@ -424,6 +497,7 @@ def fused_decode_attention(
     ragged = seq_lens is not None and not equal_lengths
     _, num_splits, split_size = plan_splits(S, block_n, num_splits, B, HKV, group, ragged=ragged)
 
+    q_in = q
     if q.dtype not in (torch.float16, torch.float32):
         q = q.float()
     q = _aligned16(q)
@@ -431,7 +505,7 @@ def fused_decode_attention(
     acc, maxs, sums, counters = _workspace_for(_workspace, B, HQ, num_splits, D, q.device, HKV)
     lens = _seq_lens_arg(seq_lens, B, S, q.device)
     order = _order_for(_workspace, B, HKV, num_splits, q.device, seq_lens if ragged else None,
-                       dispatch_order, group)
+                       dispatch_order, group, D)
 
     args = _lib.DecodeArgs(
         q=q.data_ptr(), q_is_fp32=int(q.dtype == torch.float32),
@@ -449,5 +523,11 @@ def fused_decode_attention(
     with torch.cuda.device(q.device):
         rc = _lib.load().tkv_fused_decode_attention(args, _lib.stream_handle(q.device))
     _lib.check(rc, "fused_decode_attention")
+    # q is kept as given unless it had to be converted or realigned (then no reuse)
+    if key is not None and q is q_in and kp is kq.packed and vp is vq.packed and \
+            ks is kq.scale and kz is kq.zero and vs is vq.scale and vz is vq.zero:
+        _workspace["call"] = _PreparedCall(key, args, _lib.load().tkv_fused_decode_attention,
+                                           "fused_decode_attention", (B, HQ, D), q.device,
+                                           kn is not None)
     return out
 

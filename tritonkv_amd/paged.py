@@ -177,7 +177,7 @@ def paged_decode_attention(
     acc, maxs, sums, _ = _workspace_for(_workspace, B, HQ, num_splits, D, q.device, HKV)
     lens = seq_lens.contiguous() if seq_lens is not None else None
     order = _order_for(_workspace, B, HKV, num_splits, q.device, seq_lens if ragged else None,
-                       dispatch_order, group)
+                       dispatch_order, group, D)
     args = _lib.DecodeArgs(
         q=q.data_ptr(), q_is_fp32=int(q.dtype == torch.float32),
         k=k_pool.packed.data_ptr(), k_scale=k_pool.scale.data_ptr(),
