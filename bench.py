@@ -83,6 +83,8 @@ def _args():
     ap.add_argument("--counter-summary", nargs="+", metavar="PMC_DIR", default=None,
                     help="no GPU work: per-kernel table of the SQ/GRBM counters of rocprofv3 "
                          "--pmc output directories (one per pass)")
+    ap.add_argument("--skip-dispatches", type=int, default=0,
+                    help="with --counter-summary: leave out the first N dispatches of each kernel")
     ap.add_argument("--regime-probe", choices=("hot", "cold"), default=None,
                     help="no timing: 60 eager Qwen2.5-1.5B ctx-16384 4-bit decode calls on one "
                          "cache (hot) or rotating copies >= 768 MB (cold), for rocprofv3 --pmc")
@@ -1341,9 +1343,11 @@ def kernel_probe(name, launches=6):
     return 0
 
 
-def counter_summary(dirs) -> int:
+def counter_summary(dirs, skip=0) -> int:
     """Mean value per dispatch of every counter in the --pmc directories, per
-    kernel (largest grid of each kernel name), with per-wave instruction counts."""
+    kernel (largest grid of each kernel name), with per-wave instruction counts;
+    the first ``skip`` dispatches of each kernel and counter are left out
+    (warm-up calls)."""
     rows = {}
     for d in dirs:
         for r in _csv_rows(d, "counter_collection.csv"):
@@ -1351,6 +1355,10 @@ def counter_summary(dirs) -> int:
             grid = int(r["Grid_Size"])
             ent = rows.setdefault(key, {})
             ent.setdefault((grid, r["Counter_Name"]), []).append(float(r["Counter_Value"]))
+    for ent in rows.values():
+        for k in ent:
+            if len(ent[k]) > skip:
+                ent[k] = ent[k][skip:]
     out = []
     for name, ent in rows.items():
         if "tkv::" not in name:
@@ -1505,7 +1513,7 @@ def main() -> int:
     if a.rocprof_summary:
         return rocprof_summary(a)
     if a.counter_summary:
-        return counter_summary(a.counter_summary)
+        return counter_summary(a.counter_summary, a.skip_dispatches)
     if a.kernel_probe:
         return kernel_probe(a.kernel_probe)
     if a.regime_probe:
