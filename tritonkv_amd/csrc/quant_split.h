@@ -725,6 +725,9 @@ quant_split_lds_kernel(SplitParams prm) {
   for (int mv = 0; mv < NVM; ++mv) accv[mv] = f4{0.f, 0.f, 0.f, 0.f};
   f4 oz = f4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.0f;
+  // Whether this wave has run a chunk: before its first one the accumulators
+  // are zero, and a move of the running max needs no rescale.
+  bool live = false;
   const float lscale = prm.qk_scale * __builtin_ldexpf(1.0f, 24 - eh);  // per lane (its head)
 
   // In the tail chunk, rows past the sequence hold whatever the cache holds
@@ -861,7 +864,7 @@ quant_split_lds_kernel(SplitParams prm) {
       float alpha;
       uint32_t ph[2];
       float pf[4];
-      if (softmax_chunk_pt(x, lscale, m_run, alpha, ph, pf)) {
+      if (softmax_chunk_pt(x, lscale, m_run, alpha, ph, pf) && live) {
 #pragma unroll
         for (int mv = 0; mv < NVM; ++mv) accv[mv] *= alpha;
         oz *= alpha;
@@ -1011,7 +1014,7 @@ quant_split_lds_kernel(SplitParams prm) {
       // ---- online softmax ---------------------------------------------------
       float alpha;
       ChunkProbs pr;
-      if (softmax_chunk<false>(x, lscale, m_run, l_run, alpha, pr)) {
+      if (softmax_chunk<false>(x, lscale, m_run, l_run, alpha, pr) && live) {
   #pragma unroll
         for (int mv = 0; mv < NVM; ++mv) accv[mv] *= alpha;
         oz *= alpha;
@@ -1024,6 +1027,7 @@ quant_split_lds_kernel(SplitParams prm) {
       }
     }
 
+    live = true;
     // ---- V zero point: oz += Z^T P (A rows = groups, k = the lane's 8 tokens)
     {
       uint32_t zp[4];
