@@ -456,3 +456,36 @@ def test_timing_replicas_and_warmup_floor():
     assert warmup_replays_needed(20, 10_000, 0.0045, 0.5) == 500
     # a replay longer than the floor still runs once
     assert warmup_replays_needed(20, 0, 2.0, 0.5) == 1
+
+
+def test_prepared_call_key_tracks_what_the_argument_block_depends_on():
+    """The workspace's checked argument block is reused only under an equal
+    key: a tensor's key changes with its storage address, shape, dtype and
+    layout -- also when the same tensor object is resized or restrided in
+    place -- and a workspace without a prepared call, or with another key,
+    yields none."""
+    from tritonkv_amd.kernels.fused_decode_attn import _new_key, _prepared, _tensor_key
+
+    t = torch.zeros(2, 3, 64, 16, dtype=torch.uint8)
+    k0 = _tensor_key(t)
+    assert _tensor_key(t) == k0
+    assert _tensor_key(torch.zeros_like(t)) != k0                 # another storage
+    t2 = torch.zeros(2, 3, 64, 16, dtype=torch.uint8)
+    ptr = t2.data_ptr()
+    t2.resize_(2, 3, 32, 16)                                      # same storage, new shape
+    assert t2.data_ptr() == ptr and _tensor_key(t2)[1] != k0[1]
+    v = t.view(torch.int8)
+    assert v.data_ptr() == t.data_ptr() and _tensor_key(v) != k0  # dtype view
+    tt = t.transpose(2, 3)
+    assert tt.data_ptr() == t.data_ptr() and _tensor_key(tt) != k0  # layout
+    assert _tensor_key(None) is None and _new_key(None) is None
+    assert _new_key(t) == _new_key(torch.ones_like(t))             # new rows may move
+    assert _new_key(t) != _new_key(t.half())
+
+    class Prep:
+        key = ("a", 1)
+    assert _prepared(None, ("a", 1)) is None
+    assert _prepared({}, ("a", 1)) is None
+    ws = {"call": Prep()}
+    assert _prepared(ws, ("a", 1)) is ws["call"]
+    assert _prepared(ws, ("a", 2)) is None
