@@ -178,18 +178,21 @@ __device__ __forceinline__ float coherent_load(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int D, int NW>
+// DN < D: this workgroup holds dims [d0, d0 + DN) of the output (the
+// dims-split kernels); the maxima and sums go out with dim 0's workgroup.
+// Those kernels never run the fused combine below.
+template <int D, int NW, int DN = D>
 __device__ void merge_and_store(const SplitParams& prm, const MergeView& mv, int b, int h0,
-                                int nh, int split) {
+                                int nh, int split, int d0 = 0) {
   __syncthreads();
   const int tid = threadIdx.x;
   // Each thread merges four consecutive dims of one head: every thread of
-  // the workgroup takes at most one item (at most 16 heads x D / 4), so the
+  // the workgroup takes at most one item (at most 16 heads x DN / 4), so the
   // two LDS round trips (the waves' maxima, then their partials) are paid
   // once, not once per element.
-  constexpr int DQ4 = D / 4;
+  constexpr int DQ4 = DN / 4;
   for (int idx = tid; idx < nh * DQ4; idx += NW * 64) {
-    const int n = idx / DQ4, d = 4 * (idx % DQ4);
+    const int n = idx / DQ4, d = d0 + 4 * (idx % DQ4);
     float mw[NW];
     float mstar = -INFINITY;
 #pragma unroll
@@ -239,7 +242,7 @@ __device__ void merge_and_store(const SplitParams& prm, const MergeView& mv, int
       }
     }
   }
-  if (prm.ns_total == 1 || prm.counters == nullptr) return;  // counters: split_base 0, all splits
+  if (prm.ns_total == 1 || prm.counters == nullptr || DN < D) return;  // counters: split_base 0, all splits
 
   // Fused combine.  Each workgroup publishes its partials and takes a ticket;
   // the one that draws the last ticket reads everyone's partials and merges

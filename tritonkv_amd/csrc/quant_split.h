@@ -396,12 +396,33 @@ template <int VNB, int NG>
 constexpr bool kPsRemainder = VNB == 2 && NG == 1;
 
 
+// Dims split (VS workgroups per output row): part `part` computes the V bit
+// slices [part * P / VS, (part + 1) * P / VS).  Whether V MFMA mv, and P'
+// operand v (of S-slot head columns), belong to that part.
+template <class VL, int VS>
+__device__ constexpr bool v_mfma_in_part(int mv, int part) {
+  return VL::slice_of(mv) >= part * (VL::P / VS) && VL::slice_of(mv) < (part + 1) * (VL::P / VS);
+}
+template <class VL, int VS, int S>
+__device__ constexpr bool v_operand_in_part(int v, int part) {
+  for (int mv = 0; mv < VL::NVM; ++mv)
+    if (v_mfma_in_part<VL, VS>(mv, part) && VL::group_of(mv) / S == v) return true;
+  return false;
+}
+
 // ORD: the launch carries a dispatch order (prm.order).  A separate
 // instantiation, because a run-time test of the pointer ahead of everything
 // else made the compiler fetch the cache pointers in a second, serial round
 // trip to the argument block: 0.1-0.3 us on every Qwen2.5-1.5B-shape call.
+//
+// VS: workgroups that share one (unit, split, block of heads) by splitting
+// the head dim of the output.  Workgroup z % VS computes every score (the K
+// side, the softmax) but only the V products, the partial and the merge of
+// the bit slices [P0, P1) of each V byte, i.e. dims [P0 * DP, P1 * DP): less
+// work per chunk and twice the workgroups when a launch has far fewer
+// workgroups than the GPU has CUs.
 template <int D, int KNB, int VNB, int GS, int NW, int NSTAGE, bool PAGED, bool PT, bool KCH, int HS,
-          bool ORD>
+          bool ORD, int VS>
 __global__ void __launch_bounds__(NW * 64)
 quant_split_lds_kernel(SplitParams prm) {
   using SG = StageGeom<D, KNB, VNB, GS>;
@@ -442,7 +463,9 @@ quant_split_lds_kernel(SplitParams prm) {
   const int unit = __builtin_amdgcn_readfirstlane(unit_);
   const int split = __builtin_amdgcn_readfirstlane(split_);
   const int b = unit / prm.HKV, hk = unit % prm.HKV;
-  const int hb0 = blockIdx.z * 16;
+  // z = block of 16 query heads * VS + the dims part (VS > 1)
+  const int vpart = VS > 1 ? (int)(blockIdx.z % VS) : 0;
+  const int hb0 = (VS > 1 ? (int)(blockIdx.z / VS) : (int)blockIdx.z) * 16;
   const int nh = min(16, prm.G - hb0);
   const int h0 = hk * prm.G + hb0;
   const int L = ORD ? __builtin_amdgcn_readfirstlane(L_)
@@ -460,8 +483,9 @@ quant_split_lds_kernel(SplitParams prm) {
   // leaves, with no q operands, DMA or merge.  With counters (the
   // last-workgroup merge counts every split's ticket) it takes the full path.
   if (lo >= L && prm.ns_total > 1 && prm.counters == nullptr) {
-    for (int idx = tid; idx < nh * D; idx += NW * 64) {
-      const int hn = idx / D, d = idx % D;
+    constexpr int DNV = D / VS;  // this workgroup's dims
+    for (int idx = tid; idx < nh * DNV; idx += NW * 64) {
+      const int hn = idx / DNV, d = vpart * DNV + idx % DNV;
       const int64_t pr = ((int64_t)b * prm.HQ + h0 + hn) * prm.ns_total + prm.split_base + split;
       prm.acc[pr * D + d] = 0.0f;
       if (d == 0) {
@@ -560,6 +584,8 @@ quant_split_lds_kernel(SplitParams prm) {
   for (int m = 0; m < NKM; ++m) kmask[m] = slice_mask<KNB>(KL::slice_of(m, j));
 
   constexpr bool kVChain = NPG == 1;  // every V MFMA takes the same P' operand
+  static_assert(VS == 1 || (VS == 2 && !PT && !KCH && !PAGED && !ORD && !kVChain && VL::P % 2 == 0),
+                "dims split: unpaired, per-token keys, contiguous, grid order, no slice chain");
 
   // Per-lane LDS byte offsets inside a stage.
   // K operand of tile a, load Lh: row 16a + r, byte load_offset(Lh, j).
@@ -746,9 +772,10 @@ quant_split_lds_kernel(SplitParams prm) {
 
   // Chunk k of the wave uses stage k % NSTAGE; the loop below is unrolled by
   // NSTAGE so every stage offset is a compile-time constant.
-  auto step = [&](int cb, auto tail, auto stage, auto pmode) __attribute__((always_inline)) {
+  auto step = [&](int cb, auto tail, auto stage, auto pmode, auto part) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail)::value;
     constexpr int SK = decltype(stage)::value;
+    constexpr int PART = decltype(part)::value;  // dims part (VS > 1)
     // hi/lo probabilities in the PV products (see kHiLoMaxLen)
     // Precision of the PV products (see kHiLoMaxLen and kPsRemainder): 0 fp16
     // P and P * s; 1 adds the exact remainder of each fp16 product P * s;
@@ -866,7 +893,8 @@ quant_split_lds_kernel(SplitParams prm) {
       float pf[4];
       if (softmax_chunk_pt(x, lscale, m_run, alpha, ph, pf) && live) {
 #pragma unroll
-        for (int mv = 0; mv < NVM; ++mv) accv[mv] *= alpha;
+        for (int mv = 0; mv < NVM; ++mv)
+          if (v_mfma_in_part<VL, VS>(mv, PART)) accv[mv] *= alpha;
         oz *= alpha;
 
       }
@@ -1016,7 +1044,8 @@ quant_split_lds_kernel(SplitParams prm) {
       ChunkProbs pr;
       if (softmax_chunk<false>(x, lscale, m_run, l_run, alpha, pr) && live) {
   #pragma unroll
-        for (int mv = 0; mv < NVM; ++mv) accv[mv] *= alpha;
+        for (int mv = 0; mv < NVM; ++mv)
+          if (v_mfma_in_part<VL, VS>(mv, PART)) accv[mv] *= alpha;
         oz *= alpha;
 
       }
@@ -1046,6 +1075,7 @@ quant_split_lds_kernel(SplitParams prm) {
     u4 pgl[PSREM ? NPG : 1];
 #pragma unroll
     for (int v = 0; v < NPG; ++v) {
+      if (!v_operand_in_part<VL, VS, S>(v, PART)) continue;  // another part's groups
       uint32_t sp[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -1099,9 +1129,12 @@ quant_split_lds_kernel(SplitParams prm) {
         // acc[p + 1], leaves slice 0 as the small difference of two sums of
         // whole bytes: up to ~85x the rounding at 2 bits, measured 2.8e-3
         // max-abs on the Llama-3-8B shape with outlier channels.)  Otherwise
-        // each slice is isolated by its own mask.
+        // each slice is isolated by its own mask.  (A dims part, VS > 1,
+        // takes the slices [P0, P0 + P / VS) and never runs the chain.)
+        constexpr int P0 = PART * (VL::P / VS);
 #pragma unroll
         for (int p = 0; p < VL::P; ++p) {
+          if (p < P0 || p >= P0 + VL::P / VS) continue;  // another part's slices
           const int mv = VL::mfma_index(p, wi, e);
           const uint32_t msk = kVChain ? lo_slices_mask<VNB>(p) : slice_mask<VNB>(p);
           const u4 av = (kVChain && p == VL::P - 1) ? u4{pm[0], pm[1], pm[2], pm[3]}
@@ -1118,71 +1151,86 @@ quant_split_lds_kernel(SplitParams prm) {
   // chunk holding the last token, which always runs as the TAIL step (even
   // when it is full).  A single loop exit keeps the accumulators in place
   // across the unrolled copies.
-  auto stream = [&](auto pmode) __attribute__((always_inline)) {
+  auto stream = [&](auto pmode, auto part) __attribute__((always_inline)) {
     int cb = cb0;
     for (; cb + (NSTAGE - 1) * cstride + kChunk < hi; cb += NSTAGE * cstride) {
       static_for<NSTAGE>([&](auto s) __attribute__((always_inline)) {
-        step(cb + decltype(s)::value * cstride, std::false_type{}, s, pmode);
+        step(cb + decltype(s)::value * cstride, std::false_type{}, s, pmode, part);
       });
     }
     bool more = true;
     static_for<NSTAGE>([&](auto s) __attribute__((always_inline)) {
       if (more) {
         if (cb + kChunk < hi) {
-          step(cb, std::false_type{}, s, pmode);
+          step(cb, std::false_type{}, s, pmode, part);
           cb += cstride;
         } else {
-          if (cb < hi) step(cb, std::true_type{}, s, pmode);
+          if (cb < hi) step(cb, std::true_type{}, s, pmode, part);
           more = false;
         }
       }
     });
   };
-  // Short rows take hi/lo probabilities in every chunk (see kHiLoMaxLen);
-  // longer ones the remainders of P * s where kPsRemainder asks for them.
-  if (L <= kHiLoMaxLen) stream(std::integral_constant<int, 2>{});
-  else stream(std::integral_constant<int, kPsRemainder<VNB, NG> ? 1 : 0>{});
-  wait_vmcnt<0>();  // retire the trailing (out-of-range) prefetches
-  wave_lds_fence();
-  // whether the V accumulators of columns 8-15 hold the P * s remainders of
-  // columns 0-7 (the stream ran with FOLD)
-  const bool folded = PT && HS == 16 && kPsRemainder<VNB, NG> && L > kHiLoMaxLen;
+  // The stream, this wave's partial and the workgroup merge, for dims part
+  // PART (VS > 1; one part otherwise): each part is its own straight-line
+  // copy of the loop, so a part's accumulators are all it carries.
+  auto run = [&](auto part) __attribute__((always_inline)) {
+    constexpr int PART = decltype(part)::value;
+    // Short rows take hi/lo probabilities in every chunk (see kHiLoMaxLen);
+    // longer ones the remainders of P * s where kPsRemainder asks for them.
+    if (L <= kHiLoMaxLen) stream(std::integral_constant<int, 2>{}, part);
+    else stream(std::integral_constant<int, kPsRemainder<VNB, NG> ? 1 : 0>{}, part);
+    wait_vmcnt<0>();  // retire the trailing (out-of-range) prefetches
+    wave_lds_fence();
+    // whether the V accumulators of columns 8-15 hold the P * s remainders of
+    // columns 0-7 (the stream ran with FOLD)
+    const bool folded = PT && HS == 16 && kPsRemainder<VNB, NG> && L > kHiLoMaxLen;
 
-  // ---- this wave's partial into its own ring region -------------------------
-  WavePartial<D>& wp = *reinterpret_cast<WavePartial<D>*>(ring);
-  {
-    // Row g of the V zero-point MFMA (group g; row NG: the ones row, sum p)
-    // sits in lane 16 * (g / 4) + n, element g % 4: broadcast to every lane
-    // of column n.
-    const float lt = row_bcast(oz[NG % 4], NG / 4);
-    float ozg[NG];
+    // ---- this wave's partial into its own ring region -----------------------
+    WavePartial<D>& wp = *reinterpret_cast<WavePartial<D>*>(ring);
+    {
+      // Row g of the V zero-point MFMA (group g; row NG: the ones row, sum p)
+      // sits in lane 16 * (g / 4) + n, element g % 4: broadcast to every lane
+      // of column n.
+      const float lt = row_bcast(oz[NG % 4], NG / 4);
+      float ozg[NG];
 #pragma unroll
-    for (int g = 0; g < NG; ++g) ozg[g] = row_bcast(oz[g % 4], g / 4);
+      for (int g = 0; g < NG; ++g) ozg[g] = row_bcast(oz[g % 4], g / 4);
 #pragma unroll
-    for (int mv = 0; mv < NVM; ++mv) {
-      const int p = VL::slice_of(mv);
-      const float fac = kTwo24 * __builtin_ldexpf(1.0f, -p * VNB);
-      const float zv = ozg[VL::group_of(mv)];
-      f4 a = accv[mv];
-      if (kVChain && p > 0) a -= accv[VL::mfma_index(p - 1, VL::window_of(mv), VL::e_of(mv))];
-      if (folded) {
+      for (int mv = 0; mv < NVM; ++mv) {
+        if (!v_mfma_in_part<VL, VS>(mv, PART)) continue;
+        const int p = VL::slice_of(mv);
+        const float fac = kTwo24 * __builtin_ldexpf(1.0f, -p * VNB);
+        const float zv = ozg[VL::group_of(mv)];
+        f4 a = accv[mv];
+        if (kVChain && p > 0) a -= accv[VL::mfma_index(p - 1, VL::window_of(mv), VL::e_of(mv))];
+        if (folded) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) a[i] += lane_xor8(a[i]);
+          for (int i = 0; i < 4; ++i) a[i] += lane_xor8(a[i]);
+        }
+        if (S == 1 || VL::group_of(mv) % S == slot) {  // this column's products are group mv's
+#pragma unroll
+          for (int i = 0; i < 4; ++i) wp.o[n % HS][VL::dim_of(mv, 4 * j + i)] = fmaf(a[i], fac, zv);
+        }
       }
-      if (S == 1 || VL::group_of(mv) % S == slot) {  // this column's products are group mv's
-#pragma unroll
-        for (int i = 0; i < 4; ++i) wp.o[n % HS][VL::dim_of(mv, 4 * j + i)] = fmaf(a[i], fac, zv);
+      if (j == 0) {
+        wp.m[n] = m_run;
+        wp.l[n] = lt;
       }
     }
-    if (j == 0) {
-      wp.m[n] = m_run;
-      wp.l[n] = lt;
-    }
+    WavePartial<D>& wp0 = *reinterpret_cast<WavePartial<D>*>(smem);
+    const MergeView view{&wp0.o[0][0], &wp0.m[0], &wp0.l[0], SM::WAVE / 4,
+                         reinterpret_cast<int*>(smem + sizeof(WavePartial<D>))};
+    // part PART holds the dims of slices [P0, P0 + P / VS): [PART * D / VS, ...)
+    merge_and_store<D, NW, D / VS>(prm, view, b, h0, nh, split, PART * (D / VS));
+  };
+  if constexpr (VS == 1) {
+    run(std::integral_constant<int, 0>{});
+  } else {
+    static_assert(VS == 2, "two dims parts");
+    if (vpart == 0) run(std::integral_constant<int, 0>{});
+    else run(std::integral_constant<int, 1>{});
   }
-  WavePartial<D>& wp0 = *reinterpret_cast<WavePartial<D>*>(smem);
-  const MergeView view{&wp0.o[0][0], &wp0.m[0], &wp0.l[0], SM::WAVE / 4,
-                       reinterpret_cast<int*>(smem + sizeof(WavePartial<D>))};
-  merge_and_store<D, NW>(prm, view, b, h0, nh, split);
 }
 
 // Ring depth per wave of the quantized split kernel.  8-wave workgroups run
@@ -1194,26 +1242,63 @@ constexpr int kStages8 = 2;  // also the ring depth of 12-wave workgroups
 static_assert(kStages8 == 2, "kTwelveWaves sizes two-stage rings");
 constexpr int kStages4 = 2;
 
+// Compute units of the current device (cached per device; 0 if unknown).
+inline int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess) cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// Formats with dims-split kernels: head dim 128, equal K/V bits, groups of
+// 32 and 8 head columns (GQA groups of 5-8 heads, as Qwen2.5-1.5B's small
+// grids).  There every V group has P' operands of its own (no slice chain),
+// so each part's V products, partial and merge are the very operations of
+// the one-workgroup kernel: the output is bitwise the same.  With 4 head
+// columns the slices of a byte share one chain (acc[p] - acc[p - 1]), which
+// a part that starts past slice 0 would have to restart: different bits.
+template <int D, int KNB, int VNB, int GS, int HS>
+constexpr bool kDimsSplit = D == 128 && KNB == VNB && GS == 32 && HS == 8;
+
 template <int D, int KNB, int VNB, int GS, bool PT, int HS, bool ORD>
 void launch_quant_pto(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
   const bool paged = p.page_size > 0;
+  // A grid of at most half as many workgroups as the GPU has CUs runs each
+  // (unit, split, head block) as two workgroups over half the head dim each.
+  if constexpr (!PT && !ORD && kDimsSplit<D, KNB, VNB, GS, HS>) {
+    if (!paged && p.counters == nullptr && p.key_block == 0 && waves != 12 &&
+        2ull * grid.x * grid.y * grid.z <= (unsigned long long)device_cus()) {
+      const dim3 g2(grid.x, grid.y, grid.z * 2);
+      if (waves >= 8)
+        quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, false, false, HS, false, 2>
+            <<<g2, dim3(8 * 64), 0, st>>>(p);
+      else
+        quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false, false, false, HS, false, 2>
+            <<<g2, dim3(4 * 64), 0, st>>>(p);
+      return;
+    }
+  }
   if constexpr (kTwelveWaves<D, KNB, VNB, GS, HS, PT>) {
     if (waves == 12 && !paged) {
-      quant_split_lds_kernel<D, KNB, VNB, GS, 12, kStages8, false, PT, false, HS, ORD>
+      quant_split_lds_kernel<D, KNB, VNB, GS, 12, kStages8, false, PT, false, HS, ORD, 1>
           <<<grid, dim3(12 * 64), 0, st>>>(p);
       return;
     }
   }
   if (waves >= 8) {
     if (paged)
-      quant_split_lds_kernel<D, KNB, VNB, GS, 8, 2, true, PT, false, HS, ORD><<<grid, dim3(8 * 64), 0, st>>>(p);
+      quant_split_lds_kernel<D, KNB, VNB, GS, 8, 2, true, PT, false, HS, ORD, 1><<<grid, dim3(8 * 64), 0, st>>>(p);
     else
-      quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, PT, false, HS, ORD><<<grid, dim3(8 * 64), 0, st>>>(p);
+      quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, PT, false, HS, ORD, 1><<<grid, dim3(8 * 64), 0, st>>>(p);
   } else {
     if (paged)
-      quant_split_lds_kernel<D, KNB, VNB, GS, 4, 2, true, PT, false, HS, ORD><<<grid, dim3(4 * 64), 0, st>>>(p);
+      quant_split_lds_kernel<D, KNB, VNB, GS, 4, 2, true, PT, false, HS, ORD, 1><<<grid, dim3(4 * 64), 0, st>>>(p);
     else
-      quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false, PT, false, HS, ORD><<<grid, dim3(4 * 64), 0, st>>>(p);
+      quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false, PT, false, HS, ORD, 1><<<grid, dim3(4 * 64), 0, st>>>(p);
   }
 }
 
@@ -1313,16 +1398,16 @@ void launch_quant_hs(const SplitParams& p, dim3 grid, int waves, hipStream_t st)
     if (p.key_block) {  // per-channel keys (the host checked: contiguous, no fused append)
       if constexpr (kTwelveWaves<D, KNB, VNB, GS, HS, false>) {
         if (waves == 12) {
-          quant_split_lds_kernel<D, KNB, VNB, GS, 12, kStages8, false, false, true, HS, false>
+          quant_split_lds_kernel<D, KNB, VNB, GS, 12, kStages8, false, false, true, HS, false, 1>
               <<<grid, dim3(12 * 64), 0, st>>>(p);
           return;
         }
       }
       if (waves >= 8)
-        quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, false, true, HS, false>
+        quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, false, true, HS, false, 1>
             <<<grid, dim3(8 * 64), 0, st>>>(p);
       else
-        quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false, false, true, HS, false>
+        quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false, false, true, HS, false, 1>
             <<<grid, dim3(4 * 64), 0, st>>>(p);
       return;
     }
