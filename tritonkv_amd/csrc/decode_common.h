@@ -51,6 +51,9 @@ struct SplitParams {
   // one deep).  A permutation, so every (unit, split) runs once and writes its
   // own partial row: the result does not depend on it.
   const int32_t* order;
+  // B * HKV: the units of the launch, which the dims-split kernels (whose
+  // grid is not (units, splits, head blocks)) map their workgroups onto.
+  int units;
 };
 
 // Longest piece first: the dispatch order ragged_order_kernel writes.  Piece

@@ -396,12 +396,21 @@ template <int VNB, int NG>
 constexpr bool kPsRemainder = VNB == 2 && NG == 1;
 
 
-// Dims split (VS workgroups per output row): part `part` computes the V bit
-// slices [part * P / VS, (part + 1) * P / VS).  Whether V MFMA mv, and P'
-// operand v (of S-slot head columns), belong to that part.
+// Dims split (VS workgroups per output row): part `part` computes the V
+// MFMAs [part * NVM / VS, (part + 1) * NVM / VS), whole (slice, window) blocks
+// of NE MFMAs in (slice, window) order, i.e. the dims [part * D / VS,
+// (part + 1) * D / VS).  Whether V MFMA mv, window wi, and P' operand v (of
+// S-slot head columns) are used by that part.
 template <class VL, int VS>
 __device__ constexpr bool v_mfma_in_part(int mv, int part) {
-  return VL::slice_of(mv) >= part * (VL::P / VS) && VL::slice_of(mv) < (part + 1) * (VL::P / VS);
+  return mv / (VL::NVM / VS) == part;
+}
+template <class VL, int VS>
+__device__ constexpr bool v_window_in_part(int wi, int part) {
+  for (int p = 0; p < VL::P; ++p)
+    for (int e = 0; e < VL::NE; ++e)
+      if (v_mfma_in_part<VL, VS>(VL::mfma_index(p, wi, e), part)) return true;
+  return false;
 }
 template <class VL, int VS, int S>
 __device__ constexpr bool v_operand_in_part(int v, int part) {
@@ -418,9 +427,8 @@ __device__ constexpr bool v_operand_in_part(int v, int part) {
 // VS: workgroups that share one (unit, split, block of heads) by splitting
 // the head dim of the output.  Workgroup z % VS computes every score (the K
 // side, the softmax) but only the V products, the partial and the merge of
-// the bit slices [P0, P1) of each V byte, i.e. dims [P0 * DP, P1 * DP): less
-// work per chunk and twice the workgroups when a launch has far fewer
-// workgroups than the GPU has CUs.
+// dims [part * D / VS, (part + 1) * D / VS): less work per chunk and VS times
+// the workgroups when a launch has far fewer workgroups than the GPU has CUs.
 template <int D, int KNB, int VNB, int GS, int NW, int NSTAGE, bool PAGED, bool PT, bool KCH, int HS,
           bool ORD, int VS>
 __global__ void __launch_bounds__(NW * 64)
@@ -453,19 +461,39 @@ quant_split_lds_kernel(SplitParams prm) {
 
   // x fastest: consecutive workgroups (which the dispatcher deals to the 8 XCDs
   // in turn) take other units.  A ragged batch may pass a longest-first order.
-  int unit_ = blockIdx.x, split_ = blockIdx.y, L_ = 0;
+  int unit_ = blockIdx.x, split_ = blockIdx.y, hb_ = blockIdx.z, part_ = 0, L_ = 0;
   if constexpr (ORD) {
     const int2 e = reinterpret_cast<const int2*>(prm.order)[blockIdx.y * gridDim.x + blockIdx.x];
     unit_ = e.x % (int)gridDim.x;
     split_ = e.x / (int)gridDim.x;
     L_ = e.y;
   }
+  if constexpr (VS > 1) {
+    // Dims split.  The parts of one (unit, split, head block) tuple run on one
+    // XCD, whose L2 then serves the rows they all load: the dispatcher deals
+    // workgroups to the 8 XCDs in turn, so parts 8k workgroups apart share one.
+    if (gridDim.z > 1) {
+      // T >= 8 tuples, T % 8 == 0 in the common cases: z = head block * VS +
+      // part, and the parts of a tuple are T workgroups apart.
+      part_ = (int)blockIdx.z % VS;
+      hb_ = (int)blockIdx.z / VS;
+    } else {
+      // T < 8 tuples: grid (8 * VS); workgroup x takes part x / 8 of tuple
+      // x % 8, and the workgroups past the last tuple leave at once.
+      const int tuples = prm.units * prm.num_splits * ((prm.G + 15) / 16);
+      const int t = (int)blockIdx.x % 8;
+      if (t >= tuples) return;
+      part_ = (int)blockIdx.x / 8;
+      unit_ = t % prm.units;
+      split_ = (t / prm.units) % prm.num_splits;
+      hb_ = t / (prm.units * prm.num_splits);
+    }
+  }
   const int unit = __builtin_amdgcn_readfirstlane(unit_);
   const int split = __builtin_amdgcn_readfirstlane(split_);
   const int b = unit / prm.HKV, hk = unit % prm.HKV;
-  // z = block of 16 query heads * VS + the dims part (VS > 1)
-  const int vpart = VS > 1 ? (int)(blockIdx.z % VS) : 0;
-  const int hb0 = (VS > 1 ? (int)(blockIdx.z / VS) : (int)blockIdx.z) * 16;
+  const int vpart = __builtin_amdgcn_readfirstlane(part_);  // dims part (VS > 1)
+  const int hb0 = __builtin_amdgcn_readfirstlane(hb_) * 16;
   const int nh = min(16, prm.G - hb0);
   const int h0 = hk * prm.G + hb0;
   const int L = ORD ? __builtin_amdgcn_readfirstlane(L_)
@@ -584,8 +612,10 @@ quant_split_lds_kernel(SplitParams prm) {
   for (int m = 0; m < NKM; ++m) kmask[m] = slice_mask<KNB>(KL::slice_of(m, j));
 
   constexpr bool kVChain = NPG == 1;  // every V MFMA takes the same P' operand
-  static_assert(VS == 1 || (VS == 2 && !PT && !KCH && !PAGED && !ORD && !kVChain && VL::P % 2 == 0),
-                "dims split: unpaired, per-token keys, contiguous, grid order, no slice chain");
+  static_assert(VS == 1 || ((VS == 2 || VS == 4) && !PT && !KCH && !PAGED && !ORD && !kVChain &&
+                             NVM % (VS * VL::NE) == 0),
+                "dims split: unpaired, per-token keys, contiguous, grid order, no slice chain, "
+                "whole (slice, window) blocks per part");
 
   // Per-lane LDS byte offsets inside a stage.
   // K operand of tile a, load Lh: row 16a + r, byte load_offset(Lh, j).
@@ -733,7 +763,7 @@ quant_split_lds_kernel(SplitParams prm) {
         pmeta[2 * NG + lane] = (uint16_t)(rv.meta & 0xFFFFu);
         pmeta[3 * NG + lane] = (uint16_t)(rv.meta >> 16);
       }
-      if (blockIdx.z == 0) {
+      if (hb0 == 0 && vpart == 0) {
         if (lane < KL::DP) const_cast<uint8_t*>(prm.k)[row * KL::DP + lane] = (uint8_t)rk.byte;
         if (lane < VL::DP) const_cast<uint8_t*>(prm.v)[row * VL::DP + lane] = (uint8_t)rv.byte;
         if (lane < NG) {
@@ -1105,6 +1135,7 @@ quant_split_lds_kernel(SplitParams prm) {
     // ---- O^T += V^T P'^T ---------------------------------------------------
 #pragma unroll
     for (int wi = 0; wi < VL::NWIN; ++wi) {
+      if (!v_window_in_part<VL, VS>(wi, PART)) continue;  // another part's dims
       uint32_t vx[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i)
@@ -1130,12 +1161,11 @@ quant_split_lds_kernel(SplitParams prm) {
         // whole bytes: up to ~85x the rounding at 2 bits, measured 2.8e-3
         // max-abs on the Llama-3-8B shape with outlier channels.)  Otherwise
         // each slice is isolated by its own mask.  (A dims part, VS > 1,
-        // takes the slices [P0, P0 + P / VS) and never runs the chain.)
-        constexpr int P0 = PART * (VL::P / VS);
+        // takes its own MFMAs and never runs the chain.)
 #pragma unroll
         for (int p = 0; p < VL::P; ++p) {
-          if (p < P0 || p >= P0 + VL::P / VS) continue;  // another part's slices
           const int mv = VL::mfma_index(p, wi, e);
+          if (!v_mfma_in_part<VL, VS>(mv, PART)) continue;  // another part's dims
           const uint32_t msk = kVChain ? lo_slices_mask<VNB>(p) : slice_mask<VNB>(p);
           const u4 av = (kVChain && p == VL::P - 1) ? u4{pm[0], pm[1], pm[2], pm[3]}
                                                     : u4{pm[0] & msk, pm[1] & msk, pm[2] & msk, pm[3] & msk};
@@ -1226,10 +1256,15 @@ quant_split_lds_kernel(SplitParams prm) {
   };
   if constexpr (VS == 1) {
     run(std::integral_constant<int, 0>{});
-  } else {
-    static_assert(VS == 2, "two dims parts");
+  } else if constexpr (VS == 2) {
     if (vpart == 0) run(std::integral_constant<int, 0>{});
     else run(std::integral_constant<int, 1>{});
+  } else {
+    static_assert(VS == 4, "two or four dims parts");
+    if (vpart == 0) run(std::integral_constant<int, 0>{});
+    else if (vpart == 1) run(std::integral_constant<int, 1>{});
+    else if (vpart == 2) run(std::integral_constant<int, 2>{});
+    else run(std::integral_constant<int, 3>{});
   }
 }
 
@@ -1267,12 +1302,26 @@ constexpr bool kDimsSplit = D == 128 && KNB == VNB && GS == 32 && HS == 8;
 template <int D, int KNB, int VNB, int GS, bool PT, int HS, bool ORD>
 void launch_quant_pto(const SplitParams& p, dim3 grid, int waves, hipStream_t st) {
   const bool paged = p.page_size > 0;
-  // A grid of at most half as many workgroups as the GPU has CUs runs each
-  // (unit, split, head block) as two workgroups over half the head dim each.
+  // A grid of at most a quarter (a half) as many workgroups as the GPU has
+  // CUs runs each (unit, split, head block) as four (two) workgroups, each
+  // over a quarter (a half) of the head dim.
   if constexpr (!PT && !ORD && kDimsSplit<D, KNB, VNB, GS, HS>) {
-    if (!paged && p.counters == nullptr && p.key_block == 0 && waves != 12 &&
-        2ull * grid.x * grid.y * grid.z <= (unsigned long long)device_cus()) {
-      const dim3 g2(grid.x, grid.y, grid.z * 2);
+    const unsigned long long wgs = 1ull * grid.x * grid.y * grid.z;
+    const unsigned long long cus = (unsigned long long)device_cus();
+    if (!paged && p.counters == nullptr && p.key_block == 0 && waves != 12 && 2 * wgs <= cus) {
+      // fewer than 8 tuples: grid (8 * VS); else VS times the z axis (see the
+      // kernel's dims-split mapping)
+      if (4 * wgs <= cus) {
+        const dim3 g4 = wgs < 8 ? dim3(8 * 4) : dim3(grid.x, grid.y, grid.z * 4);
+        if (waves >= 8)
+          quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, false, false, HS, false, 4>
+              <<<g4, dim3(8 * 64), 0, st>>>(p);
+        else
+          quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false, false, false, HS, false, 4>
+              <<<g4, dim3(4 * 64), 0, st>>>(p);
+        return;
+      }
+      const dim3 g2 = wgs < 8 ? dim3(8 * 2) : dim3(grid.x, grid.y, grid.z * 2);
       if (waves >= 8)
         quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, false, false, HS, false, 2>
             <<<g2, dim3(8 * 64), 0, st>>>(p);
