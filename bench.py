@@ -130,15 +130,17 @@ PAIRED_TILES_MIN_SPLIT = 8192
 
 
 def split_kernel_name(D, kbits, vbits, gs, waves, G, split_size, paged=False, kch=False,
-                      ordered=False, vsplit=1):
+                      ordered=False, vsplit=1, small_grid=False):
     """The demangled name (as rocprofv3 prints it) of the quantized split
     kernel instantiation that a launch with these arguments runs (``vsplit``:
-    2 for the dims-split kernels of small grids)."""
+    2 or 4 for the dims-split kernels of small grids, ``small_grid`` for their
+    layout on fewer than 8 tuples)."""
     pt = not kch and G <= 8 and split_size >= PAIRED_TILES_MIN_SPLIT
     hs = 16 if D // gs < 2 else 4 if G <= 4 else 8 if G <= 8 else 16  # head columns
     b = lambda x: "true" if x else "false"  # noqa: E731
     return (f"void tkv::quant_split_lds_kernel<{D}, {kbits}, {vbits}, {gs}, {waves}, 2, "
-            f"{b(paged)}, {b(pt)}, {b(kch)}, {hs}, {b(ordered)}, {vsplit}>(tkv::SplitParams)")
+            f"{b(paged)}, {b(pt)}, {b(kch)}, {hs}, {b(ordered)}, {vsplit}, {b(small_grid)}>"
+            "(tkv::SplitParams)")
 
 
 # ---------------------------------------------------------------------------

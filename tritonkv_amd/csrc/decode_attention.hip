@@ -573,7 +573,7 @@ static SplitParams make_params(const tkv_decode_args* a) {
   p.split_base = a->split_base;
   p.ns_total = a->num_splits_total ? a->num_splits_total : a->num_splits;
   p.order = nullptr;  // set by launch_fused_split once the order is written
-  p.units = a->B * a->HKV;
+  p.xcd_units = 0;   // set by the small-grid dims-split launch
   return p;
 }
 

@@ -51,9 +51,11 @@ struct SplitParams {
   // one deep).  A permutation, so every (unit, split) runs once and writes its
   // own partial row: the result does not depend on it.
   const int32_t* order;
-  // B * HKV: the units of the launch, which the dims-split kernels (whose
-  // grid is not (units, splits, head blocks)) map their workgroups onto.
-  int units;
+  // Dims-split kernels on fewer than 8 (unit, split, head block) tuples:
+  // B * HKV, the units their (8 * VS)-workgroup grid maps onto; 0 for every
+  // other launch (a flag in the argument block, which the prologue loads
+  // anyway: the grid's own size would be another load).
+  int xcd_units;
 };
 
 // Longest piece first: the dispatch order ragged_order_kernel writes.  Piece

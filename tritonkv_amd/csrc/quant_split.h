@@ -424,13 +424,18 @@ __device__ constexpr bool v_operand_in_part(int v, int part) {
 // else made the compiler fetch the cache pointers in a second, serial round
 // trip to the argument block: 0.1-0.3 us on every Qwen2.5-1.5B-shape call.
 //
+// SMALL (with VS > 1): the grid holds fewer than 8 (unit, split, head block)
+// tuples and takes the small-grid layout below.  A separate instantiation:
+// a run-time choice of layout ahead of the first DMA cost 0.2-0.25 us on
+// every cold Qwen2.5-1.5B-shape step that did not take it.
+//
 // VS: workgroups that share one (unit, split, block of heads) by splitting
 // the head dim of the output.  Workgroup z % VS computes every score (the K
 // side, the softmax) but only the V products, the partial and the merge of
 // dims [part * D / VS, (part + 1) * D / VS): less work per chunk and VS times
 // the workgroups when a launch has far fewer workgroups than the GPU has CUs.
 template <int D, int KNB, int VNB, int GS, int NW, int NSTAGE, bool PAGED, bool PT, bool KCH, int HS,
-          bool ORD, int VS>
+          bool ORD, int VS, bool SMALL>
 __global__ void __launch_bounds__(NW * 64)
 quant_split_lds_kernel(SplitParams prm) {
   using SG = StageGeom<D, KNB, VNB, GS>;
@@ -472,7 +477,7 @@ quant_split_lds_kernel(SplitParams prm) {
     // Dims split.  The parts of one (unit, split, head block) tuple run on one
     // XCD, whose L2 then serves the rows they all load: the dispatcher deals
     // workgroups to the 8 XCDs in turn, so parts 8k workgroups apart share one.
-    if (gridDim.z > 1) {
+    if constexpr (!SMALL) {
       // T >= 8 tuples, T % 8 == 0 in the common cases: z = head block * VS +
       // part, and the parts of a tuple are T workgroups apart.
       part_ = (int)blockIdx.z % VS;
@@ -480,13 +485,14 @@ quant_split_lds_kernel(SplitParams prm) {
     } else {
       // T < 8 tuples: grid (8 * VS); workgroup x takes part x / 8 of tuple
       // x % 8, and the workgroups past the last tuple leave at once.
-      const int tuples = prm.units * prm.num_splits * ((prm.G + 15) / 16);
+      const int units = prm.xcd_units;
+      const int tuples = units * prm.num_splits * ((prm.G + 15) / 16);
       const int t = (int)blockIdx.x % 8;
       if (t >= tuples) return;
       part_ = (int)blockIdx.x / 8;
-      unit_ = t % prm.units;
-      split_ = (t / prm.units) % prm.num_splits;
-      hb_ = t / (prm.units * prm.num_splits);
+      unit_ = t % units;
+      split_ = (t / units) % prm.num_splits;
+      hb_ = t / (units * prm.num_splits);
     }
   }
   const int unit = __builtin_amdgcn_readfirstlane(unit_);
@@ -612,6 +618,7 @@ quant_split_lds_kernel(SplitParams prm) {
   for (int m = 0; m < NKM; ++m) kmask[m] = slice_mask<KNB>(KL::slice_of(m, j));
 
   constexpr bool kVChain = NPG == 1;  // every V MFMA takes the same P' operand
+  static_assert(!SMALL || VS > 1, "small-grid layout: dims-split kernels only");
   static_assert(VS == 1 || ((VS == 2 || VS == 4) && !PT && !KCH && !PAGED && !ORD && !kVChain &&
                              NVM % (VS * VL::NE) == 0),
                 "dims split: unpaired, per-token keys, contiguous, grid order, no slice chain, "
@@ -1309,45 +1316,50 @@ void launch_quant_pto(const SplitParams& p, dim3 grid, int waves, hipStream_t st
     const unsigned long long wgs = 1ull * grid.x * grid.y * grid.z;
     const unsigned long long cus = (unsigned long long)device_cus();
     if (!paged && p.counters == nullptr && p.key_block == 0 && waves != 12 && 2 * wgs <= cus) {
-      // fewer than 8 tuples: grid (8 * VS); else VS times the z axis (see the
-      // kernel's dims-split mapping)
-      if (4 * wgs <= cus) {
-        const dim3 g4 = wgs < 8 ? dim3(8 * 4) : dim3(grid.x, grid.y, grid.z * 4);
+      // fewer than 8 tuples: grid (8 * VS), xcd_units set and the small-grid
+      // layout; else VS times the z axis (see the kernel's dims-split mapping)
+      auto go = [&](auto vs, auto sg) {
+        constexpr int V = decltype(vs)::value;
+        constexpr bool SGL = decltype(sg)::value;
+        SplitParams q = p;
+        if (SGL) q.xcd_units = (int)grid.x;
+        const dim3 g = SGL ? dim3(8 * V) : dim3(grid.x, grid.y, grid.z * V);
         if (waves >= 8)
-          quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, false, false, HS, false, 4>
-              <<<g4, dim3(8 * 64), 0, st>>>(p);
+          quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, false, false, HS, false, V, SGL>
+              <<<g, dim3(8 * 64), 0, st>>>(q);
         else
-          quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false, false, false, HS, false, 4>
-              <<<g4, dim3(4 * 64), 0, st>>>(p);
-        return;
+          quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false, false, false, HS, false, V, SGL>
+              <<<g, dim3(4 * 64), 0, st>>>(q);
+      };
+      using I2 = std::integral_constant<int, 2>;
+      using I4 = std::integral_constant<int, 4>;
+      if (4 * wgs <= cus) {
+        if (wgs < 8) go(I4{}, std::true_type{});
+        else go(I4{}, std::false_type{});
+      } else {
+        if (wgs < 8) go(I2{}, std::true_type{});
+        else go(I2{}, std::false_type{});
       }
-      const dim3 g2 = wgs < 8 ? dim3(8 * 2) : dim3(grid.x, grid.y, grid.z * 2);
-      if (waves >= 8)
-        quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, false, false, HS, false, 2>
-            <<<g2, dim3(8 * 64), 0, st>>>(p);
-      else
-        quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false, false, false, HS, false, 2>
-            <<<g2, dim3(4 * 64), 0, st>>>(p);
       return;
     }
   }
   if constexpr (kTwelveWaves<D, KNB, VNB, GS, HS, PT>) {
     if (waves == 12 && !paged) {
-      quant_split_lds_kernel<D, KNB, VNB, GS, 12, kStages8, false, PT, false, HS, ORD, 1>
+      quant_split_lds_kernel<D, KNB, VNB, GS, 12, kStages8, false, PT, false, HS, ORD, 1, false>
           <<<grid, dim3(12 * 64), 0, st>>>(p);
       return;
     }
   }
   if (waves >= 8) {
     if (paged)
-      quant_split_lds_kernel<D, KNB, VNB, GS, 8, 2, true, PT, false, HS, ORD, 1><<<grid, dim3(8 * 64), 0, st>>>(p);
+      quant_split_lds_kernel<D, KNB, VNB, GS, 8, 2, true, PT, false, HS, ORD, 1, false><<<grid, dim3(8 * 64), 0, st>>>(p);
     else
-      quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, PT, false, HS, ORD, 1><<<grid, dim3(8 * 64), 0, st>>>(p);
+      quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, PT, false, HS, ORD, 1, false><<<grid, dim3(8 * 64), 0, st>>>(p);
   } else {
     if (paged)
-      quant_split_lds_kernel<D, KNB, VNB, GS, 4, 2, true, PT, false, HS, ORD, 1><<<grid, dim3(4 * 64), 0, st>>>(p);
+      quant_split_lds_kernel<D, KNB, VNB, GS, 4, 2, true, PT, false, HS, ORD, 1, false><<<grid, dim3(4 * 64), 0, st>>>(p);
     else
-      quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false, PT, false, HS, ORD, 1><<<grid, dim3(4 * 64), 0, st>>>(p);
+      quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false, PT, false, HS, ORD, 1, false><<<grid, dim3(4 * 64), 0, st>>>(p);
   }
 }
 
@@ -1447,16 +1459,16 @@ void launch_quant_hs(const SplitParams& p, dim3 grid, int waves, hipStream_t st)
     if (p.key_block) {  // per-channel keys (the host checked: contiguous, no fused append)
       if constexpr (kTwelveWaves<D, KNB, VNB, GS, HS, false>) {
         if (waves == 12) {
-          quant_split_lds_kernel<D, KNB, VNB, GS, 12, kStages8, false, false, true, HS, false, 1>
+          quant_split_lds_kernel<D, KNB, VNB, GS, 12, kStages8, false, false, true, HS, false, 1, false>
               <<<grid, dim3(12 * 64), 0, st>>>(p);
           return;
         }
       }
       if (waves >= 8)
-        quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, false, true, HS, false, 1>
+        quant_split_lds_kernel<D, KNB, VNB, GS, 8, kStages8, false, false, true, HS, false, 1, false>
             <<<grid, dim3(8 * 64), 0, st>>>(p);
       else
-        quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false, false, true, HS, false, 1>
+        quant_split_lds_kernel<D, KNB, VNB, GS, 4, kStages4, false, false, true, HS, false, 1, false>
             <<<grid, dim3(4 * 64), 0, st>>>(p);
       return;
     }
