@@ -115,18 +115,24 @@ struct ChunkProbs {
   float p[8];
 };
 
+// The lane's own max decides first whether any head moved (a head's max rises
+// above m exactly when one of its lanes' does); the cross-lane max runs only
+// in chunks where one did.  The reference m stays the exact running max: a
+// dominant token then enters the PV products as p = 1 exactly, with no fp16
+// rounding.  (A lagging reference -- a rescale only when the max rises by
+// more than a few units -- rounds that p: 5.6e-3 max-abs instead of 6.6e-5
+// on a dominant-token head of 2-bit values.)
 template <bool TRACK_L = true>
 __device__ __forceinline__ bool softmax_chunk(const float (&x)[8], float lscale, float& m,
                                               float& l, float& alpha, ChunkProbs& out) {
-  float mx = x[0];
+  float lm = x[0];
 #pragma unroll
-  for (int i = 1; i < 8; ++i) mx = fmaxf(mx, x[i]);
-  mx = xor_max16_32(mx) * lscale;
-  const bool moved = mx > m;
-  const bool any_moved = __builtin_amdgcn_ballot_w64(moved) != 0;
+  for (int i = 1; i < 8; ++i) lm = fmaxf(lm, x[i]);
+  lm *= lscale;
+  const bool any_moved = __builtin_amdgcn_ballot_w64(lm > m) != 0;
   alpha = 1.0f;
   if (any_moved) {
-    const float mn = vmax(m, mx);
+    const float mn = vmax(m, xor_max16_32(lm));
     alpha = safe_exp2_diff(m, mn);
     m = mn;
     if constexpr (TRACK_L) l *= alpha;

@@ -217,6 +217,7 @@ struct QOperandsPT {
   static constexpr int NB = D / 16;   // 16-dim blocks: block p * NU + u = unit u of slice p
   u4 qb[NB];
   u4 qzb;  // zero-point MFMA (K = 32): slots 8j + g hold hi (j even) or lo (j odd) of sum q_g
+  float qsum;  // one group per row: sum q of this lane's head (its zero term by one FMA per score)
   int eh;  // this lane's head's prescale exponent (as QOperands::eh)
 };
 
@@ -313,21 +314,21 @@ __device__ __forceinline__ void load_q_operands_pt(const SplitParams& prm, int b
   }
   qo.qzb = u4{pack_h2(hl[0], hl[1]), pack_h2(hl[2], hl[3]), pack_h2(hl[4], hl[5]),
               pack_h2(hl[6], hl[7])};
+  qo.qsum = qz[0];
 }
 
 // Online-softmax step of a paired-tile chunk: 4 scores per lane (one tile, one
 // head); the head's 32 tokens span lanes c and c ^ 8 of all four lane groups.
 // Returns whether any running max moved; ph holds the lane's fp16 pairs.
+// As softmax_chunk: the lane's own max decides whether any head moved, and
+// the cross-lane max runs only when one did.
 __device__ __forceinline__ bool softmax_chunk_pt(const float (&x)[4], float lscale, float& m,
                                                  float& alpha, uint32_t (&ph)[2], float (&p)[4]) {
-  float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-  mx = vmax(mx, lane_xor8(mx));
-  mx = xor_max16_32(mx) * lscale;
-  const bool moved = mx > m;
-  const bool any_moved = __builtin_amdgcn_ballot_w64(moved) != 0;
+  const float lm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])) * lscale;  // this lane's max
+  const bool any_moved = __builtin_amdgcn_ballot_w64(lm > m) != 0;
   alpha = 1.0f;
   if (any_moved) {
-    const float mn = vmax(m, mx);
+    const float mn = vmax(m, xor_max16_32(vmax(lm, lane_xor8(lm))));
     alpha = safe_exp2_diff(m, mn);
     m = mn;
   }
@@ -885,6 +886,19 @@ quant_split_lds_kernel(SplitParams prm) {
             const int g = (p * QP::DP + 16 * u) / GS;
             c[g] = mfma_k32(k_extract8(kx[u], slice_mask<KNB>(p)), qpt.qb[p * QP::NU + u], c[g]);
           }
+        if constexpr (NG == 1) {
+          // One group per row: the zero term z_t * sum q by one FMA per score
+          // instead of an MFMA (rows past the sequence get -inf below,
+          // whatever their z).
+          const float qz = qpt.qsum * zsc;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int t = tile_pt + 4 * j + i;
+            const float zv = (float)__builtin_bit_cast(_Float16, (uint16_t)half_at(mkz, t * SG::MROW));
+            const float sv = (float)__builtin_bit_cast(_Float16, (uint16_t)half_at(mks, t * SG::MROW));
+            x[i] = fmaf(sv, c[0][i], zv * qz);
+          }
+        } else {
         // zero-point part: A row = token 16 * (j >> 1) + r, k-slots 8j + g = its zero points
         u4 za;
         {
@@ -918,6 +932,7 @@ quant_split_lds_kernel(SplitParams prm) {
           }
           x[i] = sc;
         }
+        }  // NG > 1
       }
       if constexpr (TAIL) {
 #pragma unroll
