@@ -31,9 +31,12 @@ struct StageGeom {
   using VL = VLayout<D, VNB, GS>;
   static constexpr int NG = D / GS;
   // fp16 slots per token row of a staged metadata tensor: the global row of NG
-  // values, except NG == 1, whose rows are copied one fp16 per dword (a dword
-  // copy of 2-byte rows could straddle the end of the buffer range).
+  // values, except NG == 1: a chunk whose rows all lie before the split's last
+  // token is copied as whole dwords (fp16 pairs of tokens 2i, 2i + 1, MROW_PAIRS
+  // = 1), the chunk holding the last token one fp16 per dword (MROW = 2: a dword
+  // copy could straddle the end of the buffer range there).
   static constexpr int MROW = NG >= 2 ? NG : 2;
+  static constexpr int MROW_PAIRS = NG >= 2 ? NG : 1;
   static constexpr int KB = kChunk * KL::DP;    // K code bytes per chunk
   static constexpr int VB = kChunk * VL::DP;    // V code bytes per chunk
   static constexpr int MB = kChunk * MROW * 2;  // bytes of one staged metadata tensor
@@ -140,10 +143,13 @@ __device__ __forceinline__ void wait_lgkmcnt0() {
 
 // Issue the DMA of one chunk into a stage.  `valid` false turns every lane's
 // offset out of the buffer range, so the instructions still retire (keeping
-// the vmcnt arithmetic static) but read nothing and write zeros.
+// the vmcnt arithmetic static) but read nothing and write zeros.  `pairs`
+// (wave-uniform; one group per row only): the chunk ends before the split's
+// last token, and its metadata rows go in as whole dwords (StageGeom::MROW_PAIRS).
 template <int D, int KNB, int VNB, int GS, bool KCH = false>
 __device__ __forceinline__ void issue_chunk(uint8_t* stage, const rsrc_t& rk, const rsrc_t& rv,
-                                            const rsrc_t (&rm)[4], int cb, bool valid, int lane) {
+                                            const rsrc_t (&rm)[4], int cb, bool valid, int lane,
+                                            bool pairs) {
   // cb: index, within the resources, of the chunk's first row
   using SG = StageGeom<D, KNB, VNB, GS>;
   using KL = typename SG::KL;
@@ -184,8 +190,14 @@ __device__ __forceinline__ void issue_chunk(uint8_t* stage, const rsrc_t& rk, co
         const uint32_t off = valid && q == 0 ? (uint32_t)(cb / kChunk) * D * 2 + 4 * lane : kOut;
         if (lane < D / 2) dma4<kPolDma>(rm[tsr], to_lds(dst), off);
       } else if constexpr (SG::NG == 1) {
-        const uint32_t off = valid ? (uint32_t)(cb + lane) * 2 : kOut;
-        if (lane < kChunk) dma2<kPolDma>(rm[tsr], to_lds(dst), off);
+        // One instruction either way (the vmcnt arithmetic counts instructions).
+        if (pairs) {
+          const uint32_t off = valid ? (uint32_t)(cb + 2 * lane) * 2 : kOut;
+          if (lane < kChunk / 2) dma4<kPolDma>(rm[tsr], to_lds(dst), off);
+        } else {
+          const uint32_t off = valid ? (uint32_t)(cb + lane) * 2 : kOut;
+          if (lane < kChunk) dma2<kPolDma>(rm[tsr], to_lds(dst), off);
+        }
       } else {
         const uint32_t off = valid ? (uint32_t)cb * SG::NG * 2 + 4 * (64 * q + lane) : kOut;
         if (SG::MB >= 256 || lane < SG::MB / 4) dma4<kPolDma>(rm[tsr], to_lds(dst), off);
@@ -595,7 +607,8 @@ quant_split_lds_kernel(SplitParams prm) {
     const int page0 = to_page(e0);
     page_next = to_page(e1);
     const ChunkSrc src = chunk_src(cb0, page0);
-    issue_chunk<D, KNB, VNB, GS, KCH>(ring, src.k, src.v, src.m, src.row, cb0 < hi, lane);
+    issue_chunk<D, KNB, VNB, GS, KCH>(ring, src.k, src.v, src.m, src.row, cb0 < hi, lane,
+                                      cb0 + kChunk < hi);
     tab_pending = tab_entry(cb0 + 2 * cstride);
   } else {
     // the first NSTAGE - 1 chunks into stages 0 .. NSTAGE - 2
@@ -603,7 +616,8 @@ quant_split_lds_kernel(SplitParams prm) {
       constexpr int SS = decltype(s)::value;
       const int c = cb0 + SS * cstride;
       const ChunkSrc src = chunk_src(c, 0);
-      issue_chunk<D, KNB, VNB, GS, KCH>(ring + SS * SG::BYTES, src.k, src.v, src.m, src.row, c < hi, lane);
+      issue_chunk<D, KNB, VNB, GS, KCH>(ring + SS * SG::BYTES, src.k, src.v, src.m, src.row, c < hi, lane,
+                                        c + kChunk < hi);
     });
   }
 
@@ -792,6 +806,8 @@ quant_split_lds_kernel(SplitParams prm) {
   // Whether this wave has run a chunk: before its first one the accumulators
   // are zero, and a move of the running max needs no rescale.
   bool live = false;
+  float zero_v = 0.0f;  // an opaque zero (see the one-group score fold)
+  asm volatile("" : "+v"(zero_v));
   const float lscale = prm.qk_scale * __builtin_ldexpf(1.0f, 24 - eh);  // per lane (its head)
 
   // In the tail chunk, rows past the sequence hold whatever the cache holds
@@ -828,6 +844,8 @@ quant_split_lds_kernel(SplitParams prm) {
     // order) -- so one V MFMA per product serves both, and the epilogue adds
     // column 8 + c into column c.
     constexpr bool FOLD = PMODE == 1 && PT && HS == 16;
+    // fp16 slots per staged metadata row in this chunk (see StageGeom::MROW)
+    constexpr int MR = TAIL ? SG::MROW : SG::MROW_PAIRS;
     // refill the stage consumed by the previous chunk, NSTAGE-1 chunks ahead
     {
       const int cn = cb + (NSTAGE - 1) * cstride;
@@ -836,7 +854,7 @@ quant_split_lds_kernel(SplitParams prm) {
       const bool valid = !TAIL && cn < hi;
       const ChunkSrc src = chunk_src(cn, page_next);
       issue_chunk<D, KNB, VNB, GS, KCH>(ring + ((SK + NSTAGE - 1) % NSTAGE) * SG::BYTES, src.k, src.v,
-                                   src.m, src.row, valid, lane);
+                                   src.m, src.row, valid, lane, cn + kChunk < hi);
     }
     // Paged: one more vector load in flight, behind the DMA just issued.
     uint32_t tab_new = 0;
@@ -891,18 +909,31 @@ quant_split_lds_kernel(SplitParams prm) {
           // instead of an MFMA (rows past the sequence get -inf below,
           // whatever their z).
           const float qz = qpt.qsum * zsc;
+          if constexpr (MR == 1) {
+            // z * qz as an FMA with a zero the compiler cannot see (it would
+            // fold a literal zero into a separate convert and multiply)
+            // the lane's 4 tokens are consecutive: two fp16 pairs per tensor
+            const int t0 = tile_pt + 4 * j;
+            const u2 zz = *reinterpret_cast<const u2*>(mkz + 2 * t0);
+            const u2 ss = *reinterpret_cast<const u2*>(mks + 2 * t0);
+            x[0] = fma_mix_h<false>(ss[0], c[0][0], fma_mix_h<false>(zz[0], qz, zero_v));
+            x[1] = fma_mix_h<true>(ss[0], c[0][1], fma_mix_h<true>(zz[0], qz, zero_v));
+            x[2] = fma_mix_h<false>(ss[1], c[0][2], fma_mix_h<false>(zz[1], qz, zero_v));
+            x[3] = fma_mix_h<true>(ss[1], c[0][3], fma_mix_h<true>(zz[1], qz, zero_v));
+          } else {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int t = tile_pt + 4 * j + i;
-            const float zv = (float)__builtin_bit_cast(_Float16, (uint16_t)half_at(mkz, t * SG::MROW));
-            const float sv = (float)__builtin_bit_cast(_Float16, (uint16_t)half_at(mks, t * SG::MROW));
-            x[i] = fmaf(sv, c[0][i], zv * qz);
+            for (int i = 0; i < 4; ++i) {
+              const int t = tile_pt + 4 * j + i;
+              const float zv = (float)__builtin_bit_cast(_Float16, (uint16_t)half_at(mkz, t * MR));
+              const float sv = (float)__builtin_bit_cast(_Float16, (uint16_t)half_at(mks, t * MR));
+              x[i] = fmaf(sv, c[0][i], zv * qz);
+            }
           }
         } else {
         // zero-point part: A row = token 16 * (j >> 1) + r, k-slots 8j + g = its zero points
         u4 za;
         {
-          const uint8_t* zrow = mkz + (16 * (j >> 1) + r) * SG::MROW * 2;
+          const uint8_t* zrow = mkz + (16 * (j >> 1) + r) * MR * 2;
           if constexpr (NG == 8) {
             za = *reinterpret_cast<const u4*>(zrow);
           } else if constexpr (NG == 4) {
@@ -927,7 +958,7 @@ quant_split_lds_kernel(SplitParams prm) {
 #pragma unroll
           for (int g = 0; g < NG; ++g) {
             const float sv =
-                (float)__builtin_bit_cast(_Float16, (uint16_t)half_at(mks, t * SG::MROW + g));
+                (float)__builtin_bit_cast(_Float16, (uint16_t)half_at(mks, t * MR + g));
             sc = fmaf(sv, c[g][i], sc);
           }
           x[i] = sc;
@@ -1055,7 +1086,7 @@ quant_split_lds_kernel(SplitParams prm) {
         // zero-point part: A row = token 16a + r, k-slots = its NG zero points
         u2 za;
         {
-          const uint8_t* zr = mkz + (16 * a + r) * SG::MROW * 2;
+          const uint8_t* zr = mkz + (16 * a + r) * MR * 2;
           if constexpr (NG == 8) {
             const u4 z8 = *reinterpret_cast<const u4*>(zr);
             za = (j & 1) ? u2{z8[2], z8[3]} : u2{z8[0], z8[1]};
@@ -1076,7 +1107,7 @@ quant_split_lds_kernel(SplitParams prm) {
           float sc = yz[i] * zsc;
   #pragma unroll
           for (int g = 0; g < NG; ++g) {
-            const float sv = (float)__builtin_bit_cast(_Float16, (uint16_t)half_at(mks, t * SG::MROW + g));
+            const float sv = (float)__builtin_bit_cast(_Float16, (uint16_t)half_at(mks, t * MR + g));
             sc = fmaf(sv, c[g][i], sc);
           }
           x[4 * a + i] = sc;
@@ -1115,8 +1146,15 @@ quant_split_lds_kernel(SplitParams prm) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int t0 = slot_token(j, 2 * q), t1 = slot_token(j, 2 * q + 1);
-        zp[q] = perm(*reinterpret_cast<const uint32_t*>(mvz + zoff + 2 * t1 * SG::MROW),
-                     *reinterpret_cast<const uint32_t*>(mvz + zoff + 2 * t0 * SG::MROW), zsel);
+        if constexpr (MR == 1) {
+          // fp16 pairs staged whole (t1 = t0 + 1): row 0 the zero points, row 1
+          // the ones; rows > 1 read the ones as well, and the output rows they
+          // feed are never read.
+          zp[q] = *reinterpret_cast<const uint32_t*>(mvz + zoff + 2 * t0);
+        } else {
+          zp[q] = perm(*reinterpret_cast<const uint32_t*>(mvz + zoff + 2 * t1 * MR),
+                       *reinterpret_cast<const uint32_t*>(mvz + zoff + 2 * t0 * MR), zsel);
+        }
         if constexpr (TAIL) zp[q] &= tail_pair_mask(cb + t0, cb + t1);
       }
       oz = mfma_k32(u4{zp[0], zp[1], zp[2], zp[3]}, pb, oz);
@@ -1132,9 +1170,13 @@ quant_split_lds_kernel(SplitParams prm) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int t0 = slot_token(j, 2 * q), t1 = slot_token(j, 2 * q + 1);
-        const uint32_t d0 = *reinterpret_cast<const uint32_t*>(mvs + 2 * t0 * SG::MROW + soff[v]);
-        const uint32_t d1 = *reinterpret_cast<const uint32_t*>(mvs + 2 * t1 * SG::MROW + soff[v]);
-        sp[q] = perm(d1, d0, ssel[v]);
+        if constexpr (MR == 1) {
+          sp[q] = *reinterpret_cast<const uint32_t*>(mvs + 2 * t0);  // the pair (t0, t1 = t0 + 1)
+        } else {
+          const uint32_t d0 = *reinterpret_cast<const uint32_t*>(mvs + 2 * t0 * MR + soff[v]);
+          const uint32_t d1 = *reinterpret_cast<const uint32_t*>(mvs + 2 * t1 * MR + soff[v]);
+          sp[q] = perm(d1, d0, ssel[v]);
+        }
         if constexpr (TAIL) sp[q] &= tail_pair_mask(cb + t0, cb + t1);
       }
       pg[v] = u4{pk_mul(pb[0], sp[0]), pk_mul(pb[1], sp[1]), pk_mul(pb[2], sp[2]), pk_mul(pb[3], sp[3])};
@@ -1435,14 +1477,14 @@ __global__ void __launch_bounds__(NW * 64) read_probe_kernel(SplitParams prm) {
   uint8_t* ring = smem + w * 2 * SG::BYTES;
   const int cstride = kChunk * NW;
   const int cb0 = lo + kChunk * w;
-  issue_chunk<D, KNB, VNB, GS>(ring, rk, rv, rm, cb0, cb0 < hi, lane);
+  issue_chunk<D, KNB, VNB, GS>(ring, rk, rv, rm, cb0, cb0 < hi, lane, cb0 + kChunk < hi);
   float acc = 0.0f;
   int s = 0;
   for (int cb = cb0; cb < hi; cb += cstride) {
     wait_lgkmcnt0();  // the previous read of the stage refilled next is done
     asm volatile("" ::: "memory");
     const int cn = cb + cstride;
-    issue_chunk<D, KNB, VNB, GS>(ring + (s ^ 1) * SG::BYTES, rk, rv, rm, cn, cn < hi, lane);
+    issue_chunk<D, KNB, VNB, GS>(ring + (s ^ 1) * SG::BYTES, rk, rv, rm, cn, cn < hi, lane, cn + kChunk < hi);
     wait_vmcnt<NI>();
     asm volatile("" ::: "memory");
     acc += reinterpret_cast<const float*>(ring + s * SG::BYTES)[lane];

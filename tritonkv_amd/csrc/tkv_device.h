@@ -96,6 +96,14 @@ __device__ __forceinline__ void swap_pair(float v, float& a, float& b) {
   a = __builtin_bit_cast(float, opaque(s[0]));
   b = __builtin_bit_cast(float, opaque(s[1]));
 }
+// a_h * b + c in fp32, a_h the fp16 in the low (HI false) or high half of a
+// (the conversion is exact): the compiler selects one v_fma_mix_f32.  Plain
+// code, not inline asm, so the compiler still sees the operands (b is often
+// an MFMA result, whose readers need wait states it inserts).
+template <bool HI>
+__device__ __forceinline__ float fma_mix_h(uint32_t a, float b, float c) {
+  return fmaf((float)__builtin_bit_cast(_Float16, (uint16_t)(HI ? a >> 16 : a)), b, c);
+}
 // max(a, b) as one v_max_f32.  fmaxf first quiets each operand the compiler
 // cannot prove canonical -- every value that comes out of a DPP move or a lane
 // swap -- at one more instruction per operand; the operands here are scores
