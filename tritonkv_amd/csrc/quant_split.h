@@ -175,11 +175,29 @@ __device__ __forceinline__ void issue_chunk(uint8_t* stage, const rsrc_t& rk, co
       dma16<kPolDma>(rv, to_lds(stage + SG::V_OFF + 1024 * q), off);
   }
   // metadata: the chunk's [t][g] rows are contiguous; lane L copies dword L
-  // (NG == 1: the fp16 of token L, into dword L).  Per-channel keys: the K
+  // (NG == 1: below).  Per-channel keys: the K
   // scale and zero tensors hold one row of D fp16 per 32-token block, the
   // chunk's block; its 2D bytes go to the front of the tensor's MB bytes
   // (MB >= 2D for the group sizes that allow them); further instructions read
   // nothing, keeping the instruction count of the vmcnt arithmetic.
+  if constexpr (SG::NG == 1 && !KCH) {
+    // One branch for the four tensors (one instruction each either way: the
+    // vmcnt arithmetic counts instructions).
+    if (pairs) {
+      const uint32_t off = valid ? (uint32_t)(cb + 2 * lane) * 2 : kOut;
+      if (lane < kChunk / 2) {
+#pragma unroll
+        for (int tsr = 0; tsr < 4; ++tsr) dma4<kPolDma>(rm[tsr], to_lds(stage + SG::M_OFF + tsr * SG::MB), off);
+      }
+    } else {
+      const uint32_t off = valid ? (uint32_t)(cb + lane) * 2 : kOut;
+      if (lane < kChunk) {
+#pragma unroll
+        for (int tsr = 0; tsr < 4; ++tsr) dma2<kPolDma>(rm[tsr], to_lds(stage + SG::M_OFF + tsr * SG::MB), off);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int tsr = 0; tsr < 4; ++tsr)
 #pragma unroll
@@ -189,15 +207,6 @@ __device__ __forceinline__ void issue_chunk(uint8_t* stage, const rsrc_t& rk, co
         static_assert(!KCH || SG::MB >= 2 * D, "per-channel key row must fit the K metadata slot");
         const uint32_t off = valid && q == 0 ? (uint32_t)(cb / kChunk) * D * 2 + 4 * lane : kOut;
         if (lane < D / 2) dma4<kPolDma>(rm[tsr], to_lds(dst), off);
-      } else if constexpr (SG::NG == 1) {
-        // One instruction either way (the vmcnt arithmetic counts instructions).
-        if (pairs) {
-          const uint32_t off = valid ? (uint32_t)(cb + 2 * lane) * 2 : kOut;
-          if (lane < kChunk / 2) dma4<kPolDma>(rm[tsr], to_lds(dst), off);
-        } else {
-          const uint32_t off = valid ? (uint32_t)(cb + lane) * 2 : kOut;
-          if (lane < kChunk) dma2<kPolDma>(rm[tsr], to_lds(dst), off);
-        }
       } else {
         const uint32_t off = valid ? (uint32_t)cb * SG::NG * 2 + 4 * (64 * q + lane) : kOut;
         if (SG::MB >= 256 || lane < SG::MB / 4) dma4<kPolDma>(rm[tsr], to_lds(dst), off);
