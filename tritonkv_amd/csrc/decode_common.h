@@ -354,7 +354,10 @@ __device__ __forceinline__ int q_prescale_exp(float amax, int emax) {
   return min(emax, 15 - __builtin_amdgcn_frexp_expf(amax));
 }
 
-template <int D, int KNB, int GS, int EMAX>
+// NAT: the score operands qf in natural dim order (pairs (0,1) (2,3) ...), for
+// the per-channel key path, whose codes are extracted in that order so the
+// chunk's channel scales need no reordering.
+template <int D, int KNB, int GS, int EMAX, bool NAT = false>
 __device__ __forceinline__ void load_q_operands(const SplitParams& prm, int b, int h0, int n, int nh,
                                                 int j, QOperands<D, KNB, GS>& qo) {
   using KL = KLayout<D, KNB, GS>;
@@ -416,12 +419,13 @@ __device__ __forceinline__ void load_q_operands(const SplitParams& prm, int b, i
     const int p = KL::slice_of(m, j);
     const uint32_t pe = (uint32_t)(qo.eh - p * KNB + 15) << 10;
     const uint32_t pre = pe | (pe << 16);
-    // slot order: pairs of dims (0,2) (1,3) (4,6) (5,7) of the step
+    // slot order: pairs of dims (0,2) (1,3) (4,6) (5,7) of the step (NAT:
+    // natural order)
     uint32_t sl[NP];
 #pragma unroll
     for (int e = 0; e < NP; e += 2) {
-      sl[e] = perm(qh[m][e + 1], qh[m][e], 0x05040100u);
-      sl[e + 1] = perm(qh[m][e + 1], qh[m][e], 0x07060302u);
+      sl[e] = NAT ? qh[m][e] : perm(qh[m][e + 1], qh[m][e], 0x05040100u);
+      sl[e + 1] = NAT ? qh[m][e + 1] : perm(qh[m][e + 1], qh[m][e], 0x07060302u);
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {

@@ -727,7 +727,7 @@ quant_split_lds_kernel(SplitParams prm) {
     uint32_t* const qop = reinterpret_cast<uint32_t*>(smem + NW * SM::WAVE + SM::PATCH) + lane;
     constexpr int QN = 4 * NKM;  // dword slots of qn (used by per-channel keys)
     if (w == 0) {
-      load_q_operands<D, KNB, GS, KCH ? 0 : (KL::P - 1) * KNB>(prm, b, h0, n % HS, nh, j, qo);
+      load_q_operands<D, KNB, GS, KCH ? 0 : (KL::P - 1) * KNB, KCH>(prm, b, h0, n % HS, nh, j, qo);
 #pragma unroll
       for (int m = 0; m < NKM; ++m)
 #pragma unroll
@@ -1028,9 +1028,8 @@ quant_split_lds_kernel(SplitParams prm) {
             sn = u4{s2[0], s2[1], 0u, 0u};
             zn = u4{z2[0], z2[1], 0u, 0u};
           }
-          // slot pairs (0,2) (1,3) (4,6) (5,7) of the step's dims
-          const uint32_t ss[4] = {perm(sn[1], sn[0], 0x05040100u), perm(sn[1], sn[0], 0x07060302u),
-                                  perm(sn[3], sn[2], 0x05040100u), perm(sn[3], sn[2], 0x07060302u)};
+          // natural order, as qf and the codes of this path
+          const uint32_t ss[4] = {sn[0], sn[1], sn[2], sn[3]};
           qs[m] = u4{pk_mul(qf[m][0], ss[0]), pk_mul(qf[m][1], ss[1]),
                      KL::CB == 8 ? pk_mul(qf[m][2], ss[2]) : 0u,
                      KL::CB == 8 ? pk_mul(qf[m][3], ss[3]) : 0u};
@@ -1058,11 +1057,11 @@ quant_split_lds_kernel(SplitParams prm) {
   #pragma unroll
           for (int m = 0; m < NKM; ++m) {
             if constexpr (KL::CB == 8) {
-              const u4 a8 = k_extract8(kx[KL::load_of_step(m)], kmask[m]);
+              const u4 a8 = k_extract8_nat(kx[KL::load_of_step(m)], kmask[m]);
               c = mfma_k32(a8, qs[m], c);
               c = mfma_k32(a8, ql[m], c);
             } else {
-              const u2 a4 = k_extract4(kx[KL::load_of_step(m)], kmask[m]);
+              const u2 a4 = k_extract4_nat(kx[KL::load_of_step(m)], kmask[m]);
               c = mfma_k16(a4, u2{qs[m][0], qs[m][1]}, c);
               c = mfma_k16(a4, u2{ql[m][0], ql[m][1]}, c);
             }

@@ -73,6 +73,24 @@ __device__ __forceinline__ u2 k_extract4(uint32_t x, uint32_t mask) {
   a[1] = (x >> 8) & mask;
   return a;
 }
+// The same codes in natural order (fp16 slots hold bytes 0,1 | 2,3 | ...):
+// bytes spread into the low halves by v_perm, one more instruction per
+// source dword than the shift of the slot order (the spread is shared by the
+// slices of a byte).
+__device__ __forceinline__ u4 k_extract8_nat(u2 x, uint32_t mask) {
+  u4 a;
+  a[0] = perm(x[0], x[0], 0x0C010C00u) & mask;
+  a[1] = perm(x[0], x[0], 0x0C030C02u) & mask;
+  a[2] = perm(x[1], x[1], 0x0C010C00u) & mask;
+  a[3] = perm(x[1], x[1], 0x0C030C02u) & mask;
+  return a;
+}
+__device__ __forceinline__ u2 k_extract4_nat(uint32_t x, uint32_t mask) {
+  u2 a;
+  a[0] = perm(x, x, 0x0C010C00u) & mask;
+  a[1] = perm(x, x, 0x0C030C02u) & mask;
+  return a;
+}
 
 template <int D, int NB, int GS>
 struct VLayout {
