@@ -1340,8 +1340,6 @@ quant_split_lds_kernel(SplitParams prm) {
   }
 }
 
-#include "quant_quad.h"
-
 // Ring depth per wave of the quantized split kernel.  8-wave workgroups run
 // one per CU (VGPRs), so their LDS could hold three stages, but a third stage
 // measured slightly slower at the Llama-3-8B shape (208 vs 206 us): one chunk
@@ -1407,14 +1405,6 @@ void launch_quant_pto(const SplitParams& p, dim3 grid, int waves, hipStream_t st
         if (wgs < 8) go(I2{}, std::true_type{});
         else go(I2{}, std::false_type{});
       }
-      return;
-    }
-  }
-  // Quad tiles (quant_quad.h): 2-bit codes, one group per row, GQA groups of
-  // at most 4 heads, contiguous caches.
-  if constexpr (PT && D == 128 && KNB == 2 && VNB == 2 && GS == 128 && HS == 16) {
-    if (!paged && p.G <= 4 && waves >= 8) {
-      quant_quad_kernel<8, ORD><<<grid, dim3(8 * 64), 0, st>>>(p);
       return;
     }
   }
