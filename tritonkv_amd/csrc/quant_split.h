@@ -919,9 +919,9 @@ quant_split_lds_kernel(SplitParams prm) {
           // whatever their z).
           const float qz = qpt.qsum * zsc;
           if constexpr (MR == 1) {
-            // z * qz as an FMA with a zero the compiler cannot see (it would
-            // fold a literal zero into a separate convert and multiply)
-            // the lane's 4 tokens are consecutive: two fp16 pairs per tensor
+            // The lane's 4 tokens are consecutive: two fp16 pairs per tensor.
+            // z * qz is an FMA with a zero the compiler cannot see (a literal
+            // zero would become a separate convert and multiply).
             const int t0 = tile_pt + 4 * j;
             const u2 zz = *reinterpret_cast<const u2*>(mkz + 2 * t0);
             const u2 ss = *reinterpret_cast<const u2*>(mks + 2 * t0);
