@@ -47,7 +47,11 @@ struct StageGeom {
   // MFMA reads them through the same offsets as the zero points (written
   // once per launch; no DMA touches them).
   static constexpr int ONES_OFF = M_OFF + 4 * MB;
-  static constexpr int BYTES = ONES_OFF + MB;
+  // One group per row: MB zero bytes behind the ones, read by the rows past
+  // the ones row of that MFMA when the chunk's pairs are read whole (the
+  // matrix cores then multiply zeros there).
+  static constexpr int ZERO_OFF = ONES_OFF + MB;
+  static constexpr int BYTES = ZERO_OFF + (NG == 1 ? MB : 0);
   static constexpr int NKI = (KB + 1023) / 1024;  // 16-byte-lane DMA instructions for K
   static constexpr int NVI = (VB + 1023) / 1024;
   static constexpr int NMI = (MB + 255) / 256;    // dword-lane DMA instructions per tensor
@@ -600,8 +604,10 @@ quant_split_lds_kernel(SplitParams prm) {
   uint8_t* ring = smem + w * SM::WAVE;
 #pragma unroll
   for (int s = 0; s < NSTAGE; ++s)
-    for (int i = lane; i < SG::MB / 4; i += 64)
+    for (int i = lane; i < SG::MB / 4; i += 64) {
       reinterpret_cast<uint32_t*>(ring + s * SG::BYTES + SG::ONES_OFF)[i] = 0x3C003C00u;
+      if constexpr (NG == 1) reinterpret_cast<uint32_t*>(ring + s * SG::BYTES + SG::ZERO_OFF)[i] = 0u;
+    }
 
   // Chunk k of this wave starts at token lo + 32 * (w + NW * k).
   const int cb0 = lo + kChunk * w;
@@ -662,6 +668,12 @@ quant_split_lds_kernel(SplitParams prm) {
   for (int u = 0; u < QP::NU; ++u)
     koffp[u] = SG::K_OFF + SG::template pos_of<KL::DP>(16 * (j >> 1) + r, u) * 16 + 8 * (j & 1);
   const int tile_pt = 16 * (r >> 3);  // paired tiles: the tile of this lane's scores
+  // Paired tiles: columns of padding heads (head >= nh; 8 head slots per tile
+  // at 16 head columns) carry p = 0 into the PV products, so the matrix cores
+  // multiply zeros there instead of a padding head's probabilities of 1
+  // (less switching under the power cap: 2-bit gs128 2% faster on one box,
+  // 0.5% on another).
+  const uint32_t pcol = ((r & ((HS < 8 ? HS : 8) - 1)) < nh) ? 0xFFFFFFFFu : 0u;
   // V operand of slot i, window wi: token slot_token(j, i), dword dword_offset(wi, r).
   uint32_t voff[VL::NWIN];
 #pragma unroll
@@ -685,8 +697,8 @@ quant_split_lds_kernel(SplitParams prm) {
   // pairs, read from the stage's ones area through the same offsets), so the
   // same MFMA also accumulates sum_t p_t, the softmax denominator, from the
   // very fp16 probabilities the PV products use; rows r > NG are zero (their
-  // selector yields constant zero bytes).
-  int zoff = r < NG ? 2 * (r & ~1) : SG::MB;
+  // selector yields constant zero bytes; pairs read whole: the zero area).
+  int zoff = r < NG ? 2 * (r & ~1) : (r == NG || NG > 1 ? SG::MB : 2 * SG::MB);
   uint32_t zsel = r < NG ? ((r & 1) ? 0x07060302u : 0x05040100u)
                          : (r == NG ? 0x05040100u : 0x0C0C0C0Cu);
   if constexpr (!PT) {
@@ -998,9 +1010,9 @@ quant_split_lds_kernel(SplitParams prm) {
         const uint32_t o0 = lane_xor8(a0), o1 = lane_xor8(a1);
         return swap ? u4{o0, o1, a0, a1} : u4{a0, a1, o0, o1};
       };
-      pb = tiles(ph[0], ph[1]);
+      pb = tiles(ph[0] & pcol, ph[1] & pcol);
       if constexpr (HILO)
-        pbl = tiles(pack_h2_rem(pf[0], pf[1], ph[0]), pack_h2_rem(pf[2], pf[3], ph[1]));
+        pbl = tiles(pack_h2_rem(pf[0], pf[1], ph[0]) & pcol, pack_h2_rem(pf[2], pf[3], ph[1]) & pcol);
     } else {
       // ---- scores S^T for the two 16-token tiles ---------------------------
       float x[8];
@@ -1156,8 +1168,7 @@ quant_split_lds_kernel(SplitParams prm) {
         const int t0 = slot_token(j, 2 * q), t1 = slot_token(j, 2 * q + 1);
         if constexpr (MR == 1) {
           // fp16 pairs staged whole (t1 = t0 + 1): row 0 the zero points, row 1
-          // the ones; rows > 1 read the ones as well, and the output rows they
-          // feed are never read.
+          // the ones, rows > 1 the zero area.
           zp[q] = *reinterpret_cast<const uint32_t*>(mvz + zoff + 2 * t0);
         } else {
           zp[q] = perm(*reinterpret_cast<const uint32_t*>(mvz + zoff + 2 * t1 * MR),
