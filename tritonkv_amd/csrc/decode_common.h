@@ -122,13 +122,16 @@ struct ChunkProbs {
 // rounding.  (A lagging reference -- a rescale only when the max rises by
 // more than a few units -- rounds that p: 5.6e-3 max-abs instead of 6.6e-5
 // on a dominant-token head of 2-bit values.)
-template <bool TRACK_L = true>
+// BIAS: the logits are x * lscale + bl, bl the lane's (head's) chunk-wide
+// offset, folded into the max and the exponent instead of an add per score.
+template <bool TRACK_L = true, bool BIAS = false>
 __device__ __forceinline__ bool softmax_chunk(const float (&x)[8], float lscale, float& m,
-                                              float& l, float& alpha, ChunkProbs& out) {
+                                              float& l, float& alpha, ChunkProbs& out,
+                                              float bl = 0.0f) {
   float lm = x[0];
 #pragma unroll
   for (int i = 1; i < 8; ++i) lm = fmaxf(lm, x[i]);
-  lm *= lscale;
+  lm = BIAS ? fmaf(lm, lscale, bl) : lm * lscale;
   const bool any_moved = __builtin_amdgcn_ballot_w64(lm > m) != 0;
   alpha = 1.0f;
   if (any_moved) {
@@ -138,9 +141,10 @@ __device__ __forceinline__ bool softmax_chunk(const float (&x)[8], float lscale,
     if constexpr (TRACK_L) l *= alpha;
   }
   float sum = 0.0f;
+  const float off = BIAS ? bl - m : -m;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    out.p[i] = __builtin_amdgcn_exp2f(fmaf(x[i], lscale, -m));
+    out.p[i] = __builtin_amdgcn_exp2f(fmaf(x[i], lscale, off));
     if constexpr (TRACK_L) sum += out.p[i];
   }
   if constexpr (TRACK_L) l += sum;

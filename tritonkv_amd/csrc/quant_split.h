@@ -768,6 +768,38 @@ quant_split_lds_kernel(SplitParams prm) {
   const float zsc = __builtin_ldexpf(1.0f, eh - 24);  // code-dot units per score unit
   const u4* qf = qo.qf;
   const u2 qzb = qo.qzb;
+  // Per-channel keys with replicated head columns (HS < 16): column c carries
+  // the hi part of head c % HS's q * s when c & HS is clear, the lo part when
+  // it is set, so one MFMA per step serves both and the score of a column is
+  // its own sum plus that of column c ^ HS (a DPP row rotation by HS).  qlo
+  // is q in the lo columns and zero in the hi ones, so q * s - fp16(qlo * s),
+  // one packed multiply and one packed FMA as before, is fp16(q * s) in a hi
+  // column and the exact remainder q * s - fp16(q * s) in a lo column.
+  constexpr bool KCOL = KCH && HS < 16;
+  u4 qlo[KCOL ? NKM : 1];
+  if constexpr (KCOL) {
+    const bool lo_col = (n & HS) != 0;
+#pragma unroll
+    for (int m = 0; m < NKM; ++m)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) qlo[m][e] = lo_col ? qf[m][e] : 0u;
+  }
+  // ... and when the NR = 16 / HS copies of a head cover the NKM steps
+  // (HS = 4 at D = 128, HS = 8 at D = 64), the zero term sum_d z_d q_d takes
+  // one MFMA for all steps: copy k = n / HS of column n carries q of step k,
+  // A row r the zero points of step r % NR, so lane (j, n), which holds rows
+  // 4j..4j+3, finds its step's partial in accumulator k, and row rotations by
+  // HS, 2 HS, .. add the copies' partials.
+  constexpr int NR = 16 / HS;
+  constexpr bool KZ1 = KCOL && KL::CB == 8 && NKM == NR;
+  u4 qz1 = u4{0u, 0u, 0u, 0u};
+  int zoff1 = 0;
+  if constexpr (KZ1) {
+#pragma unroll
+    for (int m = 0; m < NKM; ++m)
+      if (n / HS == m) qz1 = qo.qn[m];
+    zoff1 = 2 * ((r % NR) * KL::KSTEP + KL::CB * j);
+  }
 
   // ---- fused append ----------------------------------------------------------
   // The token at L - 1 comes from k_new / v_new.  The wave whose chunk holds it
@@ -1016,16 +1048,18 @@ quant_split_lds_kernel(SplitParams prm) {
     } else {
       // ---- scores S^T for the two 16-token tiles ---------------------------
       float x[8];
+      float kbias = 0.0f;  // KCOL: the chunk's zero term in logit units
       if constexpr (KCH) {
         // Per-channel keys: score = sum_d (q_d s_d) c_d + sum_d q_d z_d with
         // the chunk's (block's) scale and zero of channel d.  The B operands
         // become q * s for the chunk, in the slot order of qf, as two fp16
         // parts: hi = fp16(q s) and lo = q s - hi, exact by one fused
         // multiply-add (the error of an fp16 product is an fp16 number), so
-        // the two MFMAs per step see q s to about 22 bits -- a single fp16
-        // product alone put the scores of keys with large channels off by up
-        // to 2^-12 of each term.
-        u4 qs[NKM], ql[NKM];
+        // the products see q s to about 22 bits -- a single fp16 product
+        // alone put the scores of keys with large channels off by up to
+        // 2^-12 of each term.  Two MFMAs per step, or one with the parts in
+        // separate head columns (KCOL).
+        u4 qs[NKM], ql[KCOL ? 1 : NKM];
         f4 cz = f4{0.f, 0.f, 0.f, 0.f};  // the zero term, in every token row of head n
 #pragma unroll
         for (int m = 0; m < NKM; ++m) {
@@ -1042,20 +1076,41 @@ quant_split_lds_kernel(SplitParams prm) {
           }
           // natural order, as qf and the codes of this path
           const uint32_t ss[4] = {sn[0], sn[1], sn[2], sn[3]};
-          qs[m] = u4{pk_mul(qf[m][0], ss[0]), pk_mul(qf[m][1], ss[1]),
-                     KL::CB == 8 ? pk_mul(qf[m][2], ss[2]) : 0u,
-                     KL::CB == 8 ? pk_mul(qf[m][3], ss[3]) : 0u};
-          ql[m] = u4{pk_fma_rem(qf[m][0], ss[0], qs[m][0]), pk_fma_rem(qf[m][1], ss[1], qs[m][1]),
-                     KL::CB == 8 ? pk_fma_rem(qf[m][2], ss[2], qs[m][2]) : 0u,
-                     KL::CB == 8 ? pk_fma_rem(qf[m][3], ss[3], qs[m][3]) : 0u};
+          if constexpr (KCOL) {
+            // hi columns: fp16(q s) - 0; lo columns: q s - fp16(q s), exact
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              qs[m][e] = (KL::CB == 8 || e < 2) ? pk_fma_rem(qf[m][e], ss[e], pk_mul(qlo[m][e], ss[e])) : 0u;
+          } else {
+            qs[m] = u4{pk_mul(qf[m][0], ss[0]), pk_mul(qf[m][1], ss[1]),
+                       KL::CB == 8 ? pk_mul(qf[m][2], ss[2]) : 0u,
+                       KL::CB == 8 ? pk_mul(qf[m][3], ss[3]) : 0u};
+            ql[m] = u4{pk_fma_rem(qf[m][0], ss[0], qs[m][0]), pk_fma_rem(qf[m][1], ss[1], qs[m][1]),
+                       KL::CB == 8 ? pk_fma_rem(qf[m][2], ss[2], qs[m][2]) : 0u,
+                       KL::CB == 8 ? pk_fma_rem(qf[m][3], ss[3], qs[m][3]) : 0u};
+          }
           // zero term by MFMA: every A row is the step's zero points (natural
           // order), B is q of the same dims (natural order, unscaled), so each
           // output row holds sum_d z_d q_{n,d} over the step: exact fp16
           // products, fp32 sums, no cross-lane reduction.
-          if constexpr (KL::CB == 8) cz = mfma_k32(zn, qo.qn[m], cz);
-          else cz = mfma_k16(u2{zn[0], zn[1]}, u2{qo.qn[m][0], qo.qn[m][1]}, cz);
+          if constexpr (KZ1) {
+          } else if constexpr (KL::CB == 8) {
+            cz = mfma_k32(zn, qo.qn[m], cz);
+          } else {
+            cz = mfma_k16(u2{zn[0], zn[1]}, u2{qo.qn[m][0], qo.qn[m][1]}, cz);
+          }
         }
-        const float bias24 = cz[0] * zsc;
+        float zt = cz[0];
+        if constexpr (KZ1) {
+          cz = mfma_k32(*reinterpret_cast<const u4*>(mkz + zoff1), qz1, cz);
+          const int k = n / HS;
+          zt = k == 0 ? cz[0] : k == 1 ? cz[1] : k == 2 ? cz[2] : cz[3];
+          if constexpr (NR == 4) zt += lane_ror<4>(zt);
+          zt += lane_ror<8>(zt);
+        }
+        // KCOL: the zero term enters the softmax as a logit offset
+        const float bias24 = zt * (KCOL ? zsc * lscale : zsc);
+        if constexpr (KCOL) kbias = bias24;
   #pragma unroll
         for (int a = 0; a < 2; ++a) {
           f4 c = f4{0.f, 0.f, 0.f, 0.f};
@@ -1071,15 +1126,16 @@ quant_split_lds_kernel(SplitParams prm) {
             if constexpr (KL::CB == 8) {
               const u4 a8 = k_extract8_nat(kx[KL::load_of_step(m)], kmask[m]);
               c = mfma_k32(a8, qs[m], c);
-              c = mfma_k32(a8, ql[m], c);
+              if constexpr (!KCOL) c = mfma_k32(a8, ql[m], c);
             } else {
               const u2 a4 = k_extract4_nat(kx[KL::load_of_step(m)], kmask[m]);
               c = mfma_k16(a4, u2{qs[m][0], qs[m][1]}, c);
-              c = mfma_k16(a4, u2{ql[m][0], ql[m][1]}, c);
+              if constexpr (!KCOL) c = mfma_k16(a4, u2{ql[m][0], ql[m][1]}, c);
             }
           }
   #pragma unroll
-          for (int i = 0; i < 4; ++i) x[4 * a + i] = c[i] + bias24;
+          for (int i = 0; i < 4; ++i)
+            x[4 * a + i] = KCOL ? c[i] + lane_ror<HS < 16 ? HS : 8>(c[i]) : c[i] + bias24;
         }
       } else {
   #pragma unroll
@@ -1145,7 +1201,7 @@ quant_split_lds_kernel(SplitParams prm) {
       // ---- online softmax ---------------------------------------------------
       float alpha;
       ChunkProbs pr;
-      if (softmax_chunk<false>(x, lscale, m_run, l_run, alpha, pr) && live) {
+      if (softmax_chunk<false, KCOL>(x, lscale, m_run, l_run, alpha, pr, kbias) && live) {
   #pragma unroll
         for (int mv = 0; mv < NVM; ++mv)
           if (v_mfma_in_part<VL, VS>(mv, PART)) accv[mv] *= alpha;

@@ -170,6 +170,13 @@ __device__ __forceinline__ uint32_t lane_xor8(uint32_t v) {
 __device__ __forceinline__ float lane_xor8(float v) {
   return __builtin_bit_cast(float, lane_xor8(__builtin_bit_cast(uint32_t, v)));
 }
+// The value of lane (i - R) mod 16 of the lane's row of 16 (DPP row_ror:R).
+template <int R>
+__device__ __forceinline__ float lane_ror(float v) {
+  static_assert(R > 0 && R < 16, "row rotation by 1..15");
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x120 + R, 0xF,
+                                                             0xF, true));
+}
 
 __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
   h2 v = {(_Float16)lo, (_Float16)hi};
