@@ -1103,8 +1103,12 @@ quant_split_lds_kernel(SplitParams prm) {
         float zt = cz[0];
         if constexpr (KZ1) {
           cz = mfma_k32(*reinterpret_cast<const u4*>(mkz + zoff1), qz1, cz);
+          // accumulator k = n / HS by selects (a chain of equality tests
+          // became divergent branches)
           const int k = n / HS;
-          zt = k == 0 ? cz[0] : k == 1 ? cz[1] : k == 2 ? cz[2] : cz[3];
+          const float t0 = (k & 1) ? cz[1] : cz[0];
+          const float t1 = (k & 1) ? cz[3] : cz[2];
+          zt = (NR == 4 && (k & 2)) ? t1 : t0;
           if constexpr (NR == 4) zt += lane_ror<4>(zt);
           zt += lane_ror<8>(zt);
         }
