@@ -2,7 +2,8 @@
 
 * Llama-3-8B attention (B=32, HQ=32, HKV=8, D=128, ctx 32768) on its own
   inputs -- N(0,1) K/V with 4 x8 outlier channels per KV head -- for all four
-  (nbits, group_size) pairs the benchmark times.
+  (nbits, group_size) pairs the benchmark times, and for its per-channel key
+  steps (2- and 4-bit, 16-token fp16 window).
 * The 70B-style ragged batch (B=64, HQ=64, HKV=8, D=128, lengths U[1024,
   131072], K 4-bit / V 2-bit, group 32) with the decode step's one-token
   append fused into the split kernel.
@@ -32,6 +33,7 @@ import pytest
 import torch
 
 from oracle import attention as oatt
+from oracle import channel as och
 from oracle import quant as oq
 from tests.helpers import MAX_ABS_TOL, assert_close_to_reference
 
@@ -156,6 +158,59 @@ def test_llama3_8b_outlier_channels_full_shape(llama_kv, nbits, gs):
             assert_close_to_reference(out[b:b + 1, G * h:G * (h + 1)], ref,
                                       f"llama nbits={nbits} gs={gs} b={b} h={h} {plan}")
     del kq, vq
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("nbits", [2, 4])
+def test_llama3_8b_per_channel_keys_full_shape(llama_kv, nbits):
+    """The per-channel key step the benchmark times (keys per 32-token block and
+    channel, values per token, a 16-token fp16 window) on the same inputs, with
+    the unsplit plan (``equal_lengths``: one workgroup per unit, 12 waves at
+    2-bit) and the ragged plan (split rows + combine): sampled units' key and
+    value codes bitwise equal to the oracle quantizers', and attention within
+    the oracle tolerance of fp32 attention over the oracle's dequantised
+    history and window."""
+    from tritonkv_amd.channel import channel_decode_attention, quantize_keys_per_channel
+    from tritonkv_amd.quantize import quantize_groupwise
+
+    q, k, v, _ = llama_kv
+    B, HQ, HKV, S, D = (LLAMA[x] for x in ("B", "HQ", "HKV", "S", "D"))
+    G, W = HQ // HKV, 16
+    _say(f"llama per-channel keys nbits={nbits}: quantize + decode")
+    g = torch.Generator(device=DEV).manual_seed(77 + nbits)
+    kr = torch.randn(B, HKV, 32, D, device=DEV, generator=g, dtype=torch.float16)
+    vr = torch.randn(B, HKV, 32, D, device=DEV, generator=g, dtype=torch.float16)
+    ck = quantize_keys_per_channel(k, nbits)
+    vq = quantize_groupwise(v, nbits, 32)
+    ql = torch.full((B,), S, dtype=torch.int32, device=DEV)
+    rl = torch.full((B,), W, dtype=torch.int32, device=DEV)
+    got = channel_decode_attention(q, ck, vq, kr, vr, q_lens=ql, res_lens=rl, equal_lengths=True)
+    ragged = channel_decode_attention(q, ck, vq, kr, vr, q_lens=ql, res_lens=rl)
+    torch.cuda.synchronize()
+    assert torch.isfinite(got).all() and torch.isfinite(ragged).all()
+    assert (got - ragged).abs().max().item() <= 2 * MAX_ABS_TOL
+    got_np, rag_np = got.cpu().numpy(), ragged.cpu().numpy()
+    for b, h in LLAMA_UNITS:
+        _say(f"  unit b={b} h={h}")
+        want = och.quantize_keys_per_channel(k[b, h].cpu().numpy(), nbits)
+        packed = ck.packed[b, h].cpu().numpy()
+        scale, zero = ck.scale[b, h].cpu().numpy(), ck.zero[b, h].cpu().numpy()
+        assert np.array_equal(packed, want.packed), f"K codes b={b} h={h}"
+        assert np.array_equal(scale.view(np.uint16), want.scale.view(np.uint16)), f"K scale b={b} h={h}"
+        assert np.array_equal(zero.view(np.uint16), want.zero.view(np.uint16)), f"K zero b={b} h={h}"
+        vw = _assert_unit_codes(vq, v[b, h].cpu().numpy(), b, h, S, f"V b={b} h={h}")
+        ckn = och.ChannelKeysNP(packed[None, None], scale[None, None], zero[None, None], nbits,
+                                32, D)
+        vqn = oq.QuantNP(vw.packed[None, None], vw.scale[None, None], vw.zero[None, None], nbits,
+                         32, D)
+        kk, vv, _ = och.history(ckn, vqn, kr[b, h].cpu().numpy()[None, None],
+                                vr[b, h].cpu().numpy()[None, None], [S], [W])
+        qn = q[b:b + 1, G * h:G * (h + 1)].float().cpu().numpy()
+        ref = oatt.reference_decode_attention(qn, kk, vv)
+        for out, plan in ((got_np, "equal lengths"), (rag_np, "ragged plan")):
+            assert_close_to_reference(out[b:b + 1, G * h:G * (h + 1)], ref,
+                                      f"llama per-channel nbits={nbits} b={b} h={h} {plan}")
+    del ck, vq
     torch.cuda.empty_cache()
 
 
