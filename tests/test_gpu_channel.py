@@ -40,6 +40,16 @@ def test_channel_key_quantizer_matches_oracle_bitwise(D, nbits, dtype):
     k = (torch.randn(2, 3, 96, D, generator=g) * 2).to(dtype)
     k[0, 1, 32:64, 5] = 0.75       # a constant group
     k[1, 0, :, 9] *= 40            # an outlier channel
+    # non-finite input: NaN propagates through the block's min / max (the
+    # canonical NaN zero, scale 1, codes 0), +-Inf as the arithmetic gives
+    k[0, 2, 3, 9] = float("nan")
+    k[1, 1, 70, 11] = float("inf")
+    k[0, 0, 33, 2] = float("-inf")
+    if dtype == torch.float16:
+        k.view(torch.int16)[1, 2, 90, 4] = -512            # 0xFE00: a NaN with the sign bit
+    else:
+        k.view(torch.int32)[1, 2, 90, 4] = -4194304        # 0xFFC00000
+        k[1, 2, 40, 7], k[1, 2, 41, 7] = 1.0e6, -7.0e4     # beyond the fp16 range
     ck = quantize_keys_per_channel(k.to(DEV), nbits)
     ref = och.quantize_keys_per_channel(k.numpy(), nbits)
     assert np.array_equal(ck.packed.cpu().numpy(), ref.packed)

@@ -23,9 +23,10 @@ def _rand(shape, seed, scale=2.0):
     return (g.standard_normal(shape) * scale).astype(np.float16)
 
 
+@pytest.mark.parametrize("f32", [False, True])
 @pytest.mark.parametrize("nbits", [2, 4])
 @pytest.mark.parametrize("D", [64, 128])
-def test_per_channel_equals_per_token_quantizer_on_transposed_blocks(nbits, D):
+def test_per_channel_equals_per_token_quantizer_on_transposed_blocks(nbits, D, f32):
     B, H, S, T = 2, 3, 96, 32
     x = _rand((B, H, S, D), seed=nbits + D)
     x[0, 1, 40:50, 7] = 1.25                                  # a constant stretch
@@ -34,6 +35,9 @@ def test_per_channel_equals_per_token_quantizer_on_transposed_blocks(nbits, D):
     x[0, 2, 70, 11] = np.inf                                  # the per-token quantizer's
     x[1, 0, 33, 2] = -np.inf                                  # golden cases pin
     x.view(np.uint16)[1, 1, 90, 4] = 0xFE00                   # a NaN with the sign bit
+    if f32:                                                   # fp32 input beyond the
+        x = x.astype(np.float32)                              # fp16 range
+        x[1, 0, 40, 7], x[1, 0, 41, 7] = 1.0e6, -7.0e4
     ck = och.quantize_keys_per_channel(x, nbits, T)
     codes = oq.unpack_codes(ck.packed, nbits, D)              # (B, H, S, D)
     assert ck.scale.shape == (B, H, S // T, D) and ck.scale.dtype == np.float16
