@@ -86,7 +86,8 @@ def dequantize_keys_per_channel(ck: ChannelKeysNP) -> np.ndarray:
     *lead, S, D = codes.shape
     nb = S // ck.block
     cg = codes.reshape(*lead, nb, ck.block, D)
-    out = cg * ck.scale.astype(np.float32)[..., None, :] + ck.zero.astype(np.float32)[..., None, :]
+    with np.errstate(invalid="ignore"):  # 0 * inf of an infinite scale is NaN, as intended
+        out = cg * ck.scale.astype(np.float32)[..., None, :] + ck.zero.astype(np.float32)[..., None, :]
     return out.reshape(*lead, S, D).astype(np.float32)
 
 

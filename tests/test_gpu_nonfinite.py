@@ -11,7 +11,7 @@ cache rows must reproduce them bit for bit: the wide and row quantize kernels,
 the append at positions, the paged append, the decode step's fused append and
 the per-channel key quantizer.
 
-Decode over such a cache must be NaN exactly where the fp32
+Decode over such a cache (per-token or per-channel keys) must be NaN exactly where the fp32
 dequantise-then-attend oracle is NaN (a NaN key poisons every head of its KV
 head, a NaN value group the dims of that group), and within the north-star
 tolerance everywhere else.  That includes a split whose every score is NaN,
@@ -26,10 +26,12 @@ import numpy as np
 import pytest
 import torch
 
+from oracle import attention as oatt
 from oracle import channel as och
 from oracle import inputs as oinp
 from oracle import quant as oq
-from tests.helpers import assert_close_to_reference, oracle_attention_on_quant, same_float_bits
+from tests.helpers import (assert_close_to_reference, oracle_attention_on_quant, qt_to_np,
+                           same_float_bits)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -239,6 +241,49 @@ def test_decode_nan_parity_long_rows(kbits, vbits):
     torch.cuda.synchronize()
     ref = oracle_attention_on_quant(q, kq, vq)
     _assert_nan_parity(out, ref, "long rows", expect)
+
+
+@pytest.mark.parametrize("kbits,vbits", [(2, 2), (4, 4)])
+@pytest.mark.parametrize("equal", [True, False])
+def test_channel_decode_is_nan_where_the_oracle_is(kbits, vbits, equal):
+    """Per-channel keys: a NaN key poisons its channel's 32-token block (zero
+    NaN), an infinite one makes the block's scale infinite (0 * inf = NaN), so
+    every head of the unit is NaN; a NaN value group its dims.  Rows of 8704
+    tokens at GQA 4 run the 12-wave head-column kernel (unsplit plan) or split
+    rows and the window combine (ragged plan)."""
+    from tritonkv_amd.channel import channel_decode_attention, quantize_keys_per_channel
+    from tritonkv_amd.quantize import quantize_groupwise
+
+    B, HQ, HKV, S, D, gs, W = 3, 8, 2, 8704, 128, 32, 16
+    G = HQ // HKV
+    print(f"channel decode NaN parity K{kbits}/V{vbits} equal_lengths={equal}", flush=True)
+    q, k, v = oinp.make_random_kv(B, HQ, HKV, S, D, seed=kbits + 31)
+    vd = gs + 3
+    k[0, 0, S // 3, 17] = float("nan")
+    v[0, 1, S // 5, vd] = float("nan")
+    k[1, 0, S - 2, 5] = float("inf")
+    k[1, 1, S // 4:S // 2, 64] = float("nan")
+    expect = np.zeros((B, HQ, D), dtype=bool)
+    expect[0, 0:G] = True
+    expect[0, G:2 * G, gs:2 * gs] = True
+    expect[1, :2 * G] = True
+    g = torch.Generator().manual_seed(kbits)
+    kres = torch.randn(B, HKV, 32, D, generator=g).half()
+    vres = torch.randn(B, HKV, 32, D, generator=g).half()
+    ck = quantize_keys_per_channel(k.to(DEV), kbits)
+    vq = quantize_groupwise(v.to(DEV), vbits, gs)
+    ql = torch.full((B,), S, dtype=torch.int32)
+    rl = torch.full((B,), W, dtype=torch.int32)
+    out = channel_decode_attention(q.to(DEV), ck, vq, kres.to(DEV), vres.to(DEV), q_lens=ql.to(DEV),
+                                   res_lens=rl.to(DEV), equal_lengths=equal)
+    torch.cuda.synchronize()
+    ckn = och.ChannelKeysNP(ck.packed.cpu().numpy(), ck.scale.cpu().numpy(), ck.zero.cpu().numpy(),
+                            kbits, 32, D)
+    kh, vh, lens = och.history(ckn, qt_to_np(vq), kres.numpy(), vres.numpy(), ql.tolist(),
+                               rl.tolist())
+    ref = oatt.reference_grouped(q.float().numpy(), lambda s_, e_: kh[:, :, s_:e_],
+                                 lambda s_, e_: vh[:, :, s_:e_], kh.shape[2], HKV, seq_lens=lens)
+    _assert_nan_parity(out, ref, "channel decode", expect)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
