@@ -116,6 +116,7 @@ CASES = [
     (2, 4, 16, 128, 8, 2),
     (4, 2, 32, 64, 32, 4),
     (2, 2, 16, 64, 4, 1),
+    (2, 4, 32, 128, 24, 2),   # GQA 12: 16 head columns, hi and lo MFMAs per step
 ]
 
 
